@@ -1,0 +1,551 @@
+"""compile -> CompiledModel -> run(x, "mi355x") -> RunOutput: the reference driver's surface on MI355X.
+
+    cm = anvil_mi355x.compile((module, consts))          # reference anvil/driver.py:330-335
+    res = cm.run(x_float, "mi355x")                       # quantize x, run every graph op on the GPU, read back
+    res.output, res.ints["out"], res.cycles               # dequantized output, int values, per-op device us
+    cm.run(xs, "mi355x", batch=True, keep="all")          # leading batch dim (reference interp batch=True)
+
+The reference's CompiledModel.run (anvil/driver.py:305-322) binds inputs, builds a tiny-gpu Job and dispatches it
+by backend string (anvil/runtime/api.py:127-141). Here "mi355x" branches at graph level instead, as the
+reference's Vortex-V backend does (anvil/vortexv/__init__.py:102-123): weights and LUTs are uploaded once per
+compiled model, every value stays in HBM, ops run in graph order on one stream, and only the values `keep` asks
+for come back. Transposes and reshapes are strided views (no kernel) unless a consumer needs a dense layout.
+
+Per batch size a plan is built once and cached: buffers, views and the list of kernel launches with their
+arguments, so a run is a walk over prepared calls.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import ir as g
+from . import quantize as Q
+from . import runtime as rt
+from .layout import Buf, View, contig_strides
+
+BACKENDS = ("mi355x",)
+
+
+@dataclass
+class RunOutput:
+    """Reference anvil/driver.py:56-76. cycles: op sym -> device microseconds (profile=True), else None."""
+    output: np.ndarray
+    outputs: list
+    ints: dict
+    cycles: dict
+    result: dict
+    job: object = None
+    _consts: frozenset = frozenset()
+    _model: object = field(default=None, repr=False)
+
+    def stray_writes(self, *, scratch_ok: bool = True) -> list:
+        """Consts whose device copy no longer equals the uploaded values (the reference's check that a run
+        wrote nothing inside a const, driver.py:66-71). Empty for a correct run."""
+        return [] if self._model is None else self._model.changed_consts()
+
+    @property
+    def total_cycles(self):
+        c = list(self.cycles.values())
+        return None if any(v is None for v in c) else sum(c)
+
+
+def _graph_meta(module):
+    out = {}
+    for op in g.func_of(module).ops:
+        if isinstance(op, g.OutputOp) or not op.results:
+            continue
+        ty = g.qt(op.results[0])
+        out[op.sym_str] = (ty.qscale, tuple(ty.dims), ty.dtype)
+    return out
+
+
+def _resolve_model(model, consts, prove=True):
+    from .models import Built
+    if isinstance(model, Built):
+        return model.module, dict(model.consts)
+    if isinstance(model, tuple) and len(model) == 2 and isinstance(model[0], g.Module):
+        return _checked_graph(model[0], dict(model[1]), prove)
+    if isinstance(model, g.Module):
+        return _checked_graph(model, dict(consts or {}), prove)
+    raise TypeError(f"cannot compile a {type(model).__name__}: expected an anvil graph module, (module, consts) or "
+                    "a built model (the torch capture frontend is not part of this backend)")
+
+
+def _checked_graph(module, consts, prove=True):
+    """Every non-inline const needs values, no unknown consts, and the int32 overflow proof must hold
+    (reference driver.py:119-132)."""
+    need = [op.sym_str for op in g.func_of(module).ops if isinstance(op, g.ConstOp) and op.value is None]
+    missing = [s for s in need if s not in consts]
+    if missing:
+        raise ValueError(f"no values for graph consts {missing}: pass consts= or a (module, consts) pair")
+    unknown = sorted(set(consts) - set(need))
+    if unknown:
+        raise ValueError(f"consts {unknown} name no graph const of the module")
+    if prove:
+        Q.prove_no_overflow(module, consts)
+    return module, consts
+
+
+class _Plan:
+    """Buffers, views and launches of one (batch, keep) configuration."""
+
+    def __init__(self):
+        self.bufs: list[Buf] = []
+        self.views: dict = {}
+        self.steps: list = []          # (label, fn, args)
+
+    def buf(self, nbytes, name=""):
+        b = Buf(nbytes, name)
+        self.bufs.append(b)
+        return b
+
+    def dense(self, dims, dtype, name=""):
+        dims = tuple(int(d) for d in dims)
+        b = self.buf(math.prod(dims) * rt.ITEMSIZE[dtype], name)
+        return View(b, dtype, dims, contig_strides(dims))
+
+
+class CompiledModel:
+    """A graph compiled for the mi355x backend: consts resident on the device, plans per batch size."""
+
+    def __init__(self, module, consts, *, device: int = 0):
+        self.module, self.consts = module, dict(consts)
+        self.func = g.func_of(module)
+        self.ops = [op for op in self.func.ops if not isinstance(op, g.OutputOp)]
+        outs = [op for op in self.func.ops if isinstance(op, g.OutputOp)]
+        if len(outs) != 1:
+            raise ValueError("the graph needs exactly one output op")
+        self.output_values = outs[0].values
+        if not any(not isinstance(op, (g.InputOp, g.ConstOp)) for op in self.ops):
+            raise ValueError("the graph has no operations to compile (its outputs are its inputs)")
+        self.meta = _graph_meta(module)
+        self.in_dtypes = {op.sym_str: g.qt(op.result).dtype for op in self.ops if isinstance(op, g.InputOp)}
+        self.input_ops = [op for op in self.ops if isinstance(op, g.InputOp)]
+        self.users = {}
+        for op in self.func.ops:
+            for v in op.operands:
+                self.users.setdefault(v, []).append(op)
+        self.is_const = set()
+        for op in self.ops:
+            if isinstance(op, g.ConstOp) or (isinstance(op, (g.TransposeOp, g.ReshapeOp)) and op.x in self.is_const):
+                self.is_const.add(op.result)
+        self.phys = self._choose_layouts()
+        self.device_index = device
+        self.dev = None
+        self._const_views = {}
+        self._const_bt = {}
+        self._plans = {}
+
+    # --------------------------------------------------------------------------------------- layout choice
+    def _choose_layouts(self) -> dict:
+        """Physical dim order of matmul results read only through one transpose that keeps the last dim last
+        (the head merge o (H, T, d) -> (T, H, d) -> reshape (T, C)): storing the result in the transposed order
+        makes the transpose and the reshape free views."""
+        phys = {}
+        for op in self.ops:
+            if not isinstance(op, (g.QMatmulOp, g.QLinearOp)):
+                continue
+            us = self.users.get(op.result, [])
+            if len(us) != 1 or not isinstance(us[0], g.TransposeOp):
+                continue
+            p = us[0].perm_list
+            if p[-1] == len(p) - 1 and p != list(range(len(p))):
+                phys[op.result] = p
+        return phys
+
+    # ----------------------------------------------------------------------------------------- device state
+    def _ensure_device(self):
+        if self.dev is not None:
+            return
+        self.dev = rt.device(self.device_index)
+        for op in self.ops:
+            if not isinstance(op, g.ConstOp):
+                continue
+            t = g.qt(op.result)
+            vals = np.asarray(op.value if op.value is not None else self.consts[op.sym_str], dtype=np.int64)
+            vals = vals.reshape(t.dims)
+            mem = self.dev.upload(vals.astype(rt.NP_DTYPE[t.dtype]))
+            b = Buf(mem.nbytes, op.sym_str or "const")
+            b.mem = mem
+            self._const_views[op.result] = View(b, t.dtype, tuple(t.dims), contig_strides(t.dims))
+
+    def changed_consts(self) -> list:
+        bad = []
+        for op in self.ops:
+            if isinstance(op, g.ConstOp) and op.result in self._const_views:
+                v = self._const_views[op.result]
+                want = np.asarray(op.value if op.value is not None else self.consts[op.sym_str], dtype=np.int64)
+                got = v.buf.mem.download(v.dims, rt.NP_DTYPE[v.dtype]).astype(np.int64)
+                if not np.array_equal(got, want.reshape(v.dims)):
+                    bad.append(op.sym_str)
+        return bad
+
+    # ------------------------------------------------------------------------------------------- planning
+    def _plan(self, nb: int) -> _Plan:
+        P = _Plan()
+        dev = self.dev
+        views = P.views
+
+        def step(label, fn, *args):
+            P.steps.append((label, fn, args))
+
+        def lead(v):
+            return () if v in self.is_const else (nb,)
+
+        def dense_copy(src: View, label):
+            return _dense_copy_into(P, step, dev, src, label)
+
+        def dense(v: View, label) -> View:
+            return v if v.is_contiguous() else dense_copy(v, label)
+
+        for op in self.ops:
+            r = op.results[0]
+            t = g.qt(r)
+            label = op.sym_str or op.name.split(".")[-1]
+            if isinstance(op, g.InputOp):
+                views[r] = P.dense((nb, *t.dims), t.dtype, label)
+                continue
+            if isinstance(op, g.ConstOp):
+                views[r] = self._const_views[r]
+                continue
+            if isinstance(op, g.TransposeOp):
+                src = views[op.x]
+                k = 0 if op.x in self.is_const else 1
+                views[r] = src.permute(list(range(k)) + [p + k for p in op.perm_list])
+                continue
+            if isinstance(op, g.ReshapeOp):
+                src = views[op.x]
+                nd = (*lead(op.x), *t.dims)
+                v = src.reshape(nd)
+                if v is None:
+                    v = dense_copy(src, label).reshape(nd)
+                views[r] = v
+                continue
+            out_dims = (*lead(r), *t.dims)
+            if isinstance(op, (g.QMatmulOp, g.QLinearOp)):
+                views[r] = self._plan_matmul(P, op, views, out_dims, label, dense, step)
+                continue
+            out = P.dense(out_dims, t.dtype, label)
+            views[r] = out
+            if isinstance(op, g.RmsNormIntOp):
+                x = dense(views[op.x], label + ".x")
+                lut = self._const_views[op.lut] if op.lut in self._const_views else dense(views[op.lut], label)
+                w = dense(views[op.w], label + ".w")
+                rows = math.prod(x.dims[:-1])
+                step(label, _call_ptrs, dev.rmsnorm_int, [x, g.qt(op.x).dtype, w, lut, lut.size, int(op.M),
+                                                          int(op.s), op.ss_shift_int, op.ss_init_int, rows,
+                                                          x.dims[-1], out])
+            elif isinstance(op, g.SoftmaxLutOp):
+                x = dense(views[op.x], label + ".x")
+                lut = dense(views[op.lut], label + ".lut")
+                t1, t2 = x.dims[-2], x.dims[-1]
+                batch = math.prod(x.dims[:-2])
+                step(label, _call_ptrs, dev.softmax_lut, [x, lut, int(op.one), bool(op.causal), batch, t1, t2, out,
+                                                          t.dtype])
+            elif isinstance(op, g.AddRequantOp):
+                a = dense(views[op.a], label + ".a")
+                b = dense(views[op.b], label + ".b")
+                if op.a in self.is_const:
+                    a = dense_copy(a.prepend(nb), label + ".a")
+                if op.b in self.is_const:
+                    b = dense_copy(b.prepend(nb), label + ".b")
+                step(label, _call_ptrs, dev.add_requant, [a, g.qt(op.a).dtype, b, g.qt(op.b).dtype, int(op.Ma),
+                                                          int(op.Mb), int(op.s), out.size, out, t.dtype])
+            elif isinstance(op, g.LutOp):
+                x = dense(views[op.x], label + ".x")
+                if op.x in self.is_const:
+                    x = dense_copy(x.prepend(nb), label + ".x")
+                step(label, _call_ptrs, dev.lut_i8, [x, dense(views[op.table], label + ".t"), out.size, out])
+            elif isinstance(op, g.LutMulOp):
+                x = dense(views[op.x], label + ".x")
+                y = dense(views[op.y], label + ".y")
+                if op.x in self.is_const:
+                    x = dense_copy(x.prepend(nb), label + ".x")
+                if op.y in self.is_const:
+                    y = dense_copy(y.prepend(nb), label + ".y")
+                step(label, _call_ptrs, dev.lut_mul, [x, y, dense(views[op.table], label + ".t"), int(op.M),
+                                                      int(op.s), out.size, out])
+            else:
+                raise NotImplementedError(op.name)
+        return P
+
+    def _bt_const(self, op):
+        """A const right operand (K, N) stored once transposed (N, K) so its K dim is contiguous."""
+        key = op.b
+        if key not in self._const_bt:
+            c = op.b                              # a const, or a transpose / reshape chain of one: replay on host
+            chain = []
+            while c not in self._const_views:
+                chain.append(c.owner)
+                c = c.owner.x
+            vals = np.asarray(self._host_const(c), dtype=np.int64)
+            for o in reversed(chain):
+                vals = np.transpose(vals, o.perm_list) if isinstance(o, g.TransposeOp) else vals.reshape(
+                    g.qt(o.result).dims)
+            bt = np.ascontiguousarray(np.swapaxes(vals, -1, -2)).astype(np.int8)
+            mem = self.dev.upload(bt)
+            b = Buf(mem.nbytes, f"{op.sym_str}.Bt")
+            b.mem = mem
+            self._const_bt[key] = View(b, "i8", bt.shape, contig_strides(bt.shape))
+        return self._const_bt[key]
+
+    def _host_const(self, value):
+        op = value.owner
+        return op.value if op.value is not None else self.consts[op.sym_str]
+
+    def _plan_matmul(self, P, op, views, out_dims, label, dense, step):
+        t = g.qt(op.result)
+        nb_lead = len(out_dims) - 2
+        M, N = out_dims[-2], out_dims[-1]
+        K = g.qt(op.a).dims[-1]
+        # result storage: dense in the chosen physical order, logical view by permuting back
+        perm = self.phys.get(op.result)
+        if perm is not None:
+            k = 0 if op.result in self.is_const else 1
+            pfull = list(range(k)) + [p + k for p in perm]
+            st = P.dense([out_dims[i] for i in pfull], t.dtype, label)
+            inv = [pfull.index(i) for i in range(len(pfull))]
+            out = st.permute(inv)
+        else:
+            out = P.dense(out_dims, t.dtype, label)
+        # A: (lead..., M, K) with K contiguous
+        a = views[op.a]
+        if op.a in self.is_const and nb_lead:
+            a = a.prepend(out_dims[0]) if len(a.dims) < len(out_dims) else a
+        if a.strides[-1] != 1 and a.dims[-1] != 1:
+            a = dense(a, label + ".a")
+        # Bt: (lead..., N, K) with K contiguous
+        bv = views[op.b]
+        if op.b in self.is_const and len(g.qt(op.b).dims) == 2:
+            bt = self._bt_const(op)
+        else:
+            bt = bv.permute(list(range(len(bv.dims) - 2)) + [len(bv.dims) - 1, len(bv.dims) - 2])
+            if bt.strides[-1] != 1 and bt.dims[-1] != 1:
+                bt = _dense_copy_into(P, step, self.dev, bt, label + ".bt")
+        lut = None
+        if op.lut is not None:
+            lut = views[op.lut]
+        # lead dims: broadcast B over missing leading dims
+        la = list(zip(a.dims[:-2], a.strides[:-2]))
+        lc = list(zip(out.dims[:-2], out.strides[:-2]))
+        lb = list(zip(bt.dims[:-2], bt.strides[:-2]))
+        lb = [(d, 0) for d, _ in lc[:len(lc) - len(lb)]] + lb
+        la = [(d, 0) for d, _ in lc[:len(lc) - len(la)]] + la
+        # fold every lead dim into M when A and C allow it and B does not vary over them
+        if all(s == 0 for _, s in lb):
+            a2 = a.reshape((math.prod(a.dims[:-1]), K)) if len(a.dims) == len(out.dims) else None
+            c2 = out.reshape((math.prod(out.dims[:-1]), N))
+            if a2 is not None and c2 is not None and (a2.strides[-1] == 1 or K == 1):
+                strides = [0, 0, a2.strides[0], 0, 0, bt.strides[-2], 0, 0, c2.strides[0]]
+                step(label, _call_gemm, self.dev, a2, bt, c2, 1, 1, a2.dims[0], N, K, strides, op, lut, t.dtype)
+                return out
+        # merge adjacent lead dims that nest in A, B and C alike, down to at most two batch dims
+        lead = [(d, sa, sb, sc) for (d, sa), (_, sb), (_, sc) in zip(la, lb, lc)]
+        lead = [x for x in lead if x[0] != 1]
+        merged = []
+        for d, sa, sb, sc in lead:
+            if merged:
+                D, SA, SB, SC = merged[-1]
+                if SA == sa * d and SB == sb * d and SC == sc * d:
+                    merged[-1] = (D * d, sa, sb, sc)
+                    continue
+            merged.append((d, sa, sb, sc))
+        if len(merged) > 2:
+            raise NotImplementedError(f"{op.name} {op.sym_str!r}: {len(merged)} batch dims that do not merge")
+        while len(merged) < 2:
+            merged.insert(0, (1, 0, 0, 0))
+        (b0, sa0, sb0, sc0), (b1, sa1, sb1, sc1) = merged
+        strides = [sa0, sa1, a.strides[-2], sb0, sb1, bt.strides[-2], sc0, sc1, out.strides[-2]]
+        step(label, _call_gemm, self.dev, a, bt, out, b0, b1, M, N, K, strides, op, lut, t.dtype)
+        return out
+
+    def plan(self, nb: int) -> _Plan:
+        self._ensure_device()
+        if nb not in self._plans:
+            P = self._plan(nb)
+            total = 0
+            for b in P.bufs:
+                if b.mem is None:
+                    b.mem = self.dev.alloc(b.nbytes)
+                    total += b.nbytes
+            P.footprint = total
+            self._plans[nb] = P
+        return self._plans[nb]
+
+    # ------------------------------------------------------------------------------------ (de)quantization
+    @property
+    def inputs(self) -> list:
+        return [op.sym_str for op in self.input_ops]
+
+    @property
+    def outputs(self) -> list:
+        return [v.owner.sym_str for v in self.output_values]
+
+    def scale(self, sym):
+        return self.meta[sym][0]
+
+    def quantize_input(self, x, sym=None):
+        """Float -> integers at the input's scale, round half to even, saturating (reference driver.py:233-241)."""
+        sym = sym or self.inputs[0]
+        s = self.scale(sym)
+        if s is None:
+            raise ValueError(f"input {sym!r} has no scale: pass integer inputs with quantized=True")
+        lo, hi = {"i8": (-128, 127), "i16": (-(1 << 15), (1 << 15) - 1)}.get(self.meta[sym][2],
+                                                                             (-(1 << 31), (1 << 31) - 1))
+        return np.clip(np.rint(np.asarray(x, dtype=np.float64) / s), lo, hi).astype(np.int64)
+
+    def dequantize(self, sym, ints):
+        s = self.scale(sym)
+        return np.asarray(ints, dtype=np.float64) * (1.0 if s is None else s)
+
+    def _bind_inputs(self, x, quantized, batch):
+        """Reference driver.py:248-280, plus batch=True: every input has one extra leading batch dim."""
+        xs = list(x) if isinstance(x, (list, tuple)) else [x]
+        if len(xs) != len(self.inputs):
+            raise ValueError(f"{len(xs)} inputs for graph inputs {self.inputs}")
+        out, nb = {}, None
+        for sym, v in zip(self.inputs, xs):
+            v = np.asarray(v)
+            shape = tuple(self.meta[sym][1])
+            if batch:
+                if v.ndim != len(shape) + 1 or tuple(v.shape[1:]) != shape:
+                    raise ValueError(f"input {sym!r}: batched shape {v.shape} != (batch, *{shape})")
+                if nb is not None and v.shape[0] != nb:
+                    raise ValueError(f"inputs disagree on the batch size ({nb} vs {v.shape[0]})")
+                nb = v.shape[0]
+            elif v.shape != shape:
+                squeeze = lambda sh: tuple(d for d in sh if d != 1)   # noqa: E731
+                if v.size != math.prod(shape) or (v.ndim > 1 and squeeze(v.shape) != squeeze(shape)):
+                    raise ValueError(f"input {sym!r}: shape {v.shape} != {shape}")
+                v = v.reshape(shape)
+            if quantized:
+                out[sym] = self._check_int_input(sym, v)
+            else:
+                if not np.all(np.isfinite(np.asarray(v, dtype=np.float64))):
+                    raise ValueError(f"input {sym!r} has NaN or infinite values")
+                out[sym] = self.quantize_input(v, sym)
+            if not batch:
+                out[sym] = out[sym][None]
+        return out, (nb if batch else 1)
+
+    def _check_int_input(self, sym, v):
+        if v.dtype.kind not in "iub":
+            raise ValueError(f"input {sym!r}: quantized=True needs integer values, got dtype {v.dtype}")
+        dt = self.in_dtypes.get(sym, "i8")
+        bits = {"i8": 8, "i16": 16, "i32": 32}.get(dt, 32)
+        lo, hi = -(1 << (bits - 1)), (1 << (bits - 1)) - 1
+        v = np.asarray(v, dtype=np.int64)
+        if v.size and (v.min() < lo or v.max() > hi):
+            raise ValueError(f"input {sym!r}: values in [{v.min()}, {v.max()}] outside {dt} [{lo}, {hi}]")
+        return v
+
+    # ----------------------------------------------------------------------------------------------- runs
+    def readable(self, keep="outputs") -> list:
+        """Syms a run with this keep policy returns: graph outputs and inputs, or every non-const sym."""
+        if keep == "outputs":
+            syms = self.inputs + self.outputs
+        elif keep == "all":
+            syms = [op.sym_str for op in self.ops if op.result not in self.is_const]
+        else:
+            raise ValueError(f"keep must be 'outputs' or 'all', not {keep!r}")
+        return [s for s in dict.fromkeys(syms) if s is not None]
+
+    def upload_inputs(self, plan, ints: dict):
+        for op in self.input_ops:
+            v = plan.views[op.result]
+            v.buf.mem.upload(np.ascontiguousarray(ints[op.sym_str]).astype(rt.NP_DTYPE[v.dtype]))
+
+    def launch(self, plan, profile=False):
+        """Enqueue every kernel of the plan on the device stream (asynchronous unless profile)."""
+        times = {}
+        if not profile:
+            for _, fn, args in plan.steps:
+                fn(*args)
+            return times
+        for label, fn, args in plan.steps:
+            self.dev.record(0)
+            fn(*args)
+            self.dev.record(1)
+            times[label] = times.get(label, 0.0) + 1e3 * self.dev.elapsed_ms(0, 1)
+        return times
+
+    def read(self, plan, syms, nb=None, batch=True) -> dict:
+        by_sym = {op.sym_str: op.result for op in self.ops if op.sym_str is not None}
+        cache, out = {}, {}
+        for s in syms:
+            v = plan.views[by_sym[s]]
+            key = id(v.buf)
+            if key not in cache:
+                cache[key] = v.buf.mem.download((v.buf.nbytes // v.itemsize,), rt.NP_DTYPE[v.dtype])
+            a = v.read(cache[key])
+            out[s] = a if batch or by_sym[s] in self.is_const else a[0]
+        return out
+
+    def run(self, x, backend: str = "mi355x", *, quantized=False, keep="outputs", batch=False, profile=False,
+            **run_kw) -> RunOutput:
+        """Quantize x (unless quantized=True), run the graph on the GPU, read back (reference driver.py:305-322)."""
+        if backend not in BACKENDS:
+            raise ValueError(f"unknown backend {backend!r}: {', '.join(BACKENDS)}")
+        if run_kw:
+            raise TypeError(f"run() got unexpected keyword argument(s) {sorted(run_kw)}")
+        syms = self.readable(keep)
+        ints_in, nb = self._bind_inputs(x, quantized, batch)
+        plan = self.plan(nb)
+        with self.dev.lock:
+            self.upload_inputs(plan, ints_in)
+            self.dev.record(2)
+            times = self.launch(plan, profile)
+            self.dev.record(3)
+            self.dev.sync()
+            total_ms = self.dev.elapsed_ms(2, 3)
+            ints = self.read(plan, syms, nb, batch)
+        cycles = {label: (times.get(label) if profile else None) for label, _, _ in plan.steps}
+        outs = [self.dequantize(s, ints[s]) for s in self.outputs]
+        consts = frozenset(op.sym_str for op in self.ops if isinstance(op, g.ConstOp))
+        result = {"device_ms": total_ms, "batch": nb, "kernels": len(plan.steps), "footprint": plan.footprint}
+        return RunOutput(outs[0], outs, ints, cycles, result, None, consts, self)
+
+    def summary(self) -> str:
+        plan = self.plan(1)
+        return "\n".join(f"{label:>16} {getattr(fn, '__name__', str(fn))}" for label, fn, _ in plan.steps)
+
+
+# ------------------------------------------------------------------------------------------ launch helpers
+
+def _p(v):
+    return v.ptr if isinstance(v, View) else v
+
+
+def _call_ptrs(fn, args):
+    fn(*[_p(a) for a in args])
+
+
+def _copy_view(dev, src: View, dst: View):
+    dev.copy_strided(src.ptr, dst.ptr, src.itemsize, src.dims, src.strides)
+
+
+def _dense_copy_into(P, step, dev, src: View, label):
+    dst = P.dense(src.dims, src.dtype, label + ".dense")
+    step(label + ".copy", _copy_view, dev, src, dst)
+    return dst
+
+
+def _call_gemm(dev, a: View, bt: View, c: View, b0, b1, M, N, K, strides, op, lut, out_dtype):
+    dev.gemm_i8(a.ptr, bt.ptr, c.ptr, b0, b1, M, N, K, strides, int(op.M), int(op.s),
+                None if lut is None else lut.ptr, out_dtype)
+
+
+def compile(model, example_inputs=None, calib_inputs=None, params=None, schedules=None, *, consts=None,
+            device: int = 0, prove: bool = True, **kw) -> CompiledModel:   # noqa: A001  (mirrors anvil.compile)
+    """anvil.compile for the mi355x backend (reference anvil/driver.py:330-335). params / schedules configure the
+    reference's tiny-gpu targets and are ignored here; example_inputs / calib_inputs only apply to torch modules,
+    which this backend does not capture. prove=False skips the static int32 proof for a hand-built graph, as the
+    reference's graph-level Vortex-V compile does (anvil/vortexv/__init__.py:117-123): every kernel still checks
+    each intermediate on the device, so a run that leaves int32 raises OverflowError like the interpreter."""
+    if kw:
+        raise TypeError(f"compile() got unexpected keyword argument(s) {sorted(kw)}")
+    module, cs = _resolve_model(model, consts, prove)
+    return CompiledModel(module, cs, device=device)

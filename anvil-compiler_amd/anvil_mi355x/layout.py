@@ -1,0 +1,113 @@
+"""Strided views over device buffers: how graph values map onto HBM without copies.
+
+A value is a view (buffer, element offset, dims, element strides). transpose permutes strides; reshape re-strides
+when numpy could (contiguous runs split or merged), so the reference's layout ops (anvil/interp/graph.py:76-81)
+cost no kernel unless a consumer needs a dense layout the view does not have.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+ITEMSIZE = {"i8": 1, "i16": 2, "i32": 4}
+
+
+class Buf:
+    """A planned device allocation (bytes); `mem` is the DeviceBuffer once allocated."""
+    __slots__ = ("nbytes", "mem", "name")
+
+    def __init__(self, nbytes: int, name: str = ""):
+        self.nbytes, self.mem, self.name = int(nbytes), None, name
+
+    @property
+    def ptr(self) -> int:
+        return self.mem.ptr
+
+
+def contig_strides(dims) -> tuple:
+    st, acc = [], 1
+    for d in reversed(list(dims)):
+        st.append(acc)
+        acc *= int(d)
+    return tuple(reversed(st))
+
+
+@dataclass
+class View:
+    buf: Buf
+    dtype: str
+    dims: tuple
+    strides: tuple
+    offset: int = 0
+
+    @property
+    def itemsize(self) -> int:
+        return ITEMSIZE[self.dtype]
+
+    @property
+    def size(self) -> int:
+        return math.prod(self.dims)
+
+    @property
+    def ptr(self) -> int:
+        return self.buf.ptr + self.offset * self.itemsize
+
+    def is_contiguous(self) -> bool:
+        return all(s == c for d, s, c in zip(self.dims, self.strides, contig_strides(self.dims)) if d != 1)
+
+    def permute(self, perm) -> "View":
+        return View(self.buf, self.dtype, tuple(self.dims[p] for p in perm), tuple(self.strides[p] for p in perm),
+                    self.offset)
+
+    def reshape(self, newdims):
+        """The same elements as `newdims` in row-major order, or None when that needs a copy."""
+        st = nocopy_strides(self.dims, self.strides, newdims)
+        return None if st is None else View(self.buf, self.dtype, tuple(newdims), st, self.offset)
+
+    def prepend(self, n: int) -> "View":
+        """Broadcast over a new leading dim of size n (stride 0)."""
+        return View(self.buf, self.dtype, (n,) + self.dims, (0,) + self.strides, self.offset)
+
+    def read(self, base: np.ndarray) -> np.ndarray:
+        """This view of `base` (the whole buffer downloaded as self.dtype) as an int64 array."""
+        a = np.lib.stride_tricks.as_strided(base[self.offset:], shape=self.dims,
+                                            strides=tuple(s * self.itemsize for s in self.strides))
+        return a.astype(np.int64)
+
+
+def nocopy_strides(dims, strides, newdims):
+    """Strides that present (dims, strides) as newdims without moving data, or None.
+
+    The old dims are grouped into maximal runs whose strides nest (stride_i == stride_{i+1} dim_{i+1}); each new dim
+    must fall inside one run, whose elements it then walks contiguously at the run's innermost stride."""
+    dims, strides, newdims = list(map(int, dims)), list(map(int, strides)), list(map(int, newdims))
+    if math.prod(dims) != math.prod(newdims):
+        return None
+    runs = []
+    for d, s in zip(dims, strides):
+        if d == 1:
+            continue
+        if runs and runs[-1][1] == s * d:
+            runs[-1] = (runs[-1][0] * d, s)
+        else:
+            runs.append((d, s))
+    out = [0] * len(newdims)
+    idx = [i for i, d in enumerate(newdims) if d != 1]
+    pos = 0
+    for size, base in runs:
+        group, prod = [], 1
+        while prod < size and pos < len(idx):
+            group.append(idx[pos])
+            prod *= newdims[idx[pos]]
+            pos += 1
+        if prod != size:
+            return None
+        acc = base
+        for i in reversed(group):
+            out[i] = acc
+            acc *= newdims[i]
+    if pos != len(idx):
+        return None
+    return tuple(out)

@@ -1,0 +1,220 @@
+"""ctypes binding of libanvil_mi355x.so (the C ABI in include/anvil_mi355x.h) and device-memory handles.
+
+    lib = runtime.library()                   # loads the in-tree .so; raises if it is missing or stale
+    dev = runtime.Device(0)                   # anvil_init: a context with its own stream on device 0
+    buf = dev.alloc(nbytes); buf.upload(arr); buf.download(shape, np.int8)
+    dev.sync()                                # raises OverflowError / ValueError / ZeroDivisionError found on device
+
+Status codes map to the exceptions the reference interpreter raises for the same condition
+(anvil/semantics.py: OverflowError for int32 overflow, ValueError for range / shift errors, ZeroDivisionError for a
+softmax row summing to zero). There is no CPU fallback: without the library every device call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libanvil_mi355x.so"
+
+I8, I16, I32 = 1, 2, 4
+DTYPE_CODE = {"i8": I8, "i16": I16, "i32": I32}
+NP_DTYPE = {"i8": np.int8, "i16": np.int16, "i32": np.int32}
+ITEMSIZE = {"i8": 1, "i16": 2, "i32": 4}
+
+_ERRORS = {1: ValueError, 2: OverflowError, 3: ZeroDivisionError, 4: RuntimeError}
+
+_p, _i, _i64, _i32, _sz, _f64 = C.c_void_p, C.c_int, C.c_int64, C.c_int32, C.c_size_t, C.c_double
+# symbol -> argtypes (restype int for all but anvil_last_error), in include/anvil_mi355x.h order
+SIGNATURES = {
+    "anvil_last_error": None,
+    "anvil_version": [],
+    "anvil_init": [_i, C.POINTER(_p)],
+    "anvil_destroy": [_p],
+    "anvil_sync": [_p],
+    "anvil_alloc": [_p, _sz, C.POINTER(_p)],
+    "anvil_free": [_p, _p],
+    "anvil_upload": [_p, _p, _p, _sz],
+    "anvil_download": [_p, _p, _p, _sz],
+    "anvil_zero": [_p, _p, _sz],
+    "anvil_event_record": [_p, _i],
+    "anvil_event_elapsed": [_p, _i, _i, C.POINTER(C.c_float)],
+    "anvil_gemm_i8": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i],
+    "anvil_rmsnorm_int": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p],
+    "anvil_softmax_lut": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i],
+    "anvil_add_requant": [_p, _p, _i, _p, _i, _i32, _i32, _i, _i64, _p, _i],
+    "anvil_lut_i8": [_p, _p, _p, _i64, _p],
+    "anvil_lut_mul": [_p, _p, _p, _p, _i32, _i, _i64, _p],
+    "anvil_copy_strided": [_p, _p, _p, _i, _i, _p, _p],
+    "anvil_quantize": [_p, _p, _i, _f64, _i64, _p, _i],
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class Library:
+    def __init__(self, path: Path):
+        if not path.exists():
+            raise RuntimeError(f"{path} is missing: build it first (python -m anvil_mi355x.build, or "
+                               "__graft_entry__.build())")
+        self.path = path
+        self.cdll = C.CDLL(str(path))
+        for name, args in SIGNATURES.items():
+            fn = getattr(self.cdll, name)
+            if args is None:
+                fn.restype, fn.argtypes = C.c_char_p, []
+            else:
+                fn.restype, fn.argtypes = C.c_int, args
+        self.last_error = self.cdll.anvil_last_error
+
+    def call(self, name, *args):
+        rc = getattr(self.cdll, name)(*args)
+        if rc:
+            msg = self.last_error().decode(errors="replace")
+            raise _ERRORS.get(rc, RuntimeError)(f"{name}: {msg}")
+        return rc
+
+
+def library() -> Library:
+    """The process-wide handle on the in-tree libanvil_mi355x.so (ANVIL_MI355X_LIB overrides the path)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            _lib = Library(Path(os.environ.get("ANVIL_MI355X_LIB", LIB_PATH)))
+        return _lib
+
+
+def _ptr(x) -> int:
+    return x.ptr if isinstance(x, DeviceBuffer) else int(x)
+
+
+class DeviceBuffer:
+    """A device allocation owned by a Device; freed when collected."""
+
+    def __init__(self, dev: "Device", nbytes: int):
+        self.dev, self.nbytes = dev, int(nbytes)
+        out = C.c_void_p()
+        dev.lib.call("anvil_alloc", dev.ctx, C.c_size_t(max(1, self.nbytes)), C.byref(out))
+        self.ptr = int(out.value)
+
+    def upload(self, arr: np.ndarray, offset: int = 0):
+        arr = np.ascontiguousarray(arr)
+        if offset + arr.nbytes > self.nbytes:
+            raise ValueError(f"upload of {arr.nbytes} bytes at {offset} overruns a {self.nbytes}-byte buffer")
+        self.dev.lib.call("anvil_upload", self.dev.ctx, C.c_void_p(self.ptr + offset), arr.ctypes.data_as(C.c_void_p),
+                          C.c_size_t(arr.nbytes))
+
+    def download(self, shape, dtype, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError(f"download of {out.nbytes} bytes at {offset} overruns a {self.nbytes}-byte buffer")
+        self.dev.lib.call("anvil_download", self.dev.ctx, out.ctypes.data_as(C.c_void_p), C.c_void_p(self.ptr + offset),
+                          C.c_size_t(out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr and self.dev.ctx:
+            self.dev.lib.call("anvil_free", self.dev.ctx, C.c_void_p(self.ptr))
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Device:
+    """One anvil_ctx: a HIP device and the stream every op of this context runs on."""
+
+    def __init__(self, device: int = 0):
+        self.lib = library()
+        self.index = int(device)
+        ctx = C.c_void_p()
+        self.lib.call("anvil_init", self.index, C.byref(ctx))
+        self.ctx = ctx
+        self.lock = threading.Lock()
+
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def upload(self, arr: np.ndarray) -> DeviceBuffer:
+        arr = np.ascontiguousarray(arr)
+        b = DeviceBuffer(self, arr.nbytes)
+        b.upload(arr)
+        return b
+
+    def sync(self):
+        self.lib.call("anvil_sync", self.ctx)
+
+    def zero(self, ptr, nbytes: int):
+        self.lib.call("anvil_zero", self.ctx, C.c_void_p(_ptr(ptr)), C.c_size_t(nbytes))
+
+    def record(self, slot: int):
+        self.lib.call("anvil_event_record", self.ctx, slot)
+
+    def elapsed_ms(self, slot0: int, slot1: int) -> float:
+        ms = C.c_float()
+        self.lib.call("anvil_event_elapsed", self.ctx, slot0, slot1, C.byref(ms))
+        return float(ms.value)
+
+    def close(self):
+        if self.ctx:
+            self.lib.call("anvil_destroy", self.ctx)
+            self.ctx = None
+
+    # ------------------------------------------------------------------------------------------ op calls
+    def gemm_i8(self, A, Bt, Cp, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype):
+        st = (C.c_int64 * 9)(*[int(s) for s in strides])
+        self.lib.call("anvil_gemm_i8", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)), C.c_void_p(_ptr(Cp)),
+                      batch0, batch1, M, N, K, st, int(mult), shift, C.c_void_p(_ptr(lut) if lut is not None else 0),
+                      DTYPE_CODE[out_dtype])
+
+    def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out):
+        self.lib.call("anvil_rmsnorm_int", self.ctx, C.c_void_p(_ptr(x)), DTYPE_CODE[x_dtype], C.c_void_p(_ptr(w)),
+                      C.c_void_p(_ptr(lut)), lut_len, int(mult), shift, ss_shift, int(ss_init), rows, cols,
+                      C.c_void_p(_ptr(out)))
+
+    def softmax_lut(self, x, lut, one, causal, batch, t1, t2, out, out_dtype):
+        self.lib.call("anvil_softmax_lut", self.ctx, C.c_void_p(_ptr(x)), C.c_void_p(_ptr(lut)), int(one),
+                      int(bool(causal)), batch, t1, t2, C.c_void_p(_ptr(out)), DTYPE_CODE[out_dtype])
+
+    def add_requant(self, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype):
+        self.lib.call("anvil_add_requant", self.ctx, C.c_void_p(_ptr(a)), DTYPE_CODE[a_dtype], C.c_void_p(_ptr(b)),
+                      DTYPE_CODE[b_dtype], int(ma), int(mb), shift, n, C.c_void_p(_ptr(out)), DTYPE_CODE[out_dtype])
+
+    def lut_i8(self, x, table, n, out):
+        self.lib.call("anvil_lut_i8", self.ctx, C.c_void_p(_ptr(x)), C.c_void_p(_ptr(table)), n,
+                      C.c_void_p(_ptr(out)))
+
+    def lut_mul(self, x, y, table, mult, shift, n, out):
+        self.lib.call("anvil_lut_mul", self.ctx, C.c_void_p(_ptr(x)), C.c_void_p(_ptr(y)), C.c_void_p(_ptr(table)),
+                      int(mult), shift, n, C.c_void_p(_ptr(out)))
+
+    def copy_strided(self, src, dst, elem_size, dims, src_strides):
+        r = len(dims)
+        d = (C.c_int64 * r)(*[int(v) for v in dims])
+        s = (C.c_int64 * r)(*[int(v) for v in src_strides])
+        self.lib.call("anvil_copy_strided", self.ctx, C.c_void_p(_ptr(src)), C.c_void_p(_ptr(dst)), elem_size, r, d, s)
+
+    def quantize(self, x, x_is_f64, scale, n, out, out_dtype):
+        self.lib.call("anvil_quantize", self.ctx, C.c_void_p(_ptr(x)), int(bool(x_is_f64)), float(scale), n,
+                      C.c_void_p(_ptr(out)), DTYPE_CODE[out_dtype])
+
+
+_devices = {}
+
+
+def device(index: int = 0) -> Device:
+    """The shared Device for a HIP device index (one context per process and device)."""
+    with _lock:
+        d = _devices.get(index)
+    if d is None:
+        d = Device(index)
+        with _lock:
+            d = _devices.setdefault(index, d)
+    return d

@@ -1,0 +1,70 @@
+// Shared host and device helpers of the anvil_mi355x library (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/anvil_mi355x.h"
+
+// Device-side contract flags: a kernel that meets a value the reference's checked int32 semantics reject sets a
+// bit here (a rare, vector-memory atomic); anvil_sync reads and clears them and returns the matching status.
+enum : unsigned {
+  FLAG_OVERFLOW = 1u,   // an intermediate left int32            -> OverflowError
+  FLAG_SHIFT = 2u,      // rmsnorm shift s + k above 31            -> ValueError (round_term)
+  FLAG_ZERODIV = 4u,    // softmax row sum 0                       -> ZeroDivisionError
+  FLAG_RANGE = 8u,      // an operand outside its dtype            -> ValueError
+};
+
+struct anvil_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  unsigned* flags = nullptr;      // device word of FLAG_* bits
+  hipEvent_t events[16] = {};
+  int num_cu = 0;
+};
+
+namespace anvil {
+
+int set_error(int code, const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what);
+int check_ctx(anvil_ctx* ctx);
+
+#define ANVIL_HIP(call)                                        \
+  do {                                                         \
+    hipError_t e_ = (call);                                    \
+    if (e_ != hipSuccess) return ::anvil::hip_fail(e_, #call); \
+  } while (0)
+
+#define ANVIL_LAUNCHED()                                                      \
+  do {                                                                        \
+    hipError_t e_ = hipGetLastError();                                        \
+    if (e_ != hipSuccess) return ::anvil::hip_fail(e_, "kernel launch");      \
+  } while (0)
+
+constexpr long long I32_MIN = -(1ll << 31);
+constexpr long long I32_MAX = (1ll << 31) - 1;
+
+inline int dtype_lo(int dt) { return dt == ANVIL_I8 ? -128 : (dt == ANVIL_I16 ? -32768 : INT32_MIN); }
+inline int dtype_hi(int dt) { return dt == ANVIL_I8 ? 127 : (dt == ANVIL_I16 ? 32767 : INT32_MAX); }
+
+__device__ __forceinline__ void raise_flag(unsigned* flags, unsigned bit) { atomicOr(flags, bit); }
+
+// requant with every step checked against int32 in the reference's order (anvil/semantics.py:146-155):
+// p = acc * M, v = p + 2^(s-1); flag if either leaves int32; r = v >> s (arithmetic), clamped to [lo, hi].
+__device__ __forceinline__ int requant_checked(int acc, int mult, int shift, long long rnd, int lo, int hi,
+                                               unsigned& bad) {
+  long long p = (long long)acc * (long long)mult;
+  long long v = p + rnd;
+  bad |= (p < I32_MIN) | (p > I32_MAX) | (v < I32_MIN) | (v > I32_MAX);
+  long long r = v >> shift;
+  r = r < lo ? lo : r;
+  r = r > hi ? hi : r;
+  return (int)r;
+}
+
+__device__ __forceinline__ long long round_term(int s) { return s ? (1ll << (s - 1)) : 0ll; }
+
+}  // namespace anvil

@@ -1,0 +1,115 @@
+/* anvil_mi355x.h: C ABI of the MI355X (gfx950) backend for Anvil's int8 graph ops.
+ *
+ * One entry point per graph op of the reference interpreter, plus lifecycle, memory and timing calls. Every
+ * signature uses plain pointers, sizes and ints (no torch types), so a ctypes / cffi / cgo binding is a
+ * one-to-one declaration. The reference is Python: these replace the numpy evaluation of each op in
+ * anvil/interp/graph.py:52-91 (through anvil/semantics.py), and the backend dispatch of
+ * anvil/runtime/api.py:127-141 / anvil/driver.py:305-322.
+ *
+ * Conventions
+ *   - Every call returns ANVIL_OK (0) or an error code; anvil_last_error() returns the calling thread's message.
+ *   - Device pointers come from anvil_alloc (or any HIP allocation on the context's device). Op calls are
+ *     asynchronous on the context's stream; argument errors are reported at the call, int32-contract
+ *     violations found on the device (the reference's OverflowError / ValueError / ZeroDivisionError) are
+ *     reported by the next anvil_sync on that context.
+ *   - Element strides are in elements, int64. Tensors are row-major; the last dim of every operand is
+ *     contiguous unless a stride says otherwise.
+ *   - dtypes: ANVIL_I8, ANVIL_I16, ANVIL_I32 (int8_t, int16_t, int32_t elements).
+ *   - A context is used by one host thread at a time; distinct contexts may run concurrently.
+ */
+#ifndef ANVIL_MI355X_H
+#define ANVIL_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum anvil_status {
+  ANVIL_OK = 0,
+  ANVIL_E_VALUE = 1,      /* bad argument or value outside its dtype: Python ValueError            */
+  ANVIL_E_OVERFLOW = 2,   /* an int32 intermediate left int32: Python OverflowError                */
+  ANVIL_E_ZERODIV = 3,    /* a softmax row summed to zero: Python ZeroDivisionError                */
+  ANVIL_E_RUNTIME = 4,    /* HIP runtime failure: Python RuntimeError                              */
+};
+
+enum anvil_dtype { ANVIL_I8 = 1, ANVIL_I16 = 2, ANVIL_I32 = 4 };
+
+typedef struct anvil_ctx anvil_ctx;
+
+/* ------------------------------------------------------------------------------------------ lifecycle */
+const char* anvil_last_error(void);
+int anvil_version(void);
+/* Create a context on HIP device `device` with its own stream (default priority). */
+int anvil_init(int device, anvil_ctx** out);
+int anvil_destroy(anvil_ctx* ctx);
+/* Wait for the context's stream, then report (and clear) any device-side contract violation. */
+int anvil_sync(anvil_ctx* ctx);
+
+/* ------------------------------------------------------------------------------------------- memory */
+int anvil_alloc(anvil_ctx* ctx, size_t bytes, void** dptr);
+int anvil_free(anvil_ctx* ctx, void* dptr);
+/* Host <-> device copies on the context's stream; they complete before the call returns. */
+int anvil_upload(anvil_ctx* ctx, void* dst, const void* src, size_t bytes);
+int anvil_download(anvil_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Zero `bytes` of device memory with a fill kernel (safe inside a captured graph). */
+int anvil_zero(anvil_ctx* ctx, void* dst, size_t bytes);
+
+/* -------------------------------------------------------------------------------------------- timing */
+/* Events on the context's stream: record two, then read the elapsed milliseconds between them. */
+int anvil_event_record(anvil_ctx* ctx, int slot);
+int anvil_event_elapsed(anvil_ctx* ctx, int slot0, int slot1, float* ms);
+
+/* ------------------------------------------------------------------------------------------------ ops */
+
+/* qmatmul / qlinear (reference anvil/semantics.py:95-103 via anvil/interp/graph.py:62-64):
+ *   C[b0][b1][m][n] = epilogue( sum_k A[b0][b1][m][k] * Bt[b0][b1][n][k] )
+ *   epilogue: r = clamp_out((acc * mult + 2^(shift-1)) >> shift), then lut[r + 128] when lut != NULL.
+ * A and Bt are int8 with their K dim contiguous (Bt is the right operand transposed: a (K, N) weight is
+ * stored (N, K) once at upload; a head-batched kT operand is the K-contiguous rows of k). strides holds
+ *   {sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc}  (batch-0, batch-1 and row strides of A, Bt, C).
+ * out_dtype ANVIL_I8 or ANVIL_I16 (no LUT with I16). mult may be negative; shift in [0, 31]. */
+int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
+                  int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype);
+
+/* rmsnorm_int over rows of `cols` elements (reference anvil/semantics.py:158-182, golden.rmsnorm_int):
+ *   ss = ss_init + sum_j ((x_j^2 + 2^(ss_shift-1)) >> ss_shift); (i, k) = rsqrt_index(ss, lut_len);
+ *   out_j = clamp_i8((x_j * w_j * lut[i] * mult + 2^(shift+k-1)) >> (shift + k)).
+ * x is ANVIL_I8 or ANVIL_I16, contiguous rows; w int8[cols]; lut int32[lut_len]; out int8. */
+int anvil_rmsnorm_int(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* w, const int32_t* lut, int lut_len,
+                      int32_t mult, int shift, int ss_shift, int32_t ss_init, int64_t rows, int cols, int8_t* out);
+
+/* softmax_lut over the last axis of (batch, t1, t2) (reference anvil/lower/graph_to_tensor.py:352-398,
+ * golden.softmax_lut): kept_j = (j <= i) if causal else 1; m = max(-128, max kept x);
+ * e_j = lut[x_j - m + 255] (kept) else 0; S = sum e; p_j = (e_j * one + S / 2) / S.
+ * x int8 contiguous; lut int32[256]; out ANVIL_I8 (one <= 127) or ANVIL_I32. */
+int anvil_softmax_lut(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int32_t one, int causal, int64_t batch,
+                      int t1, int t2, void* out, int out_dtype);
+
+/* add_requant (reference anvil/semantics.py:106-115, golden.residual_add):
+ *   out = clamp_out((a * ma + b * mb + 2^(shift-1)) >> shift), a and b ANVIL_I8 or ANVIL_I16, n elements. */
+int anvil_add_requant(anvil_ctx* ctx, const void* a, int a_dtype, const void* b, int b_dtype, int32_t ma, int32_t mb,
+                      int shift, int64_t n, void* out, int out_dtype);
+
+/* lut (reference anvil/semantics.py:87-92): out = table[x + 128], int8, n elements. */
+int anvil_lut_i8(anvil_ctx* ctx, const int8_t* x, const int8_t* table, int64_t n, int8_t* out);
+
+/* lut_mul (golden.swiglu_lut via anvil/interp/graph.py:67-68): out = requant(table[x + 128] * y, mult, shift). */
+int anvil_lut_mul(anvil_ctx* ctx, const int8_t* x, const int8_t* y, const int8_t* table, int32_t mult, int shift,
+                  int64_t n, int8_t* out);
+
+/* transpose / reshape (reference anvil/interp/graph.py:76-81) when a consumer needs a view laid out densely:
+ * dst (contiguous, dims[0..rank)) = src viewed with element strides src_strides. elem_size 1, 2 or 4; rank <= 6. */
+int anvil_copy_strided(anvil_ctx* ctx, const void* src, void* dst, int elem_size, int rank, const int64_t* dims,
+                       const int64_t* src_strides);
+
+/* CompiledModel.quantize_input (reference anvil/driver.py:233-241): out = clamp_out(rint(x / scale)), round half
+ * to even, x float32 or float64 (x_is_f64), out ANVIL_I8 or ANVIL_I16. */
+int anvil_quantize(anvil_ctx* ctx, const void* x, int x_is_f64, double scale, int64_t n, void* out, int out_dtype);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ANVIL_MI355X_H */

@@ -1,0 +1,146 @@
+"""A CPU stand-in for anvil_mi355x.runtime.Device, for testing the driver's host logic without a GPU.
+
+Test infrastructure only: it emulates each C-ABI call (same arguments: pointers, sizes, element strides) over a
+host byte heap, computing with oracle.semantics, so the planner's buffers, views, strides and batch folding are
+checked on the CPU exactly as the kernels would read them. The product never uses it.
+"""
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+
+from oracle import semantics as sem
+
+NP = {"i8": np.int8, "i16": np.int16, "i32": np.int32}
+SIZE = {"i8": 1, "i16": 2, "i32": 4}
+BASE = 1 << 20
+
+
+class FakeBuffer:
+    def __init__(self, dev, nbytes):
+        self.dev, self.nbytes = dev, int(nbytes)
+        self.ptr = dev._bump(max(1, self.nbytes))
+
+    def upload(self, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        raw = arr.view(np.uint8).reshape(-1)
+        o = self.ptr - BASE + offset
+        self.dev.heap[o:o + raw.size] = raw
+
+    def download(self, shape, dtype, offset=0):
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        o = self.ptr - BASE + offset
+        return self.dev.heap[o:o + n].copy().view(dtype).reshape(shape)
+
+    def free(self):
+        pass
+
+
+class FakeDevice:
+    def __init__(self, heap_bytes=1 << 28):
+        self.heap = np.zeros(heap_bytes, dtype=np.uint8)
+        self.top = 0
+        self.lock = threading.Lock()
+        self.calls = []
+        self.flags = 0
+
+    def _bump(self, n):
+        p = BASE + self.top
+        self.top += (n + 255) // 256 * 256
+        if self.top > self.heap.size:
+            raise MemoryError("fake heap exhausted")
+        return p
+
+    def alloc(self, nbytes):
+        return FakeBuffer(self, nbytes)
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        b = FakeBuffer(self, arr.nbytes)
+        b.upload(arr)
+        return b
+
+    def view(self, ptr, dtype, dims, strides):
+        ptr = ptr.ptr if hasattr(ptr, "ptr") else int(ptr)
+        it = SIZE[dtype]
+        base = self.heap[ptr - BASE:].view(np.uint8)
+        arr = base[: (len(base) // it) * it].view(NP[dtype])
+        return np.lib.stride_tricks.as_strided(arr, shape=tuple(dims), strides=tuple(s * it for s in strides))
+
+    def store(self, ptr, dtype, dims, strides, values):
+        self.view(ptr, dtype, dims, strides)[...] = np.asarray(values).astype(NP[dtype])
+
+    def sync(self):
+        f, self.flags = self.flags, 0
+        if f:
+            raise f
+
+    def record(self, slot):
+        pass
+
+    def elapsed_ms(self, a, b):
+        return 0.0
+
+    def _guard(self, fn):
+        try:
+            return fn()
+        except (OverflowError, ValueError, ZeroDivisionError) as e:
+            self.flags = type(e)
+            return None
+
+    # ---------------------------------------------------------------------------------------------- ops
+    def gemm_i8(self, A, Bt, Cp, b0, b1, M, N, K, strides, mult, shift, lut, out_dtype):
+        self.calls.append(("gemm", b0, b1, M, N, K, tuple(strides)))
+        sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc = strides
+        a = self.view(A, "i8", (b0, b1, M, K), (sa0, sa1, lda, 1)).astype(np.int64)
+        bt = self.view(Bt, "i8", (b0, b1, N, K), (sb0, sb1, ldb, 1)).astype(np.int64)
+        lt = None if lut is None else self.view(lut, "i8", (256,), (1,)).astype(np.int64)
+        out = self._guard(lambda: sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, out_dtype))
+        if out is not None:
+            self.store(Cp, out_dtype, (b0, b1, M, N), (sc0, sc1, ldc, 1), out)
+
+    def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out):
+        self.calls.append(("rmsnorm", rows, cols))
+        xv = self.view(x, x_dtype, (rows, cols), (cols, 1)).astype(np.int64)
+        wv = self.view(w, "i8", (cols,), (1,)).astype(np.int64)
+        lv = self.view(lut, "i32", (lut_len,), (1,)).astype(np.int64)
+        r = self._guard(lambda: sem.rmsnorm_wide(xv, wv, lv, mult, shift, ss_shift, ss_init, x_dtype))
+        if r is not None:
+            self.store(out, "i8", (rows, cols), (cols, 1), r)
+
+    def softmax_lut(self, x, lut, one, causal, batch, t1, t2, out, out_dtype):
+        self.calls.append(("softmax", batch, t1, t2))
+        xv = self.view(x, "i8", (batch, t1, t2), (t1 * t2, t2, 1)).astype(np.int64)
+        lv = self.view(lut, "i32", (256,), (1,)).astype(np.int64)
+        r = self._guard(lambda: sem.softmax_lut(xv, lv, one, causal))
+        if r is not None:
+            self.store(out, out_dtype, (batch, t1, t2), (t1 * t2, t2, 1), r)
+
+    def add_requant(self, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype):
+        self.calls.append(("add", n))
+        av = self.view(a, a_dtype, (n,), (1,)).astype(np.int64)
+        bv = self.view(b, b_dtype, (n,), (1,)).astype(np.int64)
+        r = self._guard(lambda: sem.add_requant(av, bv, ma, mb, shift, out_dtype))
+        if r is not None:
+            self.store(out, out_dtype, (n,), (1,), r)
+
+    def lut_i8(self, x, table, n, out):
+        self.calls.append(("lut", n))
+        r = sem.lut_i8(self.view(x, "i8", (n,), (1,)).astype(np.int64), self.view(table, "i8", (256,), (1,)))
+        self.store(out, "i8", (n,), (1,), r)
+
+    def lut_mul(self, x, y, table, mult, shift, n, out):
+        self.calls.append(("lut_mul", n))
+        xv = self.view(x, "i8", (n,), (1,)).astype(np.int64)
+        yv = self.view(y, "i8", (n,), (1,)).astype(np.int64)
+        tv = self.view(table, "i8", (256,), (1,)).astype(np.int64)
+        r = self._guard(lambda: sem.swiglu_lut(xv, yv, tv, mult, shift))
+        if r is not None:
+            self.store(out, "i8", (n,), (1,), r)
+
+    def copy_strided(self, src, dst, elem_size, dims, src_strides):
+        self.calls.append(("copy", tuple(dims)))
+        dt = {1: "i8", 2: "i16", 4: "i32"}[elem_size]
+        v = self.view(src, dt, dims, src_strides).copy()
+        self.store(dst, dt, dims, [int(np.prod(dims[i + 1:])) for i in range(len(dims))], v)

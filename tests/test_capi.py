@@ -1,0 +1,50 @@
+"""The C-ABI library: it loads, exports exactly what include/anvil_mi355x.h declares, and reports argument errors
+as the exceptions the reference raises. No compute call is made (this file runs without a GPU)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from anvil_mi355x import runtime as rt
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "anvil_mi355x.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(anvil_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declarations_match_the_binding():
+    assert declared() == sorted(rt.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = rt.library()
+    for name in declared():
+        assert hasattr(lib.cdll, name), name
+    assert lib.cdll.anvil_version() == 1
+
+
+def test_null_context_is_a_value_error():
+    lib = rt.library()
+    with pytest.raises(ValueError, match="null context"):
+        lib.call("anvil_sync", None)
+    with pytest.raises(ValueError, match="null context"):
+        lib.call("anvil_gemm_i8", None, None, None, None, 1, 1, 1, 1, 1, None, 1, 0, None, 1)
+    with pytest.raises(ValueError):
+        lib.call("anvil_init", 0, None)            # null output pointer
+
+
+def test_status_codes_map_to_reference_exceptions():
+    assert rt._ERRORS == {1: ValueError, 2: OverflowError, 3: ZeroDivisionError, 4: RuntimeError}
+
+
+def test_no_gpu_here_is_a_runtime_error():
+    """anvil_init on a machine without a visible gfx950 device fails loudly (no CPU fallback)."""
+    if Path("/dev/kfd").exists():
+        pytest.skip("a GPU device node is present")
+    out = C.c_void_p()
+    with pytest.raises((RuntimeError, ValueError)):
+        rt.library().call("anvil_init", 0, C.byref(out))

@@ -1,0 +1,144 @@
+"""Driver host logic without a GPU: input binding and validation (reference anvil/driver.py:248-280), compile checks
+(driver.py:119-132), backend dispatch (runtime/api.py:141), and the layout planner's views, strides and batch
+folding, executed by a CPU stand-in of the C ABI (tests/fake_device.py) and compared with the oracle."""
+import numpy as np
+import pytest
+
+import anvil_mi355x
+import fake_device
+import helpers
+from anvil_mi355x import layout, models
+from anvil_mi355x import runtime as rt
+from anvil_mi355x.ir import GraphBuilder
+from oracle import interp
+
+
+@pytest.fixture
+def fake(monkeypatch):
+    dev = fake_device.FakeDevice()
+    monkeypatch.setattr(rt, "device", lambda index=0: dev)
+    return dev
+
+
+@pytest.fixture(scope="module")
+def cfg1():
+    return models.config(1)[0]
+
+
+def test_planner_matches_oracle_on_config1(fake, cfg1):
+    cm = anvil_mi355x.compile(cfg1)
+    x = models.eval_inputs(cfg1.spec, 3, 5)
+    res = cm.run(x, "mi355x", batch=True, keep="all")
+    want = interp.run(cfg1.module, {"x": cm.quantize_input(x)}, cfg1.consts, batch=True)
+    for k, v in want.values.items():
+        if k not in cfg1.consts:
+            assert np.array_equal(res.ints[k], v), k
+    kinds = [c[0] for c in fake.calls]
+    assert kinds.count("gemm") == 8 and kinds.count("copy") == 1     # only V's transpose is materialised
+    qkv = [c for c in fake.calls if c[0] == "gemm"][:3]
+    assert all(c[1:4] == (1, 1, 96) for c in qkv)                    # batch and T fold into one M = 3 * 32
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_planner_matches_oracle_on_random_graphs(fake, seed):
+    m, c, x, want = helpers.random_case(seed)
+    res = anvil_mi355x.compile((m, c), prove=False).run([x["x"], x["xk"]], quantized=True, keep="all")
+    for k, v in want.values.items():
+        if k not in c:
+            assert np.array_equal(res.ints[k], v), k
+
+
+def test_unknown_backend(fake, cfg1):
+    cm = anvil_mi355x.compile(cfg1)
+    with pytest.raises(ValueError, match="unknown backend 'isasim'"):
+        cm.run(np.zeros((32, 64)), "isasim")
+
+
+def test_input_binding_errors(fake, cfg1):
+    cm = anvil_mi355x.compile(cfg1)
+    with pytest.raises(ValueError, match="shape"):
+        cm.run(np.zeros((31, 64)))
+    with pytest.raises(ValueError, match="NaN"):
+        cm.run(np.full((32, 64), np.nan))
+    with pytest.raises(ValueError, match="integer"):
+        cm.run(np.zeros((32, 64)), quantized=True)
+    with pytest.raises(ValueError, match="outside i8"):
+        cm.run(np.full((32, 64), 128), quantized=True)
+    with pytest.raises(ValueError, match="inputs for graph inputs"):
+        cm.run([np.zeros((32, 64)), np.zeros((32, 64))])
+    with pytest.raises(ValueError, match="batched shape"):
+        cm.run(np.zeros((32, 64)), batch=True)
+    with pytest.raises(ValueError, match="keep"):
+        cm.run(np.zeros((32, 64)), keep="some")
+    r = cm.run(np.zeros((1, 32, 1, 64)))                                 # extra size-1 dims are accepted
+    assert r.ints["out"].shape == (32, 64)
+    with pytest.raises(TypeError):
+        cm.run(np.zeros((32, 64)), bogus=1)
+
+
+def test_quantize_input_rounds_half_to_even(fake, cfg1):
+    cm = anvil_mi355x.compile(cfg1)
+    s = cm.scale("x")
+    x = np.array([0.5, 1.5, 2.5, -0.5, -1.5, 1e6, -1e6]) * s
+    assert list(cm.quantize_input(x)) == [0, 2, 2, 0, -2, 127, -128]
+
+
+def test_compile_checks():
+    g = GraphBuilder("c")
+    x = g.input("x", [2, 4], scale=0.1)
+    y = g.qlinear("y", x, g.const("w", [4, 4]), 100, 10, scale=0.1)
+    g.output(y)
+    m = g.module()
+    with pytest.raises(ValueError, match="no values"):
+        anvil_mi355x.compile((m, {}))
+    with pytest.raises(ValueError, match="name no graph const"):
+        anvil_mi355x.compile((m, {"w": np.ones((4, 4), int), "zz": np.ones(3, int)}))
+    with pytest.raises(OverflowError):
+        anvil_mi355x.compile(_overflowing())
+    with pytest.raises(TypeError):
+        anvil_mi355x.compile(object())
+    with pytest.raises(TypeError):
+        anvil_mi355x.compile((m, {"w": np.ones((4, 4), int)}), bogus=1)
+
+
+def _overflowing():
+    g = GraphBuilder("o")
+    x = g.input("x", [2, 4], scale=0.1)
+    g.output(g.qlinear("y", x, g.const("w", [4, 4]), 1 << 30, 10, scale=0.1))
+    return g.module(), {"w": np.full((4, 4), 127)}
+
+
+def test_device_overflow_raises_like_the_interpreter(fake):
+    m, c = _overflowing()
+    cm = anvil_mi355x.compile((m, c), prove=False)
+    x = np.full((2, 4), 100)
+    with pytest.raises(OverflowError):
+        interp.run(m, {"x": x}, c)
+    with pytest.raises(OverflowError):
+        cm.run(x, quantized=True)
+
+
+def test_nocopy_strides_agree_with_numpy():
+    rng = np.random.default_rng(5)
+    for _ in range(300):
+        dims = tuple(int(d) for d in rng.integers(1, 5, int(rng.integers(1, 5))))
+        a = np.arange(int(np.prod(dims))).reshape(dims)
+        perm = list(rng.permutation(len(dims)))
+        v = np.transpose(a, perm)
+        st = tuple(s // a.itemsize for s in v.strides)
+        new = list(v.shape)
+        rng.shuffle(new)
+        if len(new) > 1 and rng.random() < 0.5:
+            new = [new[0] * new[1]] + new[2:]
+        got = layout.nocopy_strides(v.shape, st, new)
+        if got is not None:
+            view = np.lib.stride_tricks.as_strided(a, shape=new, strides=[s * a.itemsize for s in got])
+            assert np.array_equal(view, v.reshape(new))
+        if v.flags.c_contiguous:
+            assert got is not None
+
+
+def test_layout_choice_makes_head_merge_free(cfg1):
+    cm = anvil_mi355x.driver.CompiledModel(cfg1.module, cfg1.consts)
+    (val, perm), = [(v, p) for v, p in cm.phys.items()]
+    assert val.owner.sym_str == "o" and perm == [1, 0, 2]

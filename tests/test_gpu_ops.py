@@ -1,0 +1,228 @@
+"""GPU parity per op: each C-ABI entry point against the oracle on the same seeded inputs, bit-exact.
+
+Config 2 (the standalone int8 linear + requant sweep: M in {256, 4096, 16384}, K = N in {768, 3072}, uniform
+int8 in [-127, 127]) runs at its full sizes; the edge cases cover odd shapes (the byte-load path), i16 results,
+LUT epilogues, negative multipliers, head-batched strided operands and the device-side int32 contract flags.
+"""
+import numpy as np
+import pytest
+
+from anvil_mi355x import quantize as Q
+from anvil_mi355x import runtime as rt
+from oracle import semantics as sem
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return rt.device(0)
+
+
+def up(dev, arr, dt):
+    return dev.upload(np.ascontiguousarray(np.asarray(arr)).astype(rt.NP_DTYPE[dt]))
+
+
+def run_gemm(dev, a, w, m, s, lut=None, dtype="i8"):
+    """qlinear on the device: a (M, K) @ w (K, N), w uploaded transposed (N, K)."""
+    M, K = a.shape
+    N = w.shape[1]
+    A, Bt = up(dev, a, "i8"), up(dev, w.T, "i8")
+    Cb = dev.alloc(M * N * rt.ITEMSIZE[dtype])
+    L = None if lut is None else up(dev, lut, "i8")
+    dev.gemm_i8(A, Bt, Cb, 1, 1, M, N, K, [0, 0, K, 0, 0, K, 0, 0, N], m, s, L, dtype)
+    dev.sync()
+    return Cb.download((M, N), rt.NP_DTYPE[dtype]).astype(np.int64)
+
+
+CONFIG2 = [(M, K) for M in (256, 4096, 16384) for K in (768, 3072)]
+
+
+@pytest.mark.parametrize("M,K", CONFIG2)
+def test_gemm_config2_sweep(dev, M, K):
+    rng = np.random.default_rng([2, M, K])
+    a = rng.integers(-127, 128, (M, K))
+    w = rng.integers(-127, 128, (K, K))
+    acc = sem.matmul_i8(a, w, fast=True)
+    (m,), s = Q.fixed_point([127 / (1.5 * int(np.abs(acc).max()))], [128 * int(np.abs(w).sum(axis=0).max())])
+    want = sem.requant(acc, m, s)
+    got = run_gemm(dev, a, w, m, s)
+    assert np.array_equal(got, want), (M, K, int((got != want).sum()))
+    assert 50 < np.abs(want).max() <= 127          # the requant scale keeps the outputs spread, not saturated
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1, 1), (7, 5, 3), (33, 17, 65), (130, 48, 257), (255, 100, 129),
+                                   (64, 16, 64), (200, 1000, 40)])
+@pytest.mark.parametrize("dtype", ["i8", "i16"])
+def test_gemm_odd_shapes(dev, M, K, N, dtype):
+    rng = np.random.default_rng([3, M, K, N])
+    a = rng.integers(-128, 128, (M, K))
+    w = rng.integers(-128, 128, (K, N))
+    m = int(rng.integers(1, 3000)) * (-1 if N % 2 else 1)
+    s = int(rng.integers(8, 20))
+    want = sem.qmatmul(a, w, m, s, dtype=dtype)
+    assert np.array_equal(run_gemm(dev, a, w, m, s, dtype=dtype), want)
+
+
+def test_gemm_lut_epilogue(dev):
+    rng = np.random.default_rng(4)
+    a, w = rng.integers(-128, 128, (300, 96)), rng.integers(-128, 128, (96, 200))
+    lut = rng.integers(-128, 128, 256)
+    want = sem.qmatmul(a, w, 555, 17, lut)
+    assert np.array_equal(run_gemm(dev, a, w, 555, 17, lut), want)
+
+
+@pytest.mark.parametrize("B,H,T,d", [(2, 3, 40, 16), (3, 2, 130, 32), (1, 4, 64, 64)])
+def test_gemm_head_batched_strided(dev, B, H, T, d):
+    """scores = qh @ kT read in place from q, k (B, T, H*d): batch strides (T*C, d), row stride C."""
+    rng = np.random.default_rng([5, B, H, T, d])
+    C = H * d
+    q, k = rng.integers(-128, 128, (B, T, C)), rng.integers(-128, 128, (B, T, C))
+    qh = q.reshape(B, T, H, d).transpose(0, 2, 1, 3)
+    kT = k.reshape(B, T, H, d).transpose(0, 2, 3, 1)
+    want = sem.qmatmul(qh, kT, 700, 14)
+    Q_, K_ = up(dev, q, "i8"), up(dev, k, "i8")
+    out = dev.alloc(B * H * T * T)
+    dev.gemm_i8(Q_, K_, out, B, H, T, T, d, [T * C, d, C, T * C, d, C, H * T * T, T * T, T], 700, 14, None, "i8")
+    dev.sync()
+    assert np.array_equal(out.download((B, H, T, T), np.int8).astype(np.int64), want)
+
+
+def test_gemm_overflow_flag(dev):
+    """acc * M past int32 raises OverflowError, as the reference's checked requant does."""
+    a = np.full((4, 8), -128)
+    w = np.full((8, 16), 127)
+    acc = 128 * 8 * 127
+    m_ok = ((1 << 31) - 1 - (1 << 9)) // acc
+    assert np.array_equal(run_gemm(dev, a, w, m_ok, 10), sem.qmatmul(a, w, m_ok, 10))
+    with pytest.raises(OverflowError):
+        sem.qmatmul(a, w, m_ok + 1, 10)
+    with pytest.raises(OverflowError):
+        run_gemm(dev, a, w, m_ok + 1, 10)
+    assert np.array_equal(run_gemm(dev, a, w, m_ok, 10), sem.qmatmul(a, w, m_ok, 10))   # flags were cleared
+
+
+def _rms(dev, x, xdt, w, lut, m, s, c=0, e=0):
+    rows, d = x.shape
+    out = dev.alloc(rows * d)
+    dev.rmsnorm_int(up(dev, x, xdt), xdt, up(dev, w, "i8"), up(dev, lut, "i32"), len(lut), m, s, c, e, rows, d, out)
+    dev.sync()
+    return out.download((rows, d), np.int8).astype(np.int64)
+
+
+@pytest.mark.parametrize("d", [8, 64, 256, 768, 1000])
+def test_rmsnorm_i8(dev, d):
+    rng = np.random.default_rng([6, d])
+    w = rng.integers(-127, 128, d)
+    lut, s = Q.rmsnorm_lut(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
+    x = np.concatenate([rng.integers(-128, 128, (200, d)), np.full((1, d), -128), np.zeros((1, d), int),
+                        np.full((1, d), 127), np.rint(rng.standard_normal((50, d)) * 3).astype(int)])
+    want = sem.rmsnorm_int(x, w, lut, 1, s)
+    assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s), want)
+
+
+def test_rmsnorm_i16_wide(dev):
+    d = 32
+    rng = np.random.default_rng(8)
+    w = rng.integers(-127, 128, d)
+    lut, s, c, e = Q.rmsnorm_lut_wide(4e-4, 0.01, 0.02, 127, d, 1e-6, 1 << 15)
+    x = np.concatenate([rng.integers(-(1 << 15), 1 << 15, (100, d)), np.full((1, d), -(1 << 15)),
+                        np.full((1, d), (1 << 15) - 1), np.zeros((1, d), int)])
+    want = sem.rmsnorm_wide(x, w, lut, 1, s, c, e, "i16")
+    assert np.array_equal(_rms(dev, x, "i16", w, lut, 1, s, c, e), want)
+
+
+def _softmax(dev, x, lut, one, causal, dtype="i8"):
+    *lead, t1, t2 = x.shape
+    batch = int(np.prod(lead)) if lead else 1
+    out = dev.alloc(x.size * rt.ITEMSIZE[dtype])
+    dev.softmax_lut(up(dev, x, "i8"), up(dev, lut, "i32"), one, causal, batch, t1, t2, out, dtype)
+    dev.sync()
+    return out.download(x.shape, rt.NP_DTYPE[dtype]).astype(np.int64)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(2, 3, 4, 4), (5, 7, 3), (2, 1, 100, 100), (1, 2, 64, 1024), (3, 33, 65)])
+def test_softmax(dev, causal, shape):
+    rng = np.random.default_rng([9, *shape])
+    x = rng.integers(-128, 128, shape)
+    x[..., 0, :] = -128                          # a row of the minimum value
+    lut = Q.exp_lut(0.05, shape[-1])
+    want = sem.softmax_lut(x, lut, 127, causal)
+    assert np.array_equal(_softmax(dev, x, lut, 127, causal), want)
+
+
+def test_softmax_i32_result(dev):
+    rng = np.random.default_rng(10)
+    x = rng.integers(-128, 128, (4, 6, 9))
+    lut = np.round((1 << 14) * np.exp((np.arange(256) - 255) / 24.0)).astype(np.int64)
+    for one in (1, 1000, 4095):
+        want = sem.softmax_lut(x, lut, one, False)
+        assert np.array_equal(_softmax(dev, x, lut, one, False, "i32"), want)
+
+
+DT_PAIRS = [("i8", "i8", "i8"), ("i16", "i8", "i16"), ("i8", "i16", "i16"), ("i16", "i16", "i8"), ("i16", "i16", "i16")]
+
+
+@pytest.mark.parametrize("da,db,do", DT_PAIRS)
+def test_add_requant(dev, da, db, do):
+    rng = np.random.default_rng([11, len(da), len(db), DT_PAIRS.index((da, db, do))])
+    n = 10007
+    lim = {"i8": 128, "i16": 1 << 15}
+    a, b = rng.integers(-lim[da], lim[da], n), rng.integers(-lim[db], lim[db], n)
+    ma, mb, s = (300, 500, 10) if da == db == "i8" else (1 << 14, 1 << 13, 14 + (do == "i8") * 6)
+    want = sem.add_requant(a, b, ma, mb, s, do)
+    out = dev.alloc(n * rt.ITEMSIZE[do])
+    dev.add_requant(up(dev, a, da), da, up(dev, b, db), db, ma, mb, s, n, out, do)
+    dev.sync()
+    assert np.array_equal(out.download((n,), rt.NP_DTYPE[do]).astype(np.int64), want)
+
+
+def test_add_requant_known_answer(dev):
+    """Reference tests/frontend/test_quantize.py:109-112: i16 operands with an i8 result saturate at int8."""
+    a, b = np.array([30000, -30000, 200, -129, 5]), np.zeros(5, int)
+    out = dev.alloc(5)
+    dev.add_requant(up(dev, a, "i16"), "i16", up(dev, b, "i8"), "i8", 1, 1, 0, 5, out, "i8")
+    dev.sync()
+    assert list(out.download((5,), np.int8)) == [127, -128, 127, -128, 5]
+
+
+def test_lut_and_lut_mul(dev):
+    rng = np.random.default_rng(12)
+    n = 70001
+    x, y, t = rng.integers(-128, 128, n), rng.integers(-128, 128, n), rng.integers(-128, 128, 256)
+    out = dev.alloc(n)
+    dev.lut_i8(up(dev, x, "i8"), up(dev, t, "i8"), n, out)
+    dev.sync()
+    assert np.array_equal(out.download((n,), np.int8).astype(np.int64), sem.lut_i8(x, t))
+    dev.lut_mul(up(dev, x, "i8"), up(dev, y, "i8"), up(dev, t, "i8"), 300, 12, n, out)
+    dev.sync()
+    assert np.array_equal(out.download((n,), np.int8).astype(np.int64), sem.swiglu_lut(x, y, t, 300, 12))
+
+
+@pytest.mark.parametrize("dt", ["i8", "i16", "i32"])
+def test_copy_strided(dev, dt):
+    rng = np.random.default_rng(13)
+    src = rng.integers(-100, 100, (3, 4, 5, 6))
+    perm = [2, 0, 3, 1]
+    want = np.transpose(src, perm)
+    st = [int(np.prod(src.shape[i + 1:])) for i in range(4)]
+    out = dev.alloc(src.size * rt.ITEMSIZE[dt])
+    dev.copy_strided(up(dev, src, dt), out, rt.ITEMSIZE[dt], want.shape, [st[p] for p in perm])
+    dev.sync()
+    assert np.array_equal(out.download(want.shape, rt.NP_DTYPE[dt]).astype(np.int64), want)
+
+
+@pytest.mark.parametrize("f64", [False, True])
+def test_quantize_input(dev, f64):
+    """round half to even at float64, saturating (reference anvil/driver.py:233-241)."""
+    rng = np.random.default_rng(14)
+    x = np.concatenate([rng.standard_normal(5000) * 3, [0.5, 1.5, 2.5, -0.5, -2.5, 1e9, -1e9]])
+    x = x.astype(np.float64 if f64 else np.float32)
+    scale = 0.025
+    want = np.clip(np.rint(np.asarray(x, dtype=np.float64) / scale), -128, 127).astype(np.int64)
+    xd = dev.upload(np.ascontiguousarray(x))
+    out = dev.alloc(x.size)
+    dev.quantize(xd, f64, scale, x.size, out, "i8")
+    dev.sync()
+    assert np.array_equal(out.download((x.size,), np.int8).astype(np.int64), want)
