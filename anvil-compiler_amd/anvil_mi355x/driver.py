@@ -96,6 +96,7 @@ class _Plan:
         self.bufs: list[Buf] = []
         self.views: dict = {}
         self.steps: list = []          # (label, fn, args)
+        self.works: list = []          # per step: (kind, algorithmic int ops, algorithmic HBM bytes)
 
     def buf(self, nbytes, name=""):
         b = Buf(nbytes, name)
@@ -191,6 +192,7 @@ class CompiledModel:
 
         def step(label, fn, *args):
             P.steps.append((label, fn, args))
+            P.works.append(_work(fn, args))
 
         def lead(v):
             return () if v in self.is_const else (nb,)
@@ -531,6 +533,35 @@ def _dense_copy_into(P, step, dev, src: View, label):
     dst = P.dense(src.dims, src.dtype, label + ".dense")
     step(label + ".copy", _copy_view, dev, src, dst)
     return dst
+
+
+def _work(fn, args):
+    """(kind, algorithmic int ops, algorithmic HBM bytes) of one launch: every graph operand and result counted
+    once at its dtype (LUTs and weights included), layout views free."""
+    isz = rt.ITEMSIZE
+    if fn is _call_gemm:
+        _, a, bt, c, b0, b1, M, N, K, strides, _, _, dt = args
+        nb = b0 * b1
+        b_batches = nb if (strides[3] or strides[4]) else 1
+        return "gemm", 2 * nb * M * N * K, nb * M * K + b_batches * N * K + nb * M * N * isz[dt]
+    if fn is _copy_view:
+        src = args[1]
+        return "copy", 0, 2 * src.size * src.itemsize
+    f, a = args
+    name = getattr(f, "__name__", "")
+    if name == "rmsnorm_int":
+        rows, cols = a[9], a[10]
+        return "rmsnorm", 0, rows * cols * (isz[a[1]] + 1) + cols + 4 * a[4]
+    if name == "softmax_lut":
+        n = a[4] * a[5] * a[6]
+        return "softmax", 0, n * (1 + isz[a[8]]) + 1024
+    if name == "add_requant":
+        return "add", 0, a[7] * (isz[a[1]] + isz[a[3]] + isz[a[9]])
+    if name == "lut_i8":
+        return "lut", 0, 2 * a[2] + 256
+    if name == "lut_mul":
+        return "lut_mul", 0, 3 * a[5] + 256
+    return name or "other", 0, 0
 
 
 def _call_gemm(dev, a: View, bt: View, c: View, b0, b1, M, N, K, strides, op, lut, out_dtype):

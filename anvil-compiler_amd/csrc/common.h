@@ -18,11 +18,13 @@ enum : unsigned {
   FLAG_RANGE = 8u,      // an operand outside its dtype            -> ValueError
 };
 
+constexpr int EVENT_SLOTS = 512;
+
 struct anvil_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   unsigned* flags = nullptr;      // device word of FLAG_* bits
-  hipEvent_t events[16] = {};
+  hipEvent_t events[EVENT_SLOTS] = {};   // created on first use of a slot
   int num_cu = 0;
 };
 

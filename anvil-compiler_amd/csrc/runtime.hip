@@ -70,7 +70,6 @@ int anvil_init(int device, anvil_ctx** out) {
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&c->flags, 256);
   if (e == hipSuccess) e = hipMemset(c->flags, 0, 256);
-  for (int i = 0; e == hipSuccess && i < 16; ++i) e = hipEventCreate(&c->events[i]);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     anvil_destroy(c);
@@ -151,16 +150,20 @@ int anvil_zero(anvil_ctx* ctx, void* dst, size_t bytes) {
 }
 
 int anvil_event_record(anvil_ctx* ctx, int slot) {
+  if (slot < 0 || slot >= EVENT_SLOTS)
+    return set_error(ANVIL_E_VALUE, "event slot %d outside [0, %d)", slot, EVENT_SLOTS);
   if (int r = check_ctx(ctx)) return r;
-  if (slot < 0 || slot >= 16) return set_error(ANVIL_E_VALUE, "event slot %d outside [0, 16)", slot);
+  if (!ctx->events[slot]) ANVIL_HIP(hipEventCreate(&ctx->events[slot]));
   ANVIL_HIP(hipEventRecord(ctx->events[slot], ctx->stream));
   return ANVIL_OK;
 }
 
 int anvil_event_elapsed(anvil_ctx* ctx, int slot0, int slot1, float* ms) {
-  if (int r = check_ctx(ctx)) return r;
-  if (slot0 < 0 || slot0 >= 16 || slot1 < 0 || slot1 >= 16 || !ms)
+  if (slot0 < 0 || slot0 >= EVENT_SLOTS || slot1 < 0 || slot1 >= EVENT_SLOTS || !ms)
     return set_error(ANVIL_E_VALUE, "anvil_event_elapsed: bad slot or null output");
+  if (int r = check_ctx(ctx)) return r;
+  if (!ctx->events[slot0] || !ctx->events[slot1])
+    return set_error(ANVIL_E_VALUE, "anvil_event_elapsed: slot never recorded");
   ANVIL_HIP(hipEventSynchronize(ctx->events[slot1]));
   ANVIL_HIP(hipEventElapsedTime(ms, ctx->events[slot0], ctx->events[slot1]));
   return ANVIL_OK;
