@@ -112,8 +112,9 @@ class _Plan:
 class CompiledModel:
     """A graph compiled for the mi355x backend: consts resident on the device, plans per batch size."""
 
-    def __init__(self, module, consts, *, device: int = 0):
+    def __init__(self, module, consts, *, device: int = 0, proven: bool = False):
         self.module, self.consts = module, dict(consts)
+        self.proven = bool(proven)        # prove_no_overflow held: kernels may skip their int32 checks
         self.func = g.func_of(module)
         self.ops = [op for op in self.func.ops if not isinstance(op, g.OutputOp)]
         outs = [op for op in self.func.ops if isinstance(op, g.OutputOp)]
@@ -134,6 +135,9 @@ class CompiledModel:
             if isinstance(op, g.ConstOp) or (isinstance(op, (g.TransposeOp, g.ReshapeOp)) and op.x in self.is_const):
                 self.is_const.add(op.result)
         self.phys = self._choose_layouts()
+        self.acc_bounds = {}                     # matmul result -> proven bound on |accumulator|
+        if self.proven:
+            Q.prove_no_overflow(module, self.consts, acc_bounds=self.acc_bounds)
         self.device_index = device
         self.dev = None
         self._const_views = {}
@@ -155,7 +159,55 @@ class CompiledModel:
             p = us[0].perm_list
             if p[-1] == len(p) - 1 and p != list(range(len(p))):
                 phys[op.result] = p
+        for op in self.ops:
+            if isinstance(op, (g.QMatmulOp, g.QLinearOp)):
+                root = self._transposed_producer(op.b, phys)
+                if root is not None:
+                    phys[root] = _swap_last2(len(g.qt(root).dims))
         return phys
+
+    def _const_array(self, v):
+        """The int64 values of a graph const, None for a computed value."""
+        op = v.owner
+        if not isinstance(op, g.ConstOp):
+            return None
+        src = op.value if op.value is not None else self.consts[op.sym_str]
+        return np.asarray(src, dtype=np.int64).reshape(-1)
+
+    def _transposed_producer(self, b, phys):
+        """The matmul result whose transposed storage (last two dims swapped) makes the right operand `b` -- a
+        view chain of transposes / reshapes over that result -- K-contiguous, so no transpose copy is needed
+        (attention's v -> vh read as P.V's right operand). None when b is already K-contiguous, is a const, or
+        the chain does not end at a single-use matmul result."""
+        chain, v = [], b
+        while isinstance(v.owner, (g.TransposeOp, g.ReshapeOp)) and v not in self.is_const:
+            if len(self.users.get(v, [])) != 1:
+                return None
+            chain.append(v.owner)
+            v = v.owner.x
+        root = v
+        if (not isinstance(root.owner, (g.QMatmulOp, g.QLinearOp)) or root in self.is_const or root in phys
+                or len(self.users.get(root, [])) != 1 or not chain):
+            return None
+
+        def view_of(perm):
+            dims = [2] + g.qt(root).dims
+            pf = [0] + [p + 1 for p in perm]
+            st = contig_strides([dims[i] for i in pf])
+            vw = View(None, "i8", tuple([dims[i] for i in pf]), st).permute([pf.index(i) for i in range(len(pf))])
+            for o in reversed(chain):
+                if isinstance(o, g.TransposeOp):
+                    vw = vw.permute([0] + [p + 1 for p in o.perm_list])
+                else:
+                    vw = vw.reshape((2, *g.qt(o.result).dims))
+                    if vw is None:
+                        return None
+            return vw
+
+        n = len(g.qt(root).dims)
+        plain, swapped = view_of(list(range(n))), view_of(_swap_last2(n))
+        k_contig = lambda vw: vw is not None and (vw.strides[-2] == 1 or vw.dims[-2] == 1)   # noqa: E731
+        return root if not k_contig(plain) and k_contig(swapped) else None
 
     # ----------------------------------------------------------------------------------------- device state
     def _ensure_device(self):
@@ -185,7 +237,7 @@ class CompiledModel:
         return bad
 
     # ------------------------------------------------------------------------------------------- planning
-    def _plan(self, nb: int) -> _Plan:
+    def _plan(self, nb: int, keep: str) -> _Plan:
         P = _Plan()
         dev = self.dev
         views = P.views
@@ -228,7 +280,7 @@ class CompiledModel:
                 continue
             out_dims = (*lead(r), *t.dims)
             if isinstance(op, (g.QMatmulOp, g.QLinearOp)):
-                views[r] = self._plan_matmul(P, op, views, out_dims, label, dense, step)
+                views[r] = self._plan_matmul(P, op, views, out_dims, label, dense, step, keep)
                 continue
             out = P.dense(out_dims, t.dtype, label)
             views[r] = out
@@ -239,14 +291,16 @@ class CompiledModel:
                 rows = math.prod(x.dims[:-1])
                 step(label, _call_ptrs, dev.rmsnorm_int, [x, g.qt(op.x).dtype, w, lut, lut.size, int(op.M),
                                                           int(op.s), op.ss_shift_int, op.ss_init_int, rows,
-                                                          x.dims[-1], out])
+                                                          x.dims[-1], out, rt.OP_UNCHECKED if self.proven else 0])
             elif isinstance(op, g.SoftmaxLutOp):
                 x = dense(views[op.x], label + ".x")
                 lut = dense(views[op.lut], label + ".lut")
                 t1, t2 = x.dims[-2], x.dims[-1]
                 batch = math.prod(x.dims[:-2])
+                table = self._const_array(op.lut)
+                sure = self.proven and table is not None and table.min() >= 0 and table[-1] >= 1
                 step(label, _call_ptrs, dev.softmax_lut, [x, lut, int(op.one), bool(op.causal), batch, t1, t2, out,
-                                                          t.dtype])
+                                                          t.dtype, rt.OP_UNCHECKED if sure else 0])
             elif isinstance(op, g.AddRequantOp):
                 a = dense(views[op.a], label + ".a")
                 b = dense(views[op.b], label + ".b")
@@ -298,9 +352,8 @@ class CompiledModel:
         op = value.owner
         return op.value if op.value is not None else self.consts[op.sym_str]
 
-    def _plan_matmul(self, P, op, views, out_dims, label, dense, step):
+    def _plan_matmul(self, P, op, views, out_dims, label, dense, step, keep):
         t = g.qt(op.result)
-        nb_lead = len(out_dims) - 2
         M, N = out_dims[-2], out_dims[-1]
         K = g.qt(op.a).dims[-1]
         # result storage: dense in the chosen physical order, logical view by permuting back
@@ -309,73 +362,95 @@ class CompiledModel:
             k = 0 if op.result in self.is_const else 1
             pfull = list(range(k)) + [p + k for p in perm]
             st = P.dense([out_dims[i] for i in pfull], t.dtype, label)
-            inv = [pfull.index(i) for i in range(len(pfull))]
-            out = st.permute(inv)
+            out = st.permute([pfull.index(i) for i in range(len(pfull))])
         else:
             out = P.dense(out_dims, t.dtype, label)
-        # A: (lead..., M, K) with K contiguous
+        swapped = perm is not None and perm == _swap_last2(len(perm))
+        # A rows: (lead..., M, K) with K contiguous
         a = views[op.a]
-        if op.a in self.is_const and nb_lead:
-            a = a.prepend(out_dims[0]) if len(a.dims) < len(out_dims) else a
         if a.strides[-1] != 1 and a.dims[-1] != 1:
             a = dense(a, label + ".a")
-        # Bt: (lead..., N, K) with K contiguous
-        bv = views[op.b]
+        # Bt rows: (lead..., N, K) with K contiguous
         if op.b in self.is_const and len(g.qt(op.b).dims) == 2:
             bt = self._bt_const(op)
         else:
-            bt = bv.permute(list(range(len(bv.dims) - 2)) + [len(bv.dims) - 1, len(bv.dims) - 2])
+            bv = views[op.b]
+            bt = bv.permute(_swap_last2(len(bv.dims)))
             if bt.strides[-1] != 1 and bt.dims[-1] != 1:
                 bt = _dense_copy_into(P, step, self.dev, bt, label + ".bt")
-        lut = None
-        if op.lut is not None:
-            lut = views[op.lut]
-        # lead dims: broadcast B over missing leading dims
-        la = list(zip(a.dims[:-2], a.strides[:-2]))
-        lc = list(zip(out.dims[:-2], out.strides[:-2]))
-        lb = list(zip(bt.dims[:-2], bt.strides[:-2]))
-        lb = [(d, 0) for d, _ in lc[:len(lc) - len(lb)]] + lb
-        la = [(d, 0) for d, _ in lc[:len(lc) - len(la)]] + la
-        # fold every lead dim into M when A and C allow it and B does not vary over them
-        if all(s == 0 for _, s in lb):
-            a2 = a.reshape((math.prod(a.dims[:-1]), K)) if len(a.dims) == len(out.dims) else None
-            c2 = out.reshape((math.prod(out.dims[:-1]), N))
-            if a2 is not None and c2 is not None and (a2.strides[-1] == 1 or K == 1):
-                strides = [0, 0, a2.strides[0], 0, 0, bt.strides[-2], 0, 0, c2.strides[0]]
-                step(label, _call_gemm, self.dev, a2, bt, c2, 1, 1, a2.dims[0], N, K, strides, op, lut, t.dtype)
+        lut = None if op.lut is None else views[op.lut]
+        flags = rt.GEMM_UNCHECKED if self.proven else 0
+        if self.proven and self.acc_bounds.get(op.result, 1 << 31) < (1 << 23) and abs(int(op.M)) < (1 << 23):
+            flags |= rt.GEMM_MUL24
+        if swapped:
+            # the result is stored transposed: compute C^T = Bt . A^T, whose rows are N
+            rows1, rows2, c, Mx, Nx = bt, a, out.permute(_swap_last2(len(out.dims))), N, M
+        else:
+            rows1, rows2, c, Mx, Nx = a, bt, out, M, N
+            if self._causal_skip_ok(op, keep):
+                flags |= rt.GEMM_CAUSAL_SKIP
+            elif self._causal_k_ok(op):
+                flags |= rt.GEMM_CAUSAL_K
+        # lead dims: broadcast an operand over lead dims it lacks (stride 0)
+        lc = list(zip(c.dims[:-2], c.strides[:-2]))
+        l1 = list(zip(rows1.dims[:-2], rows1.strides[:-2]))
+        l2 = list(zip(rows2.dims[:-2], rows2.strides[:-2]))
+        l1 = [(d, 0) for d, _ in lc[:len(lc) - len(l1)]] + l1
+        l2 = [(d, 0) for d, _ in lc[:len(lc) - len(l2)]] + l2
+        # fold every lead dim into the row dim when rows1 and C allow it and rows2 does not vary over them
+        if all(s == 0 for _, s in l2) and not (flags & (rt.GEMM_CAUSAL_SKIP | rt.GEMM_CAUSAL_K)):
+            r1 = rows1.reshape((math.prod(rows1.dims[:-1]), K)) if len(rows1.dims) == len(c.dims) else None
+            c2 = c.reshape((math.prod(c.dims[:-1]), Nx))
+            if r1 is not None and c2 is not None and (r1.strides[-1] == 1 or K == 1):
+                strides = [0, 0, r1.strides[0], 0, 0, rows2.strides[-2], 0, 0, c2.strides[0]]
+                step(label, _call_gemm, self.dev, r1, rows2, c2, 1, 1, r1.dims[0], Nx, K, strides, op, lut, t.dtype,
+                     flags)
                 return out
-        # merge adjacent lead dims that nest in A, B and C alike, down to at most two batch dims
-        lead = [(d, sa, sb, sc) for (d, sa), (_, sb), (_, sc) in zip(la, lb, lc)]
-        lead = [x for x in lead if x[0] != 1]
+        # merge adjacent lead dims that nest in all three alike, down to at most two batch dims
+        lead = [(d, s1, s2, sc) for (d, s1), (_, s2), (_, sc) in zip(l1, l2, lc) if d != 1]
         merged = []
-        for d, sa, sb, sc in lead:
+        for d, s1, s2, sc in lead:
             if merged:
-                D, SA, SB, SC = merged[-1]
-                if SA == sa * d and SB == sb * d and SC == sc * d:
-                    merged[-1] = (D * d, sa, sb, sc)
+                D, S1, S2, SC = merged[-1]
+                if S1 == s1 * d and S2 == s2 * d and SC == sc * d:
+                    merged[-1] = (D * d, s1, s2, sc)
                     continue
-            merged.append((d, sa, sb, sc))
+            merged.append((d, s1, s2, sc))
         if len(merged) > 2:
             raise NotImplementedError(f"{op.name} {op.sym_str!r}: {len(merged)} batch dims that do not merge")
         while len(merged) < 2:
             merged.insert(0, (1, 0, 0, 0))
         (b0, sa0, sb0, sc0), (b1, sa1, sb1, sc1) = merged
-        strides = [sa0, sa1, a.strides[-2], sb0, sb1, bt.strides[-2], sc0, sc1, out.strides[-2]]
-        step(label, _call_gemm, self.dev, a, bt, out, b0, b1, M, N, K, strides, op, lut, t.dtype)
+        strides = [sa0, sa1, rows1.strides[-2], sb0, sb1, rows2.strides[-2], sc0, sc1, c.strides[-2]]
+        step(label, _call_gemm, self.dev, rows1, rows2, c, b0, b1, Mx, Nx, K, strides, op, lut, t.dtype, flags)
         return out
 
-    def plan(self, nb: int) -> _Plan:
+    def _causal_skip_ok(self, op, keep) -> bool:
+        """Scores read only by causal softmaxes, and not returned: tiles above the diagonal are never read."""
+        r = op.result
+        us = self.users.get(r, [])
+        return (keep == "outputs" and r not in self.output_values and bool(us) and r not in self.is_const
+                and all(isinstance(u, g.SoftmaxLutOp) and bool(u.causal) for u in us))
+
+    def _causal_k_ok(self, op) -> bool:
+        """A is a causal softmax output read as is: A[m][k] = 0 for k > m."""
+        own = op.a.owner
+        return isinstance(own, g.SoftmaxLutOp) and bool(own.causal) and op.a not in self.is_const
+
+    def plan(self, nb: int, keep: str = "outputs") -> _Plan:
+        """The cached plan for batch size nb and read-back policy keep."""
         self._ensure_device()
-        if nb not in self._plans:
-            P = self._plan(nb)
+        key = (nb, keep)
+        if key not in self._plans:
+            P = self._plan(nb, keep)
             total = 0
             for b in P.bufs:
                 if b.mem is None:
                     b.mem = self.dev.alloc(b.nbytes)
                     total += b.nbytes
             P.footprint = total
-            self._plans[nb] = P
-        return self._plans[nb]
+            self._plans[key] = P
+        return self._plans[key]
 
     # ------------------------------------------------------------------------------------ (de)quantization
     @property
@@ -495,7 +570,7 @@ class CompiledModel:
             raise TypeError(f"run() got unexpected keyword argument(s) {sorted(run_kw)}")
         syms = self.readable(keep)
         ints_in, nb = self._bind_inputs(x, quantized, batch)
-        plan = self.plan(nb)
+        plan = self.plan(nb, keep)
         with self.dev.lock:
             self.upload_inputs(plan, ints_in)
             self.dev.record(2)
@@ -540,7 +615,7 @@ def _work(fn, args):
     once at its dtype (LUTs and weights included), layout views free."""
     isz = rt.ITEMSIZE
     if fn is _call_gemm:
-        _, a, bt, c, b0, b1, M, N, K, strides, _, _, dt = args
+        _, a, bt, c, b0, b1, M, N, K, strides, _, _, dt, _ = args
         nb = b0 * b1
         b_batches = nb if (strides[3] or strides[4]) else 1
         return "gemm", 2 * nb * M * N * K, nb * M * K + b_batches * N * K + nb * M * N * isz[dt]
@@ -564,9 +639,13 @@ def _work(fn, args):
     return name or "other", 0, 0
 
 
-def _call_gemm(dev, a: View, bt: View, c: View, b0, b1, M, N, K, strides, op, lut, out_dtype):
+def _call_gemm(dev, a: View, bt: View, c: View, b0, b1, M, N, K, strides, op, lut, out_dtype, flags=0):
     dev.gemm_i8(a.ptr, bt.ptr, c.ptr, b0, b1, M, N, K, strides, int(op.M), int(op.s),
-                None if lut is None else lut.ptr, out_dtype)
+                None if lut is None else lut.ptr, out_dtype, flags)
+
+
+def _swap_last2(n):
+    return list(range(n - 2)) + [n - 1, n - 2]
 
 
 def compile(model, example_inputs=None, calib_inputs=None, params=None, schedules=None, *, consts=None,
@@ -579,4 +658,5 @@ def compile(model, example_inputs=None, calib_inputs=None, params=None, schedule
     if kw:
         raise TypeError(f"compile() got unexpected keyword argument(s) {sorted(kw)}")
     module, cs = _resolve_model(model, consts, prove)
-    return CompiledModel(module, cs, device=device)
+    from .models import Built
+    return CompiledModel(module, cs, device=device, proven=prove or isinstance(model, Built))

@@ -168,10 +168,11 @@ def silu_lut(s_in):
 
 # ----------------------------------------------------------------------------------------- overflow proof
 
-def prove_no_overflow(module, consts=None) -> dict:
+def prove_no_overflow(module, consts=None, acc_bounds: dict | None = None) -> dict:
     """Magnitude propagation over the graph (reference quantize.py:175-253): int8 inputs 128, i16 2^15, softmax
     outputs `one`, LUT outputs max|table|. Returns {op sym: worst |intermediate|}; raises OverflowError naming
-    every op whose bound exceeds INT32_MAX."""
+    every op whose bound exceeds INT32_MAX. acc_bounds, when given, receives {matmul result value: bound on its
+    |accumulator|} (what lets a kernel use a 24-bit requant multiply)."""
     consts = consts or {}
     mag, cval, worst, bad = {}, {}, {}, []
     for op in g.func_of(module).ops:
@@ -188,22 +189,24 @@ def prove_no_overflow(module, consts=None) -> dict:
             cval[r] = v
             m = int(np.abs(v).max()) if v.size else 0
         elif isinstance(op, (g.QMatmulOp, g.QLinearOp)):
-            M, s = int(op.M), int(op.s)
+            M, s = abs(int(op.M)), int(op.s)          # magnitudes: a negative multiplier flips no bound
             if op.b in cval:
                 acc = mag[op.a] * int(np.abs(cval[op.b]).sum(axis=0).max())
             else:
                 acc = g.qt(op.a).dims[-1] * mag[op.a] * mag[op.b]
             checks = {"acc": acc, "acc*M + round": acc * M + _rnd(s)}
+            if acc_bounds is not None:
+                acc_bounds[r] = acc
             m = mag[op.lut] if op.lut is not None else (128 if g.qt(r).dtype == "i8" else 1 << 15)
         elif isinstance(op, g.LutOp):
             m = mag[op.table]
         elif isinstance(op, g.LutMulOp):
-            M, s = int(op.M), int(op.s)
+            M, s = abs(int(op.M)), int(op.s)          # magnitudes: a negative multiplier flips no bound
             prod = mag[op.table] * mag[op.y]
             checks = {"lut*y": prod, "lut*y*M + round": prod * M + _rnd(s)}
             m = 128
         elif isinstance(op, g.RmsNormIntOp):
-            M, s = int(op.M), int(op.s)
+            M, s = abs(int(op.M)), int(op.s)          # magnitudes: a negative multiplier flips no bound
             d, n = g.qt(op.x).dims[-1], g.qt(op.lut).dims[0]
             c, e = op.ss_shift_int, op.ss_init_int
             if g.qt(op.x).dtype == "i8" and c == 0 and e == 0:
@@ -228,7 +231,7 @@ def prove_no_overflow(module, consts=None) -> dict:
             checks = {"exp sum": t * emax, "e*one + S/2": emax * one + t * emax // 2}
             m = one
         elif isinstance(op, g.AddRequantOp):
-            Ma, Mb, s = int(op.Ma), int(op.Mb), int(op.s)
+            Ma, Mb, s = abs(int(op.Ma)), abs(int(op.Mb)), int(op.s)
             checks = {"a*Ma + b*Mb + round": mag[op.a] * Ma + mag[op.b] * Mb + _rnd(s)}
             m = 128 if g.qt(r).dtype == "i8" else 1 << 15
         elif isinstance(op, (g.TransposeOp, g.ReshapeOp)):

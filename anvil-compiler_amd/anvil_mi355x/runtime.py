@@ -27,6 +27,11 @@ ITEMSIZE = {"i8": 1, "i16": 2, "i32": 4}
 
 _ERRORS = {1: ValueError, 2: OverflowError, 3: ZeroDivisionError, 4: RuntimeError}
 
+# anvil_gemm_i8_ex flags (include/anvil_mi355x.h)
+GEMM_UNCHECKED, GEMM_CAUSAL_SKIP, GEMM_CAUSAL_K, GEMM_MUL24 = 1, 2, 4, 8
+# anvil_rmsnorm_int_ex / anvil_softmax_lut_ex flags
+OP_UNCHECKED = 1
+
 _p, _i, _i64, _i32, _sz, _f64 = C.c_void_p, C.c_int, C.c_int64, C.c_int32, C.c_size_t, C.c_double
 # symbol -> argtypes (restype int for all but anvil_last_error), in include/anvil_mi355x.h order
 SIGNATURES = {
@@ -43,8 +48,11 @@ SIGNATURES = {
     "anvil_event_record": [_p, _i],
     "anvil_event_elapsed": [_p, _i, _i, C.POINTER(C.c_float)],
     "anvil_gemm_i8": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i],
+    "anvil_gemm_i8_ex": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _i],
     "anvil_rmsnorm_int": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p],
+    "anvil_rmsnorm_int_ex": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p, _i],
     "anvil_softmax_lut": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i],
+    "anvil_softmax_lut_ex": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i, _i],
     "anvil_add_requant": [_p, _p, _i, _p, _i, _i32, _i32, _i, _i64, _p, _i],
     "anvil_lut_i8": [_p, _p, _p, _i64, _p],
     "anvil_lut_mul": [_p, _p, _p, _p, _i32, _i, _i64, _p],
@@ -168,20 +176,20 @@ class Device:
             self.ctx = None
 
     # ------------------------------------------------------------------------------------------ op calls
-    def gemm_i8(self, A, Bt, Cp, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype):
+    def gemm_i8(self, A, Bt, Cp, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags=0):
         st = (C.c_int64 * 9)(*[int(s) for s in strides])
-        self.lib.call("anvil_gemm_i8", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)), C.c_void_p(_ptr(Cp)),
+        self.lib.call("anvil_gemm_i8_ex", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)), C.c_void_p(_ptr(Cp)),
                       batch0, batch1, M, N, K, st, int(mult), shift, C.c_void_p(_ptr(lut) if lut is not None else 0),
-                      DTYPE_CODE[out_dtype])
+                      DTYPE_CODE[out_dtype], int(flags))
 
-    def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out):
-        self.lib.call("anvil_rmsnorm_int", self.ctx, C.c_void_p(_ptr(x)), DTYPE_CODE[x_dtype], C.c_void_p(_ptr(w)),
+    def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out, flags=0):
+        self.lib.call("anvil_rmsnorm_int_ex", self.ctx, C.c_void_p(_ptr(x)), DTYPE_CODE[x_dtype], C.c_void_p(_ptr(w)),
                       C.c_void_p(_ptr(lut)), lut_len, int(mult), shift, ss_shift, int(ss_init), rows, cols,
-                      C.c_void_p(_ptr(out)))
+                      C.c_void_p(_ptr(out)), int(flags))
 
-    def softmax_lut(self, x, lut, one, causal, batch, t1, t2, out, out_dtype):
-        self.lib.call("anvil_softmax_lut", self.ctx, C.c_void_p(_ptr(x)), C.c_void_p(_ptr(lut)), int(one),
-                      int(bool(causal)), batch, t1, t2, C.c_void_p(_ptr(out)), DTYPE_CODE[out_dtype])
+    def softmax_lut(self, x, lut, one, causal, batch, t1, t2, out, out_dtype, flags=0):
+        self.lib.call("anvil_softmax_lut_ex", self.ctx, C.c_void_p(_ptr(x)), C.c_void_p(_ptr(lut)), int(one),
+                      int(bool(causal)), batch, t1, t2, C.c_void_p(_ptr(out)), DTYPE_CODE[out_dtype], int(flags))
 
     def add_requant(self, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype):
         self.lib.call("anvil_add_requant", self.ctx, C.c_void_p(_ptr(a)), DTYPE_CODE[a_dtype], C.c_void_p(_ptr(b)),

@@ -26,6 +26,7 @@ struct anvil_ctx {
   unsigned* flags = nullptr;      // device word of FLAG_* bits
   hipEvent_t events[EVENT_SLOTS] = {};   // created on first use of a slot
   int num_cu = 0;
+  int gemm_cfg = 0;               // ANVIL_GEMM_CFG at init: pins one GEMM tile shape (benchmarking); 0 = by problem
 };
 
 namespace anvil {

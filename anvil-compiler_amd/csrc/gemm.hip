@@ -1,15 +1,30 @@
 // int8 x int8 -> int32 GEMM on CDNA4 MFMA with the fused requant [+ LUT] epilogue of qmatmul / qlinear.
 //
-// C[b][m][n] = epilogue(sum_k A[b][m][k] * Bt[b][n][k]): both operands K-contiguous, so every lane of an MFMA
-// operand reads 16 consecutive K bytes straight from an LDS row. Workgroup tile BM x BN, BK bytes of K per
-// stage, two LDS stages (the next stage's global loads are in flight while the current one feeds the MFMAs).
-// 4 waves in a 2 x 2 grid; each wave owns (BM/2) x (BN/2) outputs as 32 x 32 MFMA tiles
-// (v_mfma_i32_32x32x32_i8: A 32 x 32 bytes, B 32 x 32 bytes, 16 int32 accumulators per lane).
+// C[b][m][n] = epilogue(sum_k A[b][m][k] * Bt[b][n][k]); both operands are K-contiguous, so every MFMA operand
+// lane reads 16 consecutive K bytes from one LDS row.
 //
-// MFMA operand layout: lane l supplies row (l % 32) of A / column (l % 32) of B and 16 K bytes at offset
-// 16 * (l / 32) of the 32-byte K slice; A and B use the same K mapping, so the dot product does not depend on
-// the order in which the hardware pairs the bytes. Accumulator r of lane l holds
-// C[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32].
+// Workgroup: 256 threads = 4 waves in a 2 x 2 grid over a BM x BN output tile; BK bytes of K per pipeline stage,
+// two LDS stages (the next stage's global loads are in flight while the current stage feeds the MFMAs). Each wave
+// owns (BM/2) x (BN/2) outputs as 32 x 32 tiles of v_mfma_i32_32x32x32_i8.
+//
+// The MFMA computes D = Bt_tile . A_tile^T (operand roles swapped), so accumulator r of lane l holds
+// C[m = 32 tm + l % 32][n = 32 tn + 8 (r / 4) + 4 (l / 32) + r % 4]: four consecutive output columns per lane, which
+// pack into one dword (i8) or two (i16) for the LDS-staged epilogue. Both operands use the same K mapping
+// (lane l supplies 16 K bytes at offset 16 (l / 32) of each 32-byte K slice), so the hardware's pairing order of the
+// bytes cannot change the dot product.
+//
+// LDS rows are BK bytes with an XOR swizzle of their 16-byte chunks (swz below), so the lanes served together by a
+// ds_read_b128 (consecutive rows, one logical chunk) hit distinct banks.
+//
+// Epilogue: requant (64-bit and checked against int32 unless the graph's static proof guarantees every value
+// fits, then 32-bit), clamp, optional LUT, staged through LDS as a row-major tile, then written with 16-byte stores.
+//
+// Tile order: workgroup ids are spread round-robin over the 8 XCDs, so consecutive logical tiles are placed on one
+// XCD, and logical tiles run in column groups of GROUP_M row tiles so concurrently running tiles share A and B rows
+// in that XCD's L2.
+//
+// causal = 1: tiles strictly above the diagonal (every n > every m) are skipped (their values are never read);
+// causal = 2: the K loop stops at m0 + BM (A[m][k] = 0 for k > m, e.g. a causal softmax output).
 #include "common.h"
 
 namespace anvil {
@@ -22,17 +37,28 @@ struct GemmArgs {
   const int8_t* B;
   void* C;
   int M, N, K;
-  int batch1;        // blockIdx.y = b0 * batch1 + b1
-  int tiles_n;
+  int batch1;
+  int tiles_m, tiles_n;
   long long sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc;
-  int mult, shift;
-  long long rnd;
+  int mult, shift, rnd;
   const int8_t* lut;
-  int out_dtype;
   unsigned* flags;
+  int causal;
+  int vec_store;
 };
 
-constexpr int G_BM = 128, G_BN = 128, G_BK = 64, G_LDK = G_BK + 16, G_THREADS = 256;
+constexpr int G_THREADS = 256;
+constexpr int GROUP_M = 4;
+
+// Physical 16-byte chunk of logical chunk `chunk` in LDS row `row`: the rows read together by one ds_read_b128
+// (8 consecutive rows at one logical chunk if the LDS serves 128 bytes a cycle from 32 banks, 16 rows if 256 bytes
+// from 64 banks) land in distinct bank groups under either organisation.
+template <int BK>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  static_assert(BK == 64 || BK == 128, "swizzle defined for 64- and 128-byte rows");
+  if (BK == 64) return chunk ^ (((row >> 1) ^ (row >> 3)) & 3);
+  return chunk ^ ((row ^ (row >> 3)) & 7);
+}
 
 // One 16-byte K chunk of one operand row, zero outside [0, rows) x [0, K).
 template <bool VEC>
@@ -53,110 +79,530 @@ __device__ __forceinline__ v4i load_chunk(const int8_t* __restrict__ base, long 
   return v;
 }
 
-template <bool VEC>
+template <bool CHECKED>
+__device__ __forceinline__ int rq(int acc, const GemmArgs& g, int lo, int hi, unsigned& bad) {
+  if (CHECKED) return requant_checked(acc, g.mult, g.shift, (long long)g.rnd, lo, hi, bad);
+  const int v = (acc * g.mult + g.rnd) >> g.shift;     // the static proof keeps acc * M + rnd inside int32
+  return min(max(v, lo), hi);
+}
+
+template <int BM, int BN, int BK, int WGM, int PF, int OSZ, bool CHECKED, bool VEC>
 __global__ __launch_bounds__(G_THREADS) void gemm_i8_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) int8_t As[2][G_BM * G_LDK];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[2][G_BN * G_LDK];
+  constexpr int WGN = 4 / WGM;                           // waves along M x along N
+  constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+  static_assert(WGM * WGN == 4 && TM >= 1 && TN >= 1, "wave grid");
+  constexpr int CPR = BK / 16;
+  constexpr int A_PASS = BM * CPR / G_THREADS, B_PASS = BN * CPR / G_THREADS;
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int SROW = BN * OSZ + 16;                    // epilogue staging row stride (bytes)
+  constexpr int LDS_MAIN = 2 * STAGE, LDS_EPI = BM * SROW;
+  constexpr int LDS_BYTES = LDS_MAIN > LDS_EPI ? LDS_MAIN : LDS_EPI;
+  static_assert(A_PASS >= 1 && B_PASS >= 1 && (BM * CPR) % G_THREADS == 0 && (BN * CPR) % G_THREADS == 0, "tile");
+  __shared__ __attribute__((aligned(16))) int8_t smem[LDS_BYTES];
   __shared__ int8_t lut_s[256];
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int tile = blockIdx.x;
-  const int m0 = (tile / g.tiles_n) * G_BM, n0 = (tile % g.tiles_n) * G_BN;
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  // XCD-aware, grouped tile order
+  const int ntiles = g.tiles_m * g.tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int in_group = GROUP_M * g.tiles_n;
+  const int first_m = (pid / in_group) * GROUP_M;
+  const int gsize = min(g.tiles_m - first_m, GROUP_M);
+  const int tile_m = first_m + (pid % in_group) % gsize;
+  const int tile_n = (pid % in_group) / gsize;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  if (g.causal == 1 && n0 > m0 + BM - 1) return;
+
   const int b0 = blockIdx.y / g.batch1, b1 = blockIdx.y % g.batch1;
   const int8_t* __restrict__ A = g.A + b0 * g.sa0 + b1 * g.sa1 + (long long)m0 * g.lda;
   const int8_t* __restrict__ B = g.B + b0 * g.sb0 + b1 * g.sb1 + (long long)n0 * g.ldb;
   const int rows_a = g.M - m0, rows_b = g.N - n0;
+  const int K = g.causal == 2 ? min(g.K, m0 + BM) : g.K;
 
   if (g.lut) lut_s[t] = g.lut[t];
 
-  // loader mapping: 4 threads per 64-byte row, 64 rows per pass, 2 passes per operand tile
-  const int lc = (t & 3) * 16, lr = t >> 2;
-  v4i ra[2], rb[2];
-  auto gload = [&](int k0) {
+  const int lc = t % CPR, lr = t / CPR;
+  constexpr int RSTEP = G_THREADS / CPR;
+  // PF register sets of staged global loads: the loads of stage s are issued PF iterations before stage s is
+  // written to LDS, so PF iterations of MFMA work cover their latency.
+  v4i ra[PF][A_PASS], rb[PF][B_PASS];
+  auto gload = [&](int set, int k0) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      ra[p] = load_chunk<VEC>(A, g.lda, lr + 64 * p, rows_a, k0 + lc, g.K);
-      rb[p] = load_chunk<VEC>(B, g.ldb, lr + 64 * p, rows_b, k0 + lc, g.K);
-    }
+    for (int p = 0; p < A_PASS; ++p) ra[set][p] = load_chunk<VEC>(A, g.lda, lr + RSTEP * p, rows_a, k0 + lc * 16, K);
+#pragma unroll
+    for (int p = 0; p < B_PASS; ++p) rb[set][p] = load_chunk<VEC>(B, g.ldb, lr + RSTEP * p, rows_b, k0 + lc * 16, K);
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int set, int buf) {
+    int8_t* As = smem + buf * STAGE;
+    int8_t* Bs = As + BM * BK;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      *reinterpret_cast<v4i*>(&As[buf][(lr + 64 * p) * G_LDK + lc]) = ra[p];
-      *reinterpret_cast<v4i*>(&Bs[buf][(lr + 64 * p) * G_LDK + lc]) = rb[p];
+    for (int p = 0; p < A_PASS; ++p) {
+      const int r = lr + RSTEP * p;
+      *reinterpret_cast<v4i*>(As + r * BK + swz<BK>(r, lc) * 16) = ra[set][p];
+    }
+#pragma unroll
+    for (int p = 0; p < B_PASS; ++p) {
+      const int r = lr + RSTEP * p;
+      *reinterpret_cast<v4i*>(Bs + r * BK + swz<BK>(r, lc) * 16) = rb[set][p];
     }
   };
 
-  v16i acc[2][2];
+  v16i acc[TN][TM];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TN; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < TM; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-  const int nk = (g.K + G_BK - 1) / G_BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  const int arow = wm * 64 + (lane & 31), brow = wn * 64 + (lane & 31), kof = (lane >> 5) * 16;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * G_BK);
+  const int half = lane >> 5, l32 = lane & 31;
+  auto compute = [&](int buf) {
+    const int8_t* As = smem + buf * STAGE;
+    const int8_t* Bs = As + BM * BK;
 #pragma unroll
-    for (int ks = 0; ks < G_BK / 32; ++ks) {
-      v4i a[2], b[2];
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      v4i af[TM], bf[TN];
+      const int ch = ks * 2 + half;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        a[i] = *reinterpret_cast<const v4i*>(&As[cur][(arow + 32 * i) * G_LDK + ks * 32 + kof]);
-        b[i] = *reinterpret_cast<const v4i*>(&Bs[cur][(brow + 32 * i) * G_LDK + ks * 32 + kof]);
+      for (int j = 0; j < TM; ++j) {
+        const int r = wm * WM + j * 32 + l32;
+        af[j] = *reinterpret_cast<const v4i*>(As + r * BK + swz<BK>(r, ch) * 16);
       }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TN; ++i) {
+        const int r = wn * WN + i * 32 + l32;
+        bf[i] = *reinterpret_cast<const v4i*>(Bs + r * BK + swz<BK>(r, ch) * 16);
+      }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i], af[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) lstore(cur ^ 1);
-    __syncthreads();
+  };
+
+  const int nk = (K + BK - 1) / BK;
+#pragma unroll
+  for (int s = 0; s < PF; ++s)
+    if (s < nk) gload(s, s * BK);
+  lstore(0, 0);
+  __syncthreads();
+  for (int kt0 = 0; kt0 < nk; kt0 += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int kt = kt0 + u;
+      if (kt < nk) {
+        if (kt + PF < nk) gload(u, (kt + PF) * BK);          // stage kt + PF has the parity of stage kt
+        compute(kt & 1);
+        if (kt + 1 < nk) lstore((u + 1) % PF, (kt + 1) & 1);
+        __syncthreads();
+      }
+    }
   }
 
-  // epilogue: checked requant, clamp to the result dtype, optional LUT; one writer per output element
-  const int lo = g.out_dtype == ANVIL_I8 ? -128 : -32768, hi = g.out_dtype == ANVIL_I8 ? 127 : 32767;
+  // epilogue: requant (+ LUT) into an LDS row-major staging tile, then 16-byte global stores
+  const int lo = OSZ == 1 ? -128 : -32768, hi = OSZ == 1 ? 127 : 32767;
   unsigned bad = 0;
-  char* Cb = reinterpret_cast<char*>(g.C);
-  const long long cbase = b0 * g.sc0 + b1 * g.sc1;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TN; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TM; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-        if (row < g.M && col < g.N) {
-          int v = requant_checked(acc[i][j][r], g.mult, g.shift, g.rnd, lo, hi, bad);
-          const long long off = cbase + (long long)row * g.ldc + col;
-          if (g.out_dtype == ANVIL_I8) {
-            if (g.lut) v = lut_s[v + 128];
-            reinterpret_cast<int8_t*>(Cb)[off] = (int8_t)v;
-          } else {
-            reinterpret_cast<int16_t*>(Cb)[off] = (int16_t)v;
-          }
+      for (int q = 0; q < 4; ++q) {
+        const int m_l = wm * WM + j * 32 + l32;
+        const int n_l = wn * WN + i * 32 + 8 * q + 4 * half;
+        int v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = rq<CHECKED>(acc[i][j][4 * q + e], g, lo, hi, bad);
+          if (OSZ == 1 && g.lut) v[e] = lut_s[v[e] + 128];
+        }
+        int8_t* dst = smem + m_l * SROW + n_l * OSZ;
+        if (OSZ == 1) {
+          *reinterpret_cast<unsigned*>(dst) =
+              (unsigned)(v[0] & 255) | ((unsigned)(v[1] & 255) << 8) | ((unsigned)(v[2] & 255) << 16) | ((unsigned)v[3] << 24);
+        } else {
+          *reinterpret_cast<unsigned*>(dst) = (unsigned)(v[0] & 0xffff) | ((unsigned)v[1] << 16);
+          *reinterpret_cast<unsigned*>(dst + 4) = (unsigned)(v[2] & 0xffff) | ((unsigned)v[3] << 16);
         }
       }
-  if (bad) raise_flag(g.flags, FLAG_OVERFLOW);
+  if (CHECKED && bad) raise_flag(g.flags, FLAG_OVERFLOW);
+  __syncthreads();
+
+  constexpr int CH_ROW = BN * OSZ / 16;                  // 16-byte chunks per staged row
+  constexpr int ROWS_PER_PASS = G_THREADS / CH_ROW;
+  const int cc = t % CH_ROW, rr0 = t / CH_ROW;
+  char* Cb = reinterpret_cast<char*>(g.C) + (b0 * g.sc0 + b1 * g.sc1) * OSZ;
+  const int cols_valid = min(BN, g.N - n0);
+  const int cfirst = cc * 16 / OSZ;                      // first column of this chunk within the tile
+#pragma unroll 4
+  for (int rr = rr0; rr < BM; rr += ROWS_PER_PASS) {
+    const int m = m0 + rr;
+    if (m >= g.M) break;
+    const int8_t* src = smem + rr * SROW + cc * 16;
+    char* dst = Cb + ((long long)m * g.ldc + n0 + cfirst) * OSZ;
+    if (g.vec_store && cfirst + 16 / OSZ <= cols_valid) {
+      *reinterpret_cast<v4i*>(dst) = *reinterpret_cast<const v4i*>(src);
+    } else {
+      for (int e = 0; e < 16 / OSZ; ++e)
+        if (cfirst + e < cols_valid) {
+          if (OSZ == 1)
+            dst[e] = src[e];
+          else
+            reinterpret_cast<int16_t*>(dst)[e] = reinterpret_cast<const int16_t*>(src)[e];
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- fast path
+// The production kernel for proven graphs with 16-byte aligned, K-contiguous operands (every block GEMM).
+//
+// Operand tiles go global -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging): each wave instruction fills one
+// contiguous KiB of LDS, lane l its 16 bytes, and the lane's global address is chosen so the KiB holds 16 swizzled
+// rows. The buffer resource's record count ends at the tile's last valid row and an out-of-range K chunk gets an
+// out-of-range offset, so the hardware writes zeros there: no branches around loads. Three LDS stages live in three
+// distinct arrays (so the compiler tracks each one's outstanding loads separately); iteration kt waits for its own
+// stage-kt loads (s_waitcnt vmcnt(G), G = one stage's loads still in flight), meets the other waves at s_barrier,
+// issues stage kt + 2 into the array stage kt - 1 used, then runs stage kt's MFMAs. The epilogue reuses the three
+// arrays as its staging tile. MUL24: every |acc| and |M| is below 2^23 (host-proven), so acc * M + rnd is one
+// 24-bit multiply-add.
+
+constexpr unsigned RSRC_DW3 = 0x00020000u;               // raw buffer, 32-bit data format (gfx9 family)
+constexpr unsigned OOB = 0xFFFFFFF0u;
+
+// 16 bytes per lane from buffer offset voff into LDS at lds + 16 * lane (lds must be wave-uniform)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, int8_t* lds, unsigned voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  // s_waitcnt with vmcnt = n (0..15), expcnt and lgkmcnt left at their "no wait" maxima
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+}
+
+// all waves' LDS writes for a stage have landed once each has waited for its own loads and the barrier is passed;
+// the acquire fence keeps the following LDS reads below the barrier without waiting on later loads
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0): this wave's loads beyond the newest N have landed and its LDS accesses are done
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
+}
+
+template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24>
+__global__ __launch_bounds__(G_THREADS) void gemm_i8_fast(GemmArgs g) {
+  constexpr int BK = 64, CPR = BK / 16;
+  constexpr int WGN = 4 / WGM;
+  constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+  static_assert(WGM * WGN == 4 && TM >= 1 && TN >= 1, "wave grid");
+  static_assert(NS == 3 || NS == 4, "three or four LDS stages");
+  constexpr int IA = BM * CPR / 64, IB = BN * CPR / 64;  // wave instructions (KiB) per operand per stage
+  static_assert(IA % 4 == 0 && IB % 4 == 0, "each wave issues an equal share of a stage");
+  constexpr int JA = IA / 4, JB = IB / 4, G = JA + JB;   // per-wave loads per stage
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int SROW = BN * OSZ + 16;
+  constexpr int ROWS_PER_ARR_MIN = (BM + NS - 1) / NS;
+  constexpr int ARR = STAGE > ROWS_PER_ARR_MIN * SROW ? STAGE : ROWS_PER_ARR_MIN * SROW;
+  constexpr int RPA = ARR / SROW;                        // staging rows per array
+  __shared__ __attribute__((aligned(1024))) int8_t L0[ARR];
+  __shared__ __attribute__((aligned(1024))) int8_t L1[ARR];
+  __shared__ __attribute__((aligned(1024))) int8_t L2[ARR];
+  __shared__ __attribute__((aligned(1024))) int8_t L3[NS == 4 ? ARR : 16];
+  __shared__ int8_t lut_s[256];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  const int ntiles = g.tiles_m * g.tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int in_group = GROUP_M * g.tiles_n;
+  const int first_m = (pid / in_group) * GROUP_M;
+  const int gsize = min(g.tiles_m - first_m, GROUP_M);
+  const int tile_m = first_m + (pid % in_group) % gsize;
+  const int tile_n = (pid % in_group) / gsize;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  if (g.causal == 1 && n0 > m0 + BM - 1) return;
+
+  const int b0 = blockIdx.y / g.batch1, b1 = blockIdx.y % g.batch1;
+  const int8_t* Ab = g.A + b0 * g.sa0 + b1 * g.sa1 + (long long)m0 * g.lda;
+  const int8_t* Bb = g.B + b0 * g.sb0 + b1 * g.sb1 + (long long)n0 * g.ldb;
+  const int rows_a = min(g.M - m0, BM), rows_b = min(g.N - n0, BN);
+  const int K = g.causal == 2 ? min(g.K, m0 + BM) : g.K;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, (int)(rows_a * g.lda), RSRC_DW3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, (int)(rows_b * g.ldb), RSRC_DW3);
+
+  if (g.lut) lut_s[t] = g.lut[t];
+
+  // per-lane global byte offsets (without k0) of the chunks this wave loads, and their K offsets
+  unsigned offa[JA], offb[JB];
+  int ka[JA], kb[JB];
+#pragma unroll
+  for (int j = 0; j < JA; ++j) {
+    const int P = (wave + 4 * j) * 64 + lane, row = P / CPR, c = swz<BK>(row, P % CPR);
+    offa[j] = (unsigned)(row * g.lda + c * 16);
+    ka[j] = c * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    const int P = (wave + 4 * j) * 64 + lane, row = P / CPR, c = swz<BK>(row, P % CPR);
+    offb[j] = (unsigned)(row * g.ldb + c * 16);
+    kb[j] = c * 16;
+  }
+  // a stage at or past K loads zeros (every offset out of range): issuing is unconditional, so the compiler's
+  // per-array tracking of outstanding LDS writes stays exact (a branch around the loads would make it wait for all)
+  auto issue = [&](int8_t* arr, int k0) {
+#pragma unroll
+    for (int j = 0; j < JA; ++j) dma16(ra, arr + (wave + 4 * j) * 1024, k0 + ka[j] < K ? offa[j] + k0 : OOB);
+#pragma unroll
+    for (int j = 0; j < JB; ++j) dma16(rb, arr + BM * BK + (wave + 4 * j) * 1024, k0 + kb[j] < K ? offb[j] + k0 : OOB);
+  };
+
+  v16i acc[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+  // MFMA fragments are double-buffered in registers: the next k-step's fragments are read from LDS while the
+  // current k-step's MFMAs run, so LDS latency never sits between two MFMA groups
+  const int half = lane >> 5, l32 = lane & 31;
+  v4i af[2][TM], bf[2][TN];
+  auto load_frags = [&](int set, const int8_t* arr, int ks) {
+    const int ch = ks * 2 + half;
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int r = wm * WM + j * 32 + l32;
+      af[set][j] = *reinterpret_cast<const v4i*>(arr + r * BK + (swz<BK>(r, ch) << 4));
+    }
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+      const int r = wn * WN + i * 32 + l32;
+      bf[set][i] = *reinterpret_cast<const v4i*>(arr + BM * BK + r * BK + (swz<BK>(r, ch) << 4));
+    }
+  };
+  auto mm = [&](int set) {
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[set][i], af[set][j], acc[i][j], 0, 0, 0);
+  };
+  // One pipeline step over stage kt (in `cur`, complete and visible on entry, its first fragments in set 0):
+  // stage kt + NS - 1 goes into `nxt` (the array of stage kt - 1, which every wave finished reading before the
+  // previous step's barrier); then the k-steps of stage kt run, and before the last one this wave waits for its
+  // share of stage kt + 1 (the loads still allowed in flight are stages kt + 2 .. kt + NS - 1) and for its own LDS
+  // reads of stage kt, meets the other waves at the barrier, and prefetches stage kt + 1's first fragments from
+  // `next` during the last k-step's MFMAs. Past the last stage those reads are harmless and unused.
+  constexpr int KS = BK / 32;
+  static_assert(KS % 2 == 0, "fragment sets alternate within a stage");
+  const int nk = (K + BK - 1) / BK;
+  auto step = [&](int kt, const int8_t* cur, int8_t* nxt, const int8_t* next) {
+    issue(nxt, (kt + NS - 1) * BK);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < KS - 1; ++ks) {
+      load_frags((ks + 1) & 1, cur, ks + 1);
+      __builtin_amdgcn_sched_barrier(0);            // keep the prefetch ahead of the MFMAs it overlaps
+      mm(ks & 1);
+      __builtin_amdgcn_sched_barrier(0);            // and the waits below after them
+    }
+    wait_vm_lgkm0<(NS - 2) * G>();
+    stage_barrier();
+    load_frags(0, next, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mm((KS - 1) & 1);
+  };
+
+  issue(L0, 0);
+  issue(L1, BK);
+  if (NS == 4) issue(L2, 2 * BK);
+  wait_vm_lgkm0<(NS - 2) * G>();
+  stage_barrier();
+  load_frags(0, L0, 0);
+  int kt = 0;
+  if (NS == 3) {
+    for (; kt + 3 <= nk; kt += 3) {
+      step(kt, L0, L2, L1);
+      step(kt + 1, L1, L0, L2);
+      step(kt + 2, L2, L1, L0);
+    }
+    if (kt < nk) step(kt, L0, L2, L1);
+    if (kt + 1 < nk) step(kt + 1, L1, L0, L2);
+  } else {
+    for (; kt + 4 <= nk; kt += 4) {
+      step(kt, L0, L3, L1);
+      step(kt + 1, L1, L0, L2);
+      step(kt + 2, L2, L1, L3);
+      step(kt + 3, L3, L2, L0);
+    }
+    if (kt < nk) step(kt, L0, L3, L1);
+    if (kt + 1 < nk) step(kt + 1, L1, L0, L2);
+    if (kt + 2 < nk) step(kt + 2, L2, L1, L3);
+  }
+
+  // epilogue: requant (+ LUT) into the staging tile spread over the stage arrays (RPA rows each), then 16-byte
+  // stores
+  __syncthreads();
+  const int lo = OSZ == 1 ? -128 : -32768, hi = OSZ == 1 ? 127 : 32767;
+  auto srow = [&](int r) -> int8_t* {
+    if (r < RPA) return L0 + r * SROW;
+    if (r < 2 * RPA) return L1 + (r - RPA) * SROW;
+    if (NS == 3 || r < 3 * RPA) return L2 + (r - 2 * RPA) * SROW;
+    return L3 + (r - 3 * RPA) * SROW;
+  };
+#pragma unroll
+  for (int j = 0; j < TM; ++j) {
+    int8_t* rowp = srow(wm * WM + j * 32 + l32);
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n_l = wn * WN + i * 32 + 8 * q + 4 * half;
+        int v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int a = acc[i][j][4 * q + e];
+          const int x = MUL24 ? (__mul24(a, g.mult) + g.rnd) : (a * g.mult + g.rnd);
+          v[e] = min(max(x >> g.shift, lo), hi);
+          if (OSZ == 1 && g.lut) v[e] = lut_s[v[e] + 128];
+        }
+        if (OSZ == 1) {
+          *reinterpret_cast<unsigned*>(rowp + n_l) =
+              (unsigned)(v[0] & 255) | ((unsigned)(v[1] & 255) << 8) | ((unsigned)(v[2] & 255) << 16) | ((unsigned)v[3] << 24);
+        } else {
+          *reinterpret_cast<unsigned*>(rowp + 2 * n_l) = (unsigned)(v[0] & 0xffff) | ((unsigned)v[1] << 16);
+          *reinterpret_cast<unsigned*>(rowp + 2 * n_l + 4) = (unsigned)(v[2] & 0xffff) | ((unsigned)v[3] << 16);
+        }
+      }
+  }
+  __syncthreads();
+
+  constexpr int CH_ROW = BN * OSZ / 16;
+  constexpr int ROWS_PER_PASS = G_THREADS / CH_ROW;
+  const int cc = t % CH_ROW, rr0 = t / CH_ROW;
+  char* Cb = reinterpret_cast<char*>(g.C) + (b0 * g.sc0 + b1 * g.sc1) * OSZ;
+  const int cols_valid = min(BN, g.N - n0);
+  const int cfirst = cc * 16 / OSZ;
+  for (int rr = rr0; rr < BM; rr += ROWS_PER_PASS) {
+    const int m = m0 + rr;
+    if (m >= g.M) break;
+    const int8_t* src = srow(rr) + cc * 16;
+    char* dst = Cb + ((long long)m * g.ldc + n0 + cfirst) * OSZ;
+    if (g.vec_store && cfirst + 16 / OSZ <= cols_valid) {
+      *reinterpret_cast<v4i*>(dst) = *reinterpret_cast<const v4i*>(src);
+    } else {
+      for (int e = 0; e < 16 / OSZ; ++e)
+        if (cfirst + e < cols_valid) {
+          if (OSZ == 1)
+            dst[e] = src[e];
+          else
+            reinterpret_cast<int16_t*>(dst)[e] = reinterpret_cast<const int16_t*>(src)[e];
+        }
+    }
+  }
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <int BM, int BN, int WGM, int NS, bool MUL24>
+static void launch_fast(GemmArgs& g, int osz, int batch, hipStream_t s) {
+  g.tiles_m = (g.M + BM - 1) / BM;
+  g.tiles_n = (g.N + BN - 1) / BN;
+  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  if (osz == 1)
+    hipLaunchKernelGGL((gemm_i8_fast<BM, BN, WGM, NS, 1, MUL24>), grid, dim3(G_THREADS), 0, s, g);
+  else
+    hipLaunchKernelGGL((gemm_i8_fast<BM, BN, WGM, NS, 2, MUL24>), grid, dim3(G_THREADS), 0, s, g);
+}
+
+template <bool MUL24>
+static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s, int cfg) {
+  switch (cfg) {
+    case 11: return launch_fast<256, 256, 2, 3, MUL24>(g, osz, batch, s);
+    case 12: return launch_fast<256, 256, 2, 4, MUL24>(g, osz, batch, s);
+    case 13: return launch_fast<128, 128, 2, 3, MUL24>(g, osz, batch, s);
+    case 14: return launch_fast<128, 128, 2, 4, MUL24>(g, osz, batch, s);
+    case 15: return launch_fast<256, 128, 2, 4, MUL24>(g, osz, batch, s);
+    default: break;
+  }
+  // measured on MI355X: three 128 x 128 workgroups per CU (48 KiB LDS each) hide each other's barriers and
+  // epilogues best; only long-K products (L2 traffic per MFMA halves with the 256 x 256 tile) prefer the big tile
+  if (g.K >= 2048 && g.M >= 1024 && g.N >= 256)
+    launch_fast<256, 256, 2, 4, MUL24>(g, osz, batch, s);
+  else
+    launch_fast<128, 128, 2, 3, MUL24>(g, osz, batch, s);
+}
+
+template <int BM, int BN, int BK, int WGM, int PF, bool CHECKED>
+static void launch_cfg(GemmArgs& g, int osz, bool vec, int batch, hipStream_t s) {
+  g.tiles_m = (g.M + BM - 1) / BM;
+  g.tiles_n = (g.N + BN - 1) / BN;
+  dim3 grid(g.tiles_m * g.tiles_n, batch);
+  if (osz == 1) {
+    if (vec)
+      hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, WGM, PF, 1, CHECKED, true>), grid, dim3(G_THREADS), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, WGM, PF, 1, CHECKED, false>), grid, dim3(G_THREADS), 0, s, g);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, WGM, PF, 2, CHECKED, true>), grid, dim3(G_THREADS), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, WGM, PF, 2, CHECKED, false>), grid, dim3(G_THREADS), 0, s, g);
+  }
+}
+
+// Tile shape by problem: 128 x 128 for checked runs (its epilogue keeps the 64-bit checks in registers) and small
+// problems, 256 x 64 with the four waves stacked along M when N <= 64 (attention's P.V), 256 x 256 otherwise.
+// cfg (the context's ANVIL_GEMM_CFG, a benchmarking override) pins one shape for every unchecked GEMM.
+static void launch_gemm(GemmArgs& g, bool checked, int osz, bool vec, int batch, hipStream_t s, int cfg) {
+  if (checked) return launch_cfg<128, 128, 64, 2, 1, true>(g, osz, vec, batch, s);
+  switch (cfg) {
+    case 1: return launch_cfg<256, 256, 64, 2, 1, false>(g, osz, vec, batch, s);
+    case 2: return launch_cfg<256, 256, 64, 2, 2, false>(g, osz, vec, batch, s);
+    case 3: return launch_cfg<256, 128, 64, 2, 2, false>(g, osz, vec, batch, s);
+    case 4: return launch_cfg<128, 128, 64, 2, 2, false>(g, osz, vec, batch, s);
+    case 5: return launch_cfg<256, 256, 128, 2, 1, false>(g, osz, vec, batch, s);
+    case 6: return launch_cfg<128, 256, 64, 2, 2, false>(g, osz, vec, batch, s);
+    default: break;
+  }
+  if (g.N <= 64)
+    launch_cfg<256, 64, 64, 4, 2, false>(g, osz, vec, batch, s);
+  else if (g.M <= 128 || g.N <= 128)
+    launch_cfg<128, 128, 64, 2, 2, false>(g, osz, vec, batch, s);
+  else
+    launch_cfg<256, 256, 64, 2, 2, false>(g, osz, vec, batch, s);
+}
 
 }  // namespace anvil
 
 using namespace anvil;
 
-extern "C" int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1,
-                             int M, int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut,
-                             int out_dtype) {
-  if (int r = check_ctx(ctx)) return r;
+extern "C" int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1,
+                                int M, int N, int K, const int64_t* strides, int32_t mult, int shift,
+                                const int8_t* lut, int out_dtype, int flags) {
   if (!A || !Bt || !C || !strides) return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: null pointer");
   if (batch0 < 1 || batch1 < 1 || M < 1 || N < 1 || K < 1)
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: non-positive size (batch %d x %d, M %d, N %d, K %d)", batch0,
@@ -166,6 +612,13 @@ extern "C" int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, 
   if (out_dtype != ANVIL_I8 && out_dtype != ANVIL_I16)
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: result dtype must be i8 or i16");
   if (lut && out_dtype != ANVIL_I8) return set_error(ANVIL_E_VALUE, "a LUT epilogue needs an i8 result");
+  if (flags & ~(ANVIL_GEMM_UNCHECKED | ANVIL_GEMM_CAUSAL_SKIP | ANVIL_GEMM_CAUSAL_K | ANVIL_GEMM_MUL24))
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: unknown flags %d", flags);
+  if ((flags & ANVIL_GEMM_MUL24) && (mult >= (1 << 23) || mult < -(1 << 23)))
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: MUL24 needs |mult| < 2^23 (got %d)", mult);
+  if ((flags & ANVIL_GEMM_CAUSAL_SKIP) && (flags & ANVIL_GEMM_CAUSAL_K))
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: the two causal modes exclude each other");
+  if (int r = check_ctx(ctx)) return r;
   GemmArgs g;
   g.A = A;
   g.B = Bt;
@@ -185,21 +638,35 @@ extern "C" int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, 
   g.ldc = strides[8];
   g.mult = mult;
   g.shift = shift;
-  g.rnd = shift ? (1ll << (shift - 1)) : 0;
+  g.rnd = shift ? (int)(1u << (shift - 1)) : 0;
   g.lut = lut;
-  g.out_dtype = out_dtype;
   g.flags = ctx->flags;
-  const int tiles_m = (M + G_BM - 1) / G_BM;
-  g.tiles_n = (N + G_BN - 1) / G_BN;
-  if ((long long)tiles_m * g.tiles_n > (1ll << 31) - 1) return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: too many tiles");
+  g.causal = (flags & ANVIL_GEMM_CAUSAL_SKIP) ? 1 : ((flags & ANVIL_GEMM_CAUSAL_K) ? 2 : 0);
+  const bool checked = !(flags & ANVIL_GEMM_UNCHECKED);
   auto ok16 = [](long long v) { return (v & 15) == 0; };
   const bool vec = (K & 15) == 0 && aligned16(A) && aligned16(Bt) && ok16(g.lda) && ok16(g.ldb) &&
                    (batch0 == 1 || (ok16(g.sa0) && ok16(g.sb0))) && (batch1 == 1 || (ok16(g.sa1) && ok16(g.sb1)));
-  dim3 grid(tiles_m * g.tiles_n, batch0 * batch1);
-  if (vec)
-    hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, dim3(G_THREADS), 0, ctx->stream, g);
-  else
-    hipLaunchKernelGGL(gemm_i8_kernel<false>, grid, dim3(G_THREADS), 0, ctx->stream, g);
+  const int osz = out_dtype == ANVIL_I8 ? 1 : 2;
+  g.vec_store = aligned16(C) && ok16(g.ldc * osz) && (batch0 == 1 || ok16(g.sc0 * osz)) &&
+                (batch1 == 1 || ok16(g.sc1 * osz));
+  if ((long long)((M + 127) / 128) * ((N + 63) / 64) > (1ll << 31) - 1)
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: too many tiles");
+  const bool force_generic = ctx->gemm_cfg >= 1 && ctx->gemm_cfg <= 6;   // benchmarking override
+  const bool fast = !checked && vec && !force_generic && 256ll * g.lda < (1ll << 31) && 256ll * g.ldb < (1ll << 31);
+  if (fast) {
+    if (flags & ANVIL_GEMM_MUL24)
+      launch_fast_by_shape<true>(g, osz, batch0 * batch1, ctx->stream, ctx->gemm_cfg);
+    else
+      launch_fast_by_shape<false>(g, osz, batch0 * batch1, ctx->stream, ctx->gemm_cfg);
+  } else {
+    launch_gemm(g, checked, osz, vec, batch0 * batch1, ctx->stream, ctx->gemm_cfg);
+  }
   ANVIL_LAUNCHED();
   return ANVIL_OK;
+}
+
+extern "C" int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1,
+                             int M, int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut,
+                             int out_dtype) {
+  return anvil_gemm_i8_ex(ctx, A, Bt, C, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, 0);
 }

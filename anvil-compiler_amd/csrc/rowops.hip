@@ -26,6 +26,150 @@ __device__ __forceinline__ long long floordiv(long long n, long long d) {
   return q;
 }
 
+__device__ __forceinline__ int wave_sum32(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int sbyte(const v4i& v, int b) {   // signed byte b (0..15) of a 16-byte chunk
+  return (int)(int8_t)((unsigned)v[b >> 2] >> (8 * (b & 3)));
+}
+
+// ------------------------------------------------------------------------------------- fast softmax_lut
+// For proven graphs (every intermediate fits int32, lut >= 0 and lut[255] >= 1, so S >= 1) with rows of a multiple
+// of 16 bytes: one wavefront per row, the row in registers as 16-byte chunks (lane l holds chunks l, l + 64, ...;
+// causally masked chunks are not loaded), wave-reduced max and exp sum. The exp value of an element depends only on
+// d = x - max + 255, so the 256 possible quotients (lut[d] one + S // 2) // S of a row are computed once (four exact
+// integer divisions per lane) into an LDS table, and each output element is one table lookup.
+template <int R, typename TO>
+__global__ __launch_bounds__(R_THREADS) void softmax_fast(const int8_t* __restrict__ x, const int* __restrict__ lut,
+                                                           int one, int causal, long long rows, int t1, int t2,
+                                                           TO* __restrict__ out) {
+  __shared__ int lut_s[256];
+  __shared__ TO ptab[R_WAVES][256];
+  lut_s[threadIdx.x] = lut[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  TO* pt = ptab[w];
+  const int chunks = t2 >> 4;
+  for (long long row = (long long)blockIdx.x * R_WAVES + w; row < rows; row += (long long)gridDim.x * R_WAVES) {
+    const int i = (int)(row % t1);
+    const int kept = causal ? min(i + 1, t2) : t2;
+    const int8_t* xr = x + row * t2;
+    v4i xv[R];
+    int m = -128;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = lane + 64 * r;
+      xv[r] = v4i{0, 0, 0, 0};
+      if (c < chunks && 16 * c < kept) {
+        xv[r] = *reinterpret_cast<const v4i*>(xr + 16 * c);
+#pragma unroll
+        for (int b = 0; b < 16; ++b)
+          if (16 * c + b < kept) m = max(m, sbyte(xv[r], b));
+      }
+    }
+    m = wave_max(m);
+    int S = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = lane + 64 * r;
+      if (c < chunks && 16 * c < kept) {
+#pragma unroll
+        for (int b = 0; b < 16; ++b)
+          if (16 * c + b < kept) S += lut_s[sbyte(xv[r], b) - m + 255];
+      }
+    }
+    S = wave_sum32(S);
+    const unsigned us = (unsigned)S, half = us >> 1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int d = lane + 64 * k;
+      pt[d] = (TO)(((unsigned)lut_s[d] * (unsigned)one + half) / us);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");     // table entries written by other lanes of the wave
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = lane + 64 * r;
+      if (c >= chunks) continue;
+      TO* o = out + row * t2 + 16 * c;
+      if (sizeof(TO) == 1) {
+        unsigned wv[4] = {0, 0, 0, 0};
+        if (16 * c < kept) {
+#pragma unroll
+          for (int b = 0; b < 16; ++b)
+            if (16 * c + b < kept) wv[b >> 2] |= (unsigned)(uint8_t)pt[sbyte(xv[r], b) - m + 255] << (8 * (b & 3));
+        }
+        *reinterpret_cast<v4i*>(o) = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          int wv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int b = 4 * q + e;
+            wv[e] = 16 * c + b < kept ? (int)pt[sbyte(xv[r], b) - m + 255] : 0;
+          }
+          *reinterpret_cast<v4i*>(o + 4 * q) = v4i{wv[0], wv[1], wv[2], wv[3]};
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();                 // the table is rewritten for the wave's next row
+  }
+}
+
+// ------------------------------------------------------------------------------------- fast rmsnorm_int
+// For proven graphs with i8 rows (ss_shift = ss_init = 0) of a multiple of 16 bytes and at most 1024: one wavefront
+// per row, lane l holds 16 consecutive entries, the sum of squares is v_dot4 of each dword with itself.
+__global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
+                                                           const int* __restrict__ lut, int lut_len, int mult,
+                                                           int shift, long long rows, int cols,
+                                                           int8_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int chunks = cols >> 4;
+  const bool active = lane < chunks;
+  v4i wv = {0, 0, 0, 0};
+  if (active) wv = *reinterpret_cast<const v4i*>(w + 16 * lane);
+  for (long long row = (long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6); row < rows;
+       row += (long long)gridDim.x * R_WAVES) {
+    v4i xv = {0, 0, 0, 0};
+    if (active) xv = *reinterpret_cast<const v4i*>(x + row * cols + 16 * lane);
+    int ss = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[q], xv[q], ss, false);
+    ss = wave_sum32(ss);
+    int k = 0;
+    while (ss >= lut_len) {
+      ss >>= 2;
+      ++k;
+    }
+    const int r = lut[ss];
+    const int sh = shift + k;
+    const int rnd = sh ? (1 << (sh - 1)) : 0;
+    if (active) {
+      unsigned ov[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {
+        const int xwr = sbyte(xv, b) * sbyte(wv, b) * r;        // proven: x w r and x w r M + rnd fit int32
+        const int v = min(max((xwr * mult + rnd) >> sh, -128), 127);
+        ov[b >> 2] |= (unsigned)(v & 255) << (8 * (b & 3));
+      }
+      *reinterpret_cast<v4i*>(out + row * cols + 16 * lane) = v4i{(int)ov[0], (int)ov[1], (int)ov[2], (int)ov[3]};
+    }
+  }
+}
+
+static unsigned row_grid(long long rows, int device_cus) {
+  long long blocks = (rows + R_WAVES - 1) / R_WAVES;
+  const long long cap = (long long)device_cus * 16;            // enough resident waves to cover HBM latency
+  return (unsigned)(blocks < cap ? blocks : cap);
+}
+
 // ---------------------------------------------------------------------------------------------- rmsnorm_int
 // Per row (anvil/semantics.py:164-182): ss = e + sum((x^2 + 2^(c-1)) >> c); (i, k) = rsqrt_index(ss, n);
 // out = requant(x * w * lut[i], M, s + k).
@@ -128,50 +272,91 @@ __global__ __launch_bounds__(R_THREADS) void softmax_kernel(const int8_t* __rest
 
 using namespace anvil;
 
-extern "C" int anvil_rmsnorm_int(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* w, const int32_t* lut,
-                                 int lut_len, int32_t mult, int shift, int ss_shift, int32_t ss_init, int64_t rows,
-                                 int cols, int8_t* out) {
-  if (int r = check_ctx(ctx)) return r;
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* w, const int32_t* lut,
+                                    int lut_len, int32_t mult, int shift, int ss_shift, int32_t ss_init, int64_t rows,
+                                    int cols, int8_t* out, int flags) {
   if (!x || !w || !lut || !out) return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: null pointer");
   if (rows < 0 || cols < 1 || lut_len < 1) return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: bad size");
   if (x_dtype != ANVIL_I8 && x_dtype != ANVIL_I16) return set_error(ANVIL_E_VALUE, "rmsnorm x must be i8 or i16");
   if (shift < 0 || shift > 31) return set_error(ANVIL_E_VALUE, "shift %d outside [0, 31]", shift);
   if (ss_shift < 0 || ss_shift > 30) return set_error(ANVIL_E_VALUE, "ss_shift %d outside [0, 30]", ss_shift);
   if (ss_init < 0) return set_error(ANVIL_E_VALUE, "ss_init %d negative", ss_init);
+  if (flags & ~ANVIL_OP_UNCHECKED) return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: unknown flags %d", flags);
+  if (int r = check_ctx(ctx)) return r;
   if (rows == 0) return ANVIL_OK;
   const long long blocks = (rows + R_WAVES - 1) / R_WAVES;
   if (blocks > (1ll << 31) - 1) return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: too many rows");
-  if (x_dtype == ANVIL_I8)
+  if ((flags & ANVIL_OP_UNCHECKED) && x_dtype == ANVIL_I8 && ss_shift == 0 && ss_init == 0 && cols % 16 == 0 &&
+      cols <= 1024 && al16(x) && al16(w) && al16(out)) {
+    hipLaunchKernelGGL(rmsnorm_fast, dim3(row_grid(rows, ctx->num_cu)), dim3(R_THREADS), 0, ctx->stream,
+                       (const int8_t*)x, w, lut, lut_len, mult, shift, (long long)rows, cols, out);
+  } else if (x_dtype == ANVIL_I8) {
     hipLaunchKernelGGL(rmsnorm_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
                        (const int8_t*)x, w, lut, lut_len, mult, shift, ss_shift, ss_init, (long long)rows, cols, out,
                        ctx->flags);
-  else
+  } else {
     hipLaunchKernelGGL(rmsnorm_kernel<int16_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
                        (const int16_t*)x, w, lut, lut_len, mult, shift, ss_shift, ss_init, (long long)rows, cols,
                        out, ctx->flags);
+  }
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }
 
-extern "C" int anvil_softmax_lut(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int32_t one, int causal,
-                                 int64_t batch, int t1, int t2, void* out, int out_dtype) {
-  if (int r = check_ctx(ctx)) return r;
+extern "C" int anvil_rmsnorm_int(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* w, const int32_t* lut,
+                                 int lut_len, int32_t mult, int shift, int ss_shift, int32_t ss_init, int64_t rows,
+                                 int cols, int8_t* out) {
+  return anvil_rmsnorm_int_ex(ctx, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out, 0);
+}
+
+template <typename TO>
+static void launch_softmax_fast(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int one, int causal,
+                                long long rows, int t1, int t2, TO* out) {
+  const unsigned grid = row_grid(rows, ctx->num_cu);
+  if (t2 <= 1024)
+    hipLaunchKernelGGL((softmax_fast<1, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
+                       t1, t2, out);
+  else if (t2 <= 2048)
+    hipLaunchKernelGGL((softmax_fast<2, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
+                       t1, t2, out);
+  else
+    hipLaunchKernelGGL((softmax_fast<4, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
+                       t1, t2, out);
+}
+
+extern "C" int anvil_softmax_lut_ex(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int32_t one, int causal,
+                                    int64_t batch, int t1, int t2, void* out, int out_dtype, int flags) {
   if (!x || !lut || !out) return set_error(ANVIL_E_VALUE, "anvil_softmax_lut: null pointer");
   if (batch < 0 || t1 < 1 || t2 < 1) return set_error(ANVIL_E_VALUE, "anvil_softmax_lut: bad size");
   if (out_dtype != ANVIL_I8 && out_dtype != ANVIL_I32)
     return set_error(ANVIL_E_VALUE, "softmax result must be i8 or i32");
   if (one < 1 || (out_dtype == ANVIL_I8 && one > 127))
     return set_error(ANVIL_E_VALUE, "one=%d does not fit the result dtype", one);
+  if (flags & ~ANVIL_OP_UNCHECKED) return set_error(ANVIL_E_VALUE, "anvil_softmax_lut: unknown flags %d", flags);
+  if (int r = check_ctx(ctx)) return r;
   const long long rows = batch * t1;
   if (rows == 0) return ANVIL_OK;
   const long long blocks = (rows + R_WAVES - 1) / R_WAVES;
   if (blocks > (1ll << 31) - 1) return set_error(ANVIL_E_VALUE, "anvil_softmax_lut: too many rows");
-  if (out_dtype == ANVIL_I8)
+  if ((flags & ANVIL_OP_UNCHECKED) && t2 % 16 == 0 && t2 <= 4096 && al16(x) && al16(out)) {
+    if (out_dtype == ANVIL_I8)
+      launch_softmax_fast<int8_t>(ctx, x, lut, one, causal, rows, t1, t2, (int8_t*)out);
+    else
+      launch_softmax_fast<int32_t>(ctx, x, lut, one, causal, rows, t1, t2, (int32_t*)out);
+  } else if (out_dtype == ANVIL_I8) {
     hipLaunchKernelGGL(softmax_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream, x, lut, one,
                        causal, rows, t1, t2, (int8_t*)out, ctx->flags);
-  else
+  } else {
     hipLaunchKernelGGL(softmax_kernel<int32_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream, x, lut, one,
                        causal, rows, t1, t2, (int32_t*)out, ctx->flags);
+  }
   ANVIL_LAUNCHED();
   return ANVIL_OK;
+}
+
+extern "C" int anvil_softmax_lut(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int32_t one, int causal,
+                                 int64_t batch, int t1, int t2, void* out, int out_dtype) {
+  return anvil_softmax_lut_ex(ctx, x, lut, one, causal, batch, t1, t2, out, out_dtype, 0);
 }

@@ -1,5 +1,6 @@
 // Context, memory, timing and error reporting of the anvil_mi355x C ABI.
 #include <cstdarg>
+#include <cstdlib>
 #include <cstring>
 
 #include "common.h"
@@ -67,6 +68,7 @@ int anvil_init(int device, anvil_ctx** out) {
   anvil_ctx* c = new anvil_ctx();
   c->device = device;
   c->num_cu = prop.multiProcessorCount;
+  if (const char* cfg = std::getenv("ANVIL_GEMM_CFG")) c->gemm_cfg = std::atoi(cfg);
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&c->flags, 256);
   if (e == hipSuccess) e = hipMemset(c->flags, 0, 256);

@@ -74,6 +74,26 @@ int anvil_event_elapsed(anvil_ctx* ctx, int slot0, int slot1, float* ms);
 int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
                   int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype);
 
+/* anvil_gemm_i8 with execution flags (same reference op, anvil/semantics.py:95-103):
+ *   ANVIL_GEMM_UNCHECKED    the caller has proven every acc * mult + round fits int32 (the reference quantizer's
+ *                           prove_no_overflow, anvil/frontend/quantize.py:175-253): the epilogue skips the
+ *                           64-bit checks. Without it, a value outside int32 is reported by anvil_sync.
+ *   ANVIL_GEMM_CAUSAL_SKIP  output tiles whose every column exceeds every row (n > m) are not computed: only for a
+ *                           result read by causal softmaxes alone, which never read those entries.
+ *   ANVIL_GEMM_CAUSAL_K     A[m][k] is zero for k > m (a causal softmax output): the K loop of a row tile stops at
+ *                           its last row, which leaves every result unchanged.
+ *   ANVIL_GEMM_MUL24        (with UNCHECKED) every |acc| and |mult| is below 2^23, so the requant product is one
+ *                           24-bit multiply. */
+enum anvil_gemm_flags {
+  ANVIL_GEMM_UNCHECKED = 1,
+  ANVIL_GEMM_CAUSAL_SKIP = 2,
+  ANVIL_GEMM_CAUSAL_K = 4,
+  ANVIL_GEMM_MUL24 = 8
+};
+int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
+                     int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
+                     int flags);
+
 /* rmsnorm_int over rows of `cols` elements (reference anvil/semantics.py:158-182, golden.rmsnorm_int):
  *   ss = ss_init + sum_j ((x_j^2 + 2^(ss_shift-1)) >> ss_shift); (i, k) = rsqrt_index(ss, lut_len);
  *   out_j = clamp_i8((x_j * w_j * lut[i] * mult + 2^(shift+k-1)) >> (shift + k)).
@@ -81,12 +101,28 @@ int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, in
 int anvil_rmsnorm_int(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* w, const int32_t* lut, int lut_len,
                       int32_t mult, int shift, int ss_shift, int32_t ss_init, int64_t rows, int cols, int8_t* out);
 
+/* Execution flags of the row ops' _ex entry points:
+ *   ANVIL_OP_UNCHECKED  the caller has proven every int32 intermediate of the op in range (the reference quantizer's
+ *                       prove_no_overflow, anvil/frontend/quantize.py:175-253); for softmax_lut also that every lut
+ *                       entry is >= 0 and lut[255] >= 1 (so no row sums to zero). The op may then run a kernel
+ *                       without the 64-bit range checks; without the flag, violations are reported by anvil_sync. */
+enum anvil_op_flags { ANVIL_OP_UNCHECKED = 1 };
+
+/* anvil_rmsnorm_int with flags (same reference op, anvil/semantics.py:158-182). */
+int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* w, const int32_t* lut,
+                         int lut_len, int32_t mult, int shift, int ss_shift, int32_t ss_init, int64_t rows, int cols,
+                         int8_t* out, int flags);
+
 /* softmax_lut over the last axis of (batch, t1, t2) (reference anvil/lower/graph_to_tensor.py:352-398,
  * golden.softmax_lut): kept_j = (j <= i) if causal else 1; m = max(-128, max kept x);
  * e_j = lut[x_j - m + 255] (kept) else 0; S = sum e; p_j = (e_j * one + S / 2) / S.
  * x int8 contiguous; lut int32[256]; out ANVIL_I8 (one <= 127) or ANVIL_I32. */
 int anvil_softmax_lut(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int32_t one, int causal, int64_t batch,
                       int t1, int t2, void* out, int out_dtype);
+
+/* anvil_softmax_lut with flags (same reference op, anvil/lower/graph_to_tensor.py:352-398). */
+int anvil_softmax_lut_ex(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int32_t one, int causal, int64_t batch,
+                         int t1, int t2, void* out, int out_dtype, int flags);
 
 /* add_requant (reference anvil/semantics.py:106-115, golden.residual_add):
  *   out = clamp_out((a * ma + b * mb + 2^(shift-1)) >> shift), a and b ANVIL_I8 or ANVIL_I16, n elements. */

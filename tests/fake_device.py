@@ -90,8 +90,9 @@ class FakeDevice:
             return None
 
     # ---------------------------------------------------------------------------------------------- ops
-    def gemm_i8(self, A, Bt, Cp, b0, b1, M, N, K, strides, mult, shift, lut, out_dtype):
-        self.calls.append(("gemm", b0, b1, M, N, K, tuple(strides)))
+    def gemm_i8(self, A, Bt, Cp, b0, b1, M, N, K, strides, mult, shift, lut, out_dtype, flags=0):
+        """Every output is computed, also under the causal flags (a superset of what the kernel writes)."""
+        self.calls.append(("gemm", b0, b1, M, N, K, tuple(strides), flags))
         sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc = strides
         a = self.view(A, "i8", (b0, b1, M, K), (sa0, sa1, lda, 1)).astype(np.int64)
         bt = self.view(Bt, "i8", (b0, b1, N, K), (sb0, sb1, ldb, 1)).astype(np.int64)
@@ -100,8 +101,8 @@ class FakeDevice:
         if out is not None:
             self.store(Cp, out_dtype, (b0, b1, M, N), (sc0, sc1, ldc, 1), out)
 
-    def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out):
-        self.calls.append(("rmsnorm", rows, cols))
+    def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out, flags=0):
+        self.calls.append(("rmsnorm", rows, cols, flags))
         xv = self.view(x, x_dtype, (rows, cols), (cols, 1)).astype(np.int64)
         wv = self.view(w, "i8", (cols,), (1,)).astype(np.int64)
         lv = self.view(lut, "i32", (lut_len,), (1,)).astype(np.int64)
@@ -109,8 +110,8 @@ class FakeDevice:
         if r is not None:
             self.store(out, "i8", (rows, cols), (cols, 1), r)
 
-    def softmax_lut(self, x, lut, one, causal, batch, t1, t2, out, out_dtype):
-        self.calls.append(("softmax", batch, t1, t2))
+    def softmax_lut(self, x, lut, one, causal, batch, t1, t2, out, out_dtype, flags=0):
+        self.calls.append(("softmax", batch, t1, t2, flags))
         xv = self.view(x, "i8", (batch, t1, t2), (t1 * t2, t2, 1)).astype(np.int64)
         lv = self.view(lut, "i32", (256,), (1,)).astype(np.int64)
         r = self._guard(lambda: sem.softmax_lut(xv, lv, one, causal))

@@ -27,14 +27,42 @@ def test_library_exports_every_declared_symbol():
     assert lib.cdll.anvil_version() == 1
 
 
+def test_library_leaves_none_of_its_own_symbols_undefined():
+    """A kernel whose host launch stub was never emitted shows up as an undefined anvil:: symbol."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--undefined-only", "-C", str(rt.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    assert "anvil" not in out, [l for l in out.splitlines() if "anvil" in l][:5]
+
+
 def test_null_context_is_a_value_error():
     lib = rt.library()
     with pytest.raises(ValueError, match="null context"):
         lib.call("anvil_sync", None)
-    with pytest.raises(ValueError, match="null context"):
+    with pytest.raises(ValueError, match="null pointer"):
         lib.call("anvil_gemm_i8", None, None, None, None, 1, 1, 1, 1, 1, None, 1, 0, None, 1)
     with pytest.raises(ValueError):
         lib.call("anvil_init", 0, None)            # null output pointer
+
+
+def test_gemm_argument_validation_precedes_the_device():
+    """Arguments are validated on the host before any device call (non-null dummies are never dereferenced)."""
+    lib = rt.library()
+    st = (C.c_int64 * 9)(*[0, 0, 16, 0, 0, 16, 0, 0, 16])
+    p = C.c_void_p(4096)
+    gemm = lambda *a: lib.call("anvil_gemm_i8_ex", None, p, p, p, *a)   # noqa: E731
+    with pytest.raises(ValueError, match="shift 32"):
+        gemm(1, 1, 16, 16, 16, st, 1, 32, None, 1, 0)
+    with pytest.raises(ValueError, match="non-positive"):
+        gemm(1, 1, 0, 16, 16, st, 1, 3, None, 1, 0)
+    with pytest.raises(ValueError, match="LUT epilogue needs an i8"):
+        gemm(1, 1, 16, 16, 16, st, 1, 3, p, 2, 0)
+    with pytest.raises(ValueError, match="unknown flags"):
+        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 64)
+    with pytest.raises(ValueError, match="exclude each other"):
+        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 6)
+    with pytest.raises(ValueError, match="null context"):
+        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 1)
 
 
 def test_status_codes_map_to_reference_exceptions():

@@ -34,9 +34,22 @@ def test_planner_matches_oracle_on_config1(fake, cfg1):
         if k not in cfg1.consts:
             assert np.array_equal(res.ints[k], v), k
     kinds = [c[0] for c in fake.calls]
-    assert kinds.count("gemm") == 8 and kinds.count("copy") == 1     # only V's transpose is materialised
-    qkv = [c for c in fake.calls if c[0] == "gemm"][:3]
-    assert all(c[1:4] == (1, 1, 96) for c in qkv)                    # batch and T fold into one M = 3 * 32
+    assert kinds.count("gemm") == 8 and kinds.count("copy") == 0     # no layout op is materialised
+    gemms = [c for c in fake.calls if c[0] == "gemm"]
+    assert all(c[1:4] == (1, 1, 96) for c in gemms[:2])              # q, k: batch and T fold into one M = 3 * 32
+    assert gemms[2][1:6] == (1, 3, 64, 32, 64)                       # v is computed transposed, per sequence
+    # proven: unchecked (1), bounds below 2^23 allow the 24-bit requant multiply (8); P.V: causal K limit (4)
+    assert gemms[3][7] == 1 | 8 and gemms[4][7] == 1 | 4 | 8
+
+
+def test_keep_outputs_plan_skips_masked_score_tiles(fake, cfg1):
+    cm = anvil_mi355x.compile(cfg1)
+    x = models.eval_inputs(cfg1.spec, 2, 6)
+    a = cm.run(x, "mi355x", batch=True, keep="outputs").ints["out"]
+    scores = [c for c in fake.calls if c[0] == "gemm"][3]
+    assert scores[7] & 2                                              # causal tile skip when scores are not kept
+    b = cm.run(x, "mi355x", batch=True, keep="all").ints["out"]
+    assert np.array_equal(a, b)
 
 
 @pytest.mark.parametrize("seed", range(12))
@@ -140,5 +153,5 @@ def test_nocopy_strides_agree_with_numpy():
 
 def test_layout_choice_makes_head_merge_free(cfg1):
     cm = anvil_mi355x.driver.CompiledModel(cfg1.module, cfg1.consts)
-    (val, perm), = [(v, p) for v, p in cm.phys.items()]
-    assert val.owner.sym_str == "o" and perm == [1, 0, 2]
+    phys = {v.owner.sym_str: p for v, p in cm.phys.items()}
+    assert phys == {"o": [1, 0, 2], "v": [1, 0]}     # o stored head-merged, v stored transposed for P.V

@@ -83,6 +83,20 @@ def test_config5_gpt2_small_block():
     _config_case(5, sample=[0, 31])
 
 
+@pytest.mark.parametrize("n,sample", [(3, [0, 63]), (5, [7])])
+def test_keep_outputs_fast_path_matches_oracle(n, sample):
+    """keep="outputs" plans skip masked score tiles and bound P.V's K loop: the outputs stay bit-exact."""
+    built, nb = models.config(n)
+    cm = anvil_mi355x.compile(built)
+    x = models.to_float_input(built.spec, built.params, models.eval_inputs(built.spec, nb, 1234))
+    res = cm.run(x, "mi355x", batch=True)
+    xq = cm.quantize_input(x)
+    for i in sample:
+        want = interp.run(built.module, {"x": xq[i:i + 1]}, built.consts, batch=True, fast=True)
+        for s in cm.outputs:
+            assert np.array_equal(res.ints[s][i:i + 1], want.values[s]), (n, i, s)
+
+
 def test_keep_outputs_equals_keep_all_and_runs_repeat():
     built, _ = models.config(1)
     cm = anvil_mi355x.compile(built)

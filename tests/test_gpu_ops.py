@@ -102,23 +102,27 @@ def test_gemm_overflow_flag(dev):
     assert np.array_equal(run_gemm(dev, a, w, m_ok, 10), sem.qmatmul(a, w, m_ok, 10))   # flags were cleared
 
 
-def _rms(dev, x, xdt, w, lut, m, s, c=0, e=0):
+def _rms(dev, x, xdt, w, lut, m, s, c=0, e=0, flags=0):
     rows, d = x.shape
     out = dev.alloc(rows * d)
-    dev.rmsnorm_int(up(dev, x, xdt), xdt, up(dev, w, "i8"), up(dev, lut, "i32"), len(lut), m, s, c, e, rows, d, out)
+    dev.rmsnorm_int(up(dev, x, xdt), xdt, up(dev, w, "i8"), up(dev, lut, "i32"), len(lut), m, s, c, e, rows, d, out,
+                    flags)
     dev.sync()
     return out.download((rows, d), np.int8).astype(np.int64)
 
 
-@pytest.mark.parametrize("d", [8, 64, 256, 768, 1000])
-def test_rmsnorm_i8(dev, d):
+@pytest.mark.parametrize("flags", [0, rt.OP_UNCHECKED])
+@pytest.mark.parametrize("d", [8, 64, 256, 768, 1000, 1024])
+def test_rmsnorm_i8(dev, d, flags):
+    """flags=UNCHECKED selects the one-wave-per-row dot4 kernel where d is a multiple of 16 up to 1024 (the
+    proof's bounds hold for m = 1 and these LUTs); results are the same bits either way."""
     rng = np.random.default_rng([6, d])
     w = rng.integers(-127, 128, d)
     lut, s = Q.rmsnorm_lut(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
     x = np.concatenate([rng.integers(-128, 128, (200, d)), np.full((1, d), -128), np.zeros((1, d), int),
                         np.full((1, d), 127), np.rint(rng.standard_normal((50, d)) * 3).astype(int)])
     want = sem.rmsnorm_int(x, w, lut, 1, s)
-    assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s), want)
+    assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s, flags=flags), want)
 
 
 def test_rmsnorm_i16_wide(dev):
@@ -132,33 +136,44 @@ def test_rmsnorm_i16_wide(dev):
     assert np.array_equal(_rms(dev, x, "i16", w, lut, 1, s, c, e), want)
 
 
-def _softmax(dev, x, lut, one, causal, dtype="i8"):
+def _softmax(dev, x, lut, one, causal, dtype="i8", flags=0):
     *lead, t1, t2 = x.shape
     batch = int(np.prod(lead)) if lead else 1
     out = dev.alloc(x.size * rt.ITEMSIZE[dtype])
-    dev.softmax_lut(up(dev, x, "i8"), up(dev, lut, "i32"), one, causal, batch, t1, t2, out, dtype)
+    dev.softmax_lut(up(dev, x, "i8"), up(dev, lut, "i32"), one, causal, batch, t1, t2, out, dtype, flags)
     dev.sync()
     return out.download(x.shape, rt.NP_DTYPE[dtype]).astype(np.int64)
 
 
+SOFTMAX_SHAPES = [(2, 3, 4, 4), (5, 7, 3), (2, 1, 100, 100), (1, 2, 64, 1024), (3, 33, 65), (1, 17, 16),
+                  (2, 40, 1040), (1, 9, 2048), (1, 5, 4096), (3, 70, 48)]
+
+
+@pytest.mark.parametrize("flags", [0, rt.OP_UNCHECKED])
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("shape", [(2, 3, 4, 4), (5, 7, 3), (2, 1, 100, 100), (1, 2, 64, 1024), (3, 33, 65)])
-def test_softmax(dev, causal, shape):
+@pytest.mark.parametrize("shape", SOFTMAX_SHAPES)
+def test_softmax(dev, causal, shape, flags):
+    """flags=UNCHECKED (exp_lut keeps every intermediate in int32, entries >= 0, lut[255] = 2^E) selects the
+    per-row quotient-table kernel where t2 is a multiple of 16 up to 4096; results are the same bits either way."""
     rng = np.random.default_rng([9, *shape])
     x = rng.integers(-128, 128, shape)
     x[..., 0, :] = -128                          # a row of the minimum value
+    x[..., -1, :] = 127                          # and one of the maximum
     lut = Q.exp_lut(0.05, shape[-1])
     want = sem.softmax_lut(x, lut, 127, causal)
-    assert np.array_equal(_softmax(dev, x, lut, 127, causal), want)
+    assert np.array_equal(_softmax(dev, x, lut, 127, causal, flags=flags), want)
 
 
-def test_softmax_i32_result(dev):
+@pytest.mark.parametrize("flags", [0, rt.OP_UNCHECKED])
+def test_softmax_i32_result(dev, flags):
     rng = np.random.default_rng(10)
-    x = rng.integers(-128, 128, (4, 6, 9))
-    lut = np.round((1 << 14) * np.exp((np.arange(256) - 255) / 24.0)).astype(np.int64)
-    for one in (1, 1000, 4095):
-        want = sem.softmax_lut(x, lut, one, False)
-        assert np.array_equal(_softmax(dev, x, lut, one, False, "i32"), want)
+    for shape in ((4, 6, 9), (2, 5, 32)):
+        x = rng.integers(-128, 128, shape)
+        lut = np.round((1 << 14) * np.exp((np.arange(256) - 255) / 24.0)).astype(np.int64)
+        for one in (1, 1000, 4095):
+            for causal in (False, True):
+                want = sem.softmax_lut(x, lut, one, causal)
+                assert np.array_equal(_softmax(dev, x, lut, one, causal, "i32", flags), want)
 
 
 DT_PAIRS = [("i8", "i8", "i8"), ("i16", "i8", "i16"), ("i8", "i16", "i16"), ("i16", "i16", "i8"), ("i16", "i16", "i16")]
