@@ -149,3 +149,40 @@ def test_fast_matmul_path_equals_literal_path_on_a_block():
     a = interp.run(built.module, {"x": xq}, built.consts, batch=True)
     b = interp.run(built.module, {"x": xq}, built.consts, batch=True, fast=True)
     assert all(np.array_equal(a.values[k], b.values[k]) for k in a.values)
+
+
+_SOFTMAX, _MATMUL = sem.softmax_lut, sem.matmul_i8
+
+
+def _softmax_wrong_mask(x, lut, one, causal):
+    """The oracle's softmax with the causal mask off by one (keeps j < i instead of j <= i, i > 0)."""
+    x = np.asarray(x)
+    if not causal:
+        return _SOFTMAX(x, lut, one, False)
+    out = np.zeros(x.shape, dtype=np.int64)
+    t1 = x.shape[-2]
+    for i in range(t1):
+        kept = max(i, 1)
+        out[..., i, :kept] = _SOFTMAX(x[..., i:i + 1, :kept], lut, one, False)[..., 0, :]
+    return out
+
+
+def _matmul_transposed(a, b, fast=False):
+    """The oracle's matmul reading its right operand transposed."""
+    return _MATMUL(a, np.asarray(b).T if np.asarray(b).shape[0] == np.asarray(b).shape[1] else b, fast)
+
+
+@pytest.mark.parametrize("plant", ["mask", "transpose"])
+def test_planted_oracle_mistakes_fail_the_pins(monkeypatch, plant):
+    """A wrong causal mask or a transposed matmul operand planted in the oracle makes the pins above fail."""
+    if plant == "mask":
+        monkeypatch.setattr(sem, "softmax_lut", _softmax_wrong_mask)
+        with pytest.raises(AssertionError):
+            test_softmax_closed_forms_and_mask()
+    else:
+        monkeypatch.setattr(sem, "matmul_i8", _matmul_transposed)
+        with pytest.raises(AssertionError):
+            a, b = RNG.integers(-128, 128, (4, 4)), RNG.integers(-128, 128, (4, 4))
+            brute = np.array([[sum(int(a[i, t]) * int(b[t, j]) for t in range(4)) for j in range(4)]
+                              for i in range(4)])
+            assert np.array_equal(sem.matmul_i8(a, b), brute)
