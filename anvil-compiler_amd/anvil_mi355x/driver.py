@@ -255,7 +255,11 @@ class CompiledModel:
         def dense(v: View, label) -> View:
             return v if v.is_contiguous() else dense_copy(v, label)
 
+        fused = self._attention_chains(keep)
+        skip = {o for s_op, sm in fused.values() for o in (s_op, sm)}
         for op in self.ops:
+            if op in skip:
+                continue
             r = op.results[0]
             t = g.qt(r)
             label = op.sym_str or op.name.split(".")[-1]
@@ -279,8 +283,14 @@ class CompiledModel:
                 views[r] = v
                 continue
             out_dims = (*lead(r), *t.dims)
+            if op in fused:
+                views[r] = self._plan_attention(P, op, *fused[op], views, nb, label, dense, step, keep)
+                continue
             if isinstance(op, (g.QMatmulOp, g.QLinearOp)):
                 views[r] = self._plan_matmul(P, op, views, out_dims, label, dense, step, keep)
+                continue
+            if isinstance(op, g.SoftmaxLutOp):
+                views[r] = self._plan_softmax(P, op, views, out_dims, label, dense, step)
                 continue
             out = P.dense(out_dims, t.dtype, label)
             views[r] = out
@@ -292,15 +302,6 @@ class CompiledModel:
                 step(label, _call_ptrs, dev.rmsnorm_int, [x, g.qt(op.x).dtype, w, lut, lut.size, int(op.M),
                                                           int(op.s), op.ss_shift_int, op.ss_init_int, rows,
                                                           x.dims[-1], out, rt.OP_UNCHECKED if self.proven else 0])
-            elif isinstance(op, g.SoftmaxLutOp):
-                x = dense(views[op.x], label + ".x")
-                lut = dense(views[op.lut], label + ".lut")
-                t1, t2 = x.dims[-2], x.dims[-1]
-                batch = math.prod(x.dims[:-2])
-                table = self._const_array(op.lut)
-                sure = self.proven and table is not None and table.min() >= 0 and table[-1] >= 1
-                step(label, _call_ptrs, dev.softmax_lut, [x, lut, int(op.one), bool(op.causal), batch, t1, t2, out,
-                                                          t.dtype, rt.OP_UNCHECKED if sure else 0])
             elif isinstance(op, g.AddRequantOp):
                 a = dense(views[op.a], label + ".a")
                 b = dense(views[op.b], label + ".b")
@@ -328,6 +329,99 @@ class CompiledModel:
                 raise NotImplementedError(op.name)
         return P
 
+    def _softmax_lut_ok(self, op) -> bool:
+        """The exp LUT is a const with every entry >= 0 and lut[255] >= 1: no row can sum to zero."""
+        table = self._const_array(op.lut)
+        return table is not None and table.size == 256 and table.min() >= 0 and table[-1] >= 1
+
+    def _plan_softmax(self, P, op, views, out_dims, label, dense, step):
+        t = g.qt(op.result)
+        out = P.dense(out_dims, t.dtype, label)
+        x = dense(views[op.x], label + ".x")
+        lut = dense(views[op.lut], label + ".lut")
+        t1, t2 = x.dims[-2], x.dims[-1]
+        batch = math.prod(x.dims[:-2])
+        sure = self.proven and self._softmax_lut_ok(op)
+        step(label, _call_ptrs, self.dev.softmax_lut, [x, lut, int(op.one), bool(op.causal), batch, t1, t2, out,
+                                                       t.dtype, rt.OP_UNCHECKED if sure else 0])
+        return out
+
+    def _attention_chains(self, keep) -> dict:
+        """{P.V matmul: (scores matmul, softmax)} for every chain qmatmul -> softmax_lut -> qmatmul whose scores and
+        probabilities are read by nothing else and not returned, in a proven graph with int8 values throughout, a
+        square (T x T) score matrix with T a multiple of 32 up to 1024 and one head dim of 16, 32, 64 or 128: the
+        chains anvil_attention_i8 evaluates without materialising scores or p."""
+        if keep != "outputs" or not self.proven:
+            return {}
+        found = {}
+        for o_op in self.ops:
+            if not isinstance(o_op, g.QMatmulOp) or o_op.lut is not None or g.qt(o_op.result).dtype != "i8":
+                continue
+            sm = o_op.a.owner
+            if not isinstance(sm, g.SoftmaxLutOp) or g.qt(sm.result).dtype != "i8" or not 1 <= int(sm.one) <= 127:
+                continue
+            s_op = sm.x.owner
+            if (not isinstance(s_op, g.QMatmulOp) or s_op.lut is not None or g.qt(s_op.result).dtype != "i8"
+                    or not self._softmax_lut_ok(sm)):
+                continue
+            if any(v in self.output_values or v in self.is_const or self.users.get(v, []) != [u]
+                   for v, u in ((s_op.result, sm), (sm.result, o_op))):
+                continue
+            sd, od = g.qt(s_op.result).dims, g.qt(o_op.result).dims
+            T, D = sd[-1], g.qt(s_op.a).dims[-1]
+            if sd[-2] != T or T % 32 or T > 1024 or D not in (16, 32, 64, 128) or od[-1] != D or od[-2] != T:
+                continue
+            found[o_op] = (s_op, sm)
+        return found
+
+    def _plan_attention(self, P, o_op, s_op, sm, views, nb, label, dense, step, keep):
+        """One anvil_attention_i8 launch for a fused chain, or the three ops when the operand views do not fit it."""
+        n = len(g.qt(o_op.result).dims) + 1
+        qa = views[s_op.a]
+        kb = views[s_op.b].permute(_swap_last2(n))           # key rows (..., T, d)
+        vb = views[o_op.b].permute(_swap_last2(n))           # V^T rows (..., d, T)
+        out = self._alloc_result(P, o_op, (nb, *g.qt(o_op.result).dims), label)
+        vs = [qa, kb, vb, out]
+        lead = out.dims[:-2]
+        idx = [i for i, d in enumerate(lead) if d != 1]
+        fits = (all(len(v.dims) == n and v.dims[:-2] == lead and v.strides[-1] == 1 for v in vs)
+                and len(idx) <= 2)
+        if fits:
+            idx = [None] * (2 - len(idx)) + idx
+            strides = []
+            for v in vs:
+                strides += [0 if i is None else v.strides[i] for i in idx] + [v.strides[-2]]
+            offs = [v.offset for v in vs]
+            fits = (all(st % 16 == 0 for st in strides[:9]) and all(st % 4 == 0 for st in strides[9:])
+                    and all(o % 16 == 0 for o in offs[:3]) and offs[3] % 4 == 0)
+        if not fits:
+            sv = self._plan_matmul(P, s_op, views, (nb, *g.qt(s_op.result).dims), label + ".scores", dense, step,
+                                   keep)
+            views[s_op.result] = sv
+            views[sm.result] = self._plan_softmax(P, sm, views, (nb, *g.qt(sm.result).dims), label + ".p", dense,
+                                                  step)
+            return self._plan_matmul(P, o_op, views, (nb, *g.qt(o_op.result).dims), label, dense, step, keep,
+                                     out=out)
+        b0, b1 = [1 if i is None else lead[i] for i in idx]
+        T, D = qa.dims[-2], qa.dims[-1]
+        flags = rt.OP_UNCHECKED
+        if self.acc_bounds.get(s_op.result, 1 << 31) < (1 << 23) and abs(int(s_op.M)) < (1 << 23):
+            flags |= rt.ATTN_S24
+        step(label, _call_attention, self.dev, qa, kb, vb, out, b0, b1, T, D, strides, s_op, sm, o_op,
+             views[sm.lut], flags)
+        return out
+
+    def _alloc_result(self, P, op, out_dims, label):
+        """Dense storage of a matmul result in its chosen physical order, viewed in the logical order."""
+        t = g.qt(op.result)
+        perm = self.phys.get(op.result)
+        if perm is None:
+            return P.dense(out_dims, t.dtype, label)
+        k = 0 if op.result in self.is_const else 1
+        pfull = list(range(k)) + [p + k for p in perm]
+        st = P.dense([out_dims[i] for i in pfull], t.dtype, label)
+        return st.permute([pfull.index(i) for i in range(len(pfull))])
+
     def _bt_const(self, op):
         """A const right operand (K, N) stored once transposed (N, K) so its K dim is contiguous."""
         key = op.b
@@ -352,19 +446,14 @@ class CompiledModel:
         op = value.owner
         return op.value if op.value is not None else self.consts[op.sym_str]
 
-    def _plan_matmul(self, P, op, views, out_dims, label, dense, step, keep):
+    def _plan_matmul(self, P, op, views, out_dims, label, dense, step, keep, out=None):
         t = g.qt(op.result)
         M, N = out_dims[-2], out_dims[-1]
         K = g.qt(op.a).dims[-1]
         # result storage: dense in the chosen physical order, logical view by permuting back
         perm = self.phys.get(op.result)
-        if perm is not None:
-            k = 0 if op.result in self.is_const else 1
-            pfull = list(range(k)) + [p + k for p in perm]
-            st = P.dense([out_dims[i] for i in pfull], t.dtype, label)
-            out = st.permute([pfull.index(i) for i in range(len(pfull))])
-        else:
-            out = P.dense(out_dims, t.dtype, label)
+        if out is None:
+            out = self._alloc_result(P, op, out_dims, label)
         swapped = perm is not None and perm == _swap_last2(len(perm))
         # A rows: (lead..., M, K) with K contiguous
         a = views[op.a]
@@ -619,6 +708,10 @@ def _work(fn, args):
         nb = b0 * b1
         b_batches = nb if (strides[3] or strides[4]) else 1
         return "gemm", 2 * nb * M * N * K, nb * M * K + b_batches * N * K + nb * M * N * isz[dt]
+    if fn is _call_attention:
+        _, q, k, v, o, b0, b1, T, D = args[:9]
+        nb = b0 * b1
+        return "attention", 4 * nb * T * T * D, 4 * nb * T * D + 1024
     if fn is _copy_view:
         src = args[1]
         return "copy", 0, 2 * src.size * src.itemsize
@@ -642,6 +735,12 @@ def _work(fn, args):
 def _call_gemm(dev, a: View, bt: View, c: View, b0, b1, M, N, K, strides, op, lut, out_dtype, flags=0):
     dev.gemm_i8(a.ptr, bt.ptr, c.ptr, b0, b1, M, N, K, strides, int(op.M), int(op.s),
                 None if lut is None else lut.ptr, out_dtype, flags)
+
+
+def _call_attention(dev, q: View, k: View, v: View, o: View, b0, b1, T, D, strides, s_op, sm, o_op, lut: View,
+                    flags):
+    dev.attention_i8(q.ptr, k.ptr, v.ptr, o.ptr, b0, b1, T, D, strides, int(s_op.M), int(s_op.s), lut.ptr,
+                     int(sm.one), bool(sm.causal), int(o_op.M), int(o_op.s), flags)
 
 
 def _swap_last2(n):

@@ -29,8 +29,8 @@ _ERRORS = {1: ValueError, 2: OverflowError, 3: ZeroDivisionError, 4: RuntimeErro
 
 # anvil_gemm_i8_ex flags (include/anvil_mi355x.h)
 GEMM_UNCHECKED, GEMM_CAUSAL_SKIP, GEMM_CAUSAL_K, GEMM_MUL24 = 1, 2, 4, 8
-# anvil_rmsnorm_int_ex / anvil_softmax_lut_ex flags
-OP_UNCHECKED = 1
+# anvil_rmsnorm_int_ex / anvil_softmax_lut_ex / anvil_attention_i8 flags
+OP_UNCHECKED, ATTN_S24 = 1, 2
 
 _p, _i, _i64, _i32, _sz, _f64 = C.c_void_p, C.c_int, C.c_int64, C.c_int32, C.c_size_t, C.c_double
 # symbol -> argtypes (restype int for all but anvil_last_error), in include/anvil_mi355x.h order
@@ -53,6 +53,7 @@ SIGNATURES = {
     "anvil_rmsnorm_int_ex": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p, _i],
     "anvil_softmax_lut": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i],
     "anvil_softmax_lut_ex": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i, _i],
+    "anvil_attention_i8": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p, _i32, _i, _p, _i32, _i, _i32, _i, _i],
     "anvil_add_requant": [_p, _p, _i, _p, _i, _i32, _i32, _i, _i64, _p, _i],
     "anvil_lut_i8": [_p, _p, _p, _i64, _p],
     "anvil_lut_mul": [_p, _p, _p, _p, _i32, _i, _i64, _p],
@@ -190,6 +191,12 @@ class Device:
     def softmax_lut(self, x, lut, one, causal, batch, t1, t2, out, out_dtype, flags=0):
         self.lib.call("anvil_softmax_lut_ex", self.ctx, C.c_void_p(_ptr(x)), C.c_void_p(_ptr(lut)), int(one),
                       int(bool(causal)), batch, t1, t2, C.c_void_p(_ptr(out)), DTYPE_CODE[out_dtype], int(flags))
+
+    def attention_i8(self, Q, K, Vt, O, b0, b1, T, D, strides, ms, ss, lut, one, causal, mo, so, flags):
+        st = (C.c_int64 * 12)(*[int(s) for s in strides])
+        self.lib.call("anvil_attention_i8", self.ctx, C.c_void_p(_ptr(Q)), C.c_void_p(_ptr(K)), C.c_void_p(_ptr(Vt)),
+                      C.c_void_p(_ptr(O)), b0, b1, T, D, st, int(ms), ss, C.c_void_p(_ptr(lut)), int(one),
+                      int(bool(causal)), int(mo), so, int(flags))
 
     def add_requant(self, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype):
         self.lib.call("anvil_add_requant", self.ctx, C.c_void_p(_ptr(a)), DTYPE_CODE[a_dtype], C.c_void_p(_ptr(b)),

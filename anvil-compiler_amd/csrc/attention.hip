@@ -1,0 +1,348 @@
+// Fused attention chain for proven graphs whose scores and probabilities are not returned:
+//
+//   scores = qmatmul(qh, kT, M_s, s_s)          (anvil/semantics.py:95-103, int8 result)
+//   p      = softmax_lut(scores, lut, one)      (anvil/lower/graph_to_tensor.py:352-398, int8 result)
+//   o      = qmatmul(p, vh, M_o, s_o)           (int8 result)
+//
+// computed per (batch, head) without writing scores or p to memory, bit-exact with the three ops. The reference
+// lowers softmax_lut in three stages (row max, exp sum, normalise); the same three stages run here over score rows
+// held in registers. Nothing is approximated: the LUT softmax is not invariant under rescaling, which rules out an
+// online (single-pass) softmax.
+//
+// Workgroup: 4 waves on 32 query rows q0 .. q0 + 31; wave w takes the 32-key tiles w, w + 4, w + 8, ... up to the
+// causal diagonal, so the waves share the row's keys evenly and each holds at most T / 128 tiles of scores.
+//   1. S = Q K^T per tile on v_mfma_i32_32x32x32_i8, requantised to int8 and kept packed in registers: lane l holds
+//      row q0 + l % 32 and, of each tile, the keys 8 g + 4 (l / 32) + e (g, e = 0..3) in dword g, byte e. Partial
+//      row maxima (init -128, kept keys only) meet in LDS.
+//   2. Partial sums of lut[s - max + 255] (lut staged in LDS) meet in LDS.
+//   3. p = (lut[d] one + S // 2) // S, d = s - max + 255, by an exact multiply-shift division (the divisor is fixed
+//      per row; Granlund and Montgomery, "Division by invariant integers using multiplication", 1994, thm 4.2: for
+//      2^(l-1) < S <= 2^l and m = ceil(2^(31+l) / S), floor(n / S) = floor(n m / 2^(31+l)) for 0 <= n < 2^31;
+//      lut[d] one is tabled in LDS once per workgroup). O_w = P V over the wave's tiles on MFMA, P straight from
+//      registers: the MFMA's K order only has to agree between its two operands, so the V fragment is read in the
+//      packed P's key order (dwords 2 g + l / 32 of each 32-key group).
+//   4. The four partial O tiles (int32) are summed through LDS; o = clamp((O M_o + rnd(s_o)) >> s_o), 4-byte
+//      stores.
+// Every product is proven to fit int32 (prove_no_overflow), so the requants run in 32 bits; with S24 the score
+// requant multiply is one 24-bit multiply-add (|acc|, |M_s| < 2^23).
+#include <utility>
+
+#include "common.h"
+
+namespace anvil {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+struct AttnArgs {
+  const int8_t* Q;
+  const int8_t* K;
+  const int8_t* V;     // V^T rows: (d, T) per (batch, head), keys contiguous
+  int8_t* O;
+  int batch1, T, D;
+  long long sq0, sq1, ldq, sk0, sk1, ldk, sv0, sv1, ldv, so0, so1, ldo;
+  int ms, ss, rnds;    // scores requant
+  const int* lut;
+  int one, causal;
+  int mo, so, rndo;    // output requant
+  int nqt;             // query tiles of 32 rows per head
+};
+
+constexpr int A_THREADS = 256;
+
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, expanded at compile time: register arrays indexed by i stay in
+// registers (a loop the unroller declines would index them dynamically, through scratch).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+__device__ __forceinline__ int sbyte(unsigned v, int e) { return (int)(int8_t)(v >> (8 * e)); }
+
+// low bytes of four ints -> one dword (three v_perm_b32)
+__device__ __forceinline__ unsigned pack4(int v0, int v1, int v2, int v3) {
+  const unsigned t01 = __builtin_amdgcn_perm((unsigned)v1, (unsigned)v0, 0x0c0c0400u);
+  const unsigned t23 = __builtin_amdgcn_perm((unsigned)v3, (unsigned)v2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+}
+
+// One 16-byte chunk of a K-contiguous operand row; zero past the head dim.
+template <int D>
+__device__ __forceinline__ v4i chunk16(const int8_t* row, int chunk) {
+  if (chunk * 16 >= D) return v4i{0, 0, 0, 0};
+  return *reinterpret_cast<const v4i*>(row + chunk * 16);
+}
+
+template <int NTW, int D, bool S24>
+__global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
+  constexpr int KS = (D + 31) / 32;         // 32-wide MFMA k-steps over the head dim
+  constexpr int CT = (D + 31) / 32;         // 32-wide output column tiles
+  constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
+  __shared__ int lut_s[256];
+  __shared__ int eone_s[256];               // lut[d] * one
+  __shared__ int red_m[4][32], red_s[4][32];
+  __shared__ __attribute__((aligned(16))) int opart[4][32 * OROW];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, w = t >> 6;
+  const int l32 = lane & 31, half = lane >> 5;
+  {
+    const int v = a.lut[t];
+    lut_s[t] = v;
+    eone_s[t] = v * a.one;                   // proven: lut * one fits int32
+  }
+
+  // XCD-aware order: consecutive logical tiles on one XCD (its L2 holds the head's K and V), each head's query tiles
+  // together, the longest (last) query tile of a head first
+  const int nblk = gridDim.x;
+  int pid = blockIdx.x;
+  if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
+  const int bh = pid / a.nqt;
+  const int qt = a.nqt - 1 - pid % a.nqt;
+  const int q0 = qt * 32;
+  const int b0 = bh / a.batch1, b1 = bh % a.batch1;
+  const int qrow = q0 + l32;
+  const int ntiles = a.causal ? qt + 1 : a.nqt;
+
+  const int8_t* Qr = a.Q + b0 * a.sq0 + b1 * a.sq1 + (long long)qrow * a.ldq;
+  const int8_t* Kb = a.K + b0 * a.sk0 + b1 * a.sk1 + (long long)l32 * a.ldk;
+  const int8_t* Vb = a.V + b0 * a.sv0 + b1 * a.sv1;
+
+  v4i qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qf[ks] = chunk16<D>(Qr, 2 * ks + half);
+
+  // ---- 1. scores of this wave's tiles (w + 4 i), partial row max
+  unsigned sc[NTW][4];
+  int mx = -128;
+  auto kload = [&](int nt, v4i* kf) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = chunk16<D>(Kb + (long long)nt * 32 * a.ldk, 2 * ks + half);
+  };
+  v4i kf[KS];
+  if (w < ntiles) kload(w, kf);
+  static_for<NTW>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const int nt = w + 4 * i;
+    if (nt < ntiles) {
+      v4i kn[KS];
+      if (i + 1 < NTW && nt + 4 < ntiles) kload(nt + 4, kn);
+      v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[ks], qf[ks], acc, 0, 0, 0);
+      int v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int x = S24 ? __mul24(acc[r], a.ms) + a.rnds : acc[r] * a.ms + a.rnds;
+        v[r] = min(max(x >> a.ss, -128), 127);
+      }
+      if (a.causal && nt == ntiles - 1) {             // the diagonal tile: keys past the row are masked
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (nt * 32 + 8 * (r >> 2) + 4 * half + (r & 3) <= qrow) mx = max(mx, v[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = max(mx, v[r]);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) sc[i][g] = pack4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = kn[ks];
+    }
+  });
+  mx = max(mx, __shfl_xor(mx, 32, 64));
+  if (half == 0) red_m[w][l32] = mx;
+  __syncthreads();                                        // also publishes lut_s / eone_s
+  mx = max(max(red_m[0][l32], red_m[1][l32]), max(red_m[2][l32], red_m[3][l32]));
+
+  // ---- 2. partial exp sums over the kept keys
+  const int* erow = lut_s + (255 - mx);                   // erow[s] = lut[s - max + 255]
+  int S = 0;
+  static_for<NTW>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const int nt = w + 4 * i;
+    if (nt < ntiles) {
+      if (a.causal && nt == ntiles - 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int s = sbyte(sc[i][r >> 2], r & 3);
+          const bool kept = nt * 32 + 8 * (r >> 2) + 4 * half + (r & 3) <= qrow;
+          const int e = erow[kept ? s : mx];              // a masked score may exceed the max: read inside the table
+          S += kept ? e : 0;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) S += erow[sbyte(sc[i][r >> 2], r & 3)];
+      }
+    }
+  });
+  S += __shfl_xor(S, 32, 64);
+  if (half == 0) red_s[w][l32] = S;
+  __syncthreads();
+  S = red_s[0][l32] + red_s[1][l32] + red_s[2][l32] + red_s[3][l32];
+
+  // ---- 3. probabilities, O_w = P V over this wave's tiles
+  const unsigned us = (unsigned)S;                       // >= lut[255] >= 1: the row maximum maps to d = 255
+  const int lg = 32 - __clz(us - 1);                     // ceil(log2 S)
+  const unsigned mg = (unsigned)(((1ull << (31 + lg)) + us - 1) / us);
+  const int sh = lg > 0 ? lg - 1 : 0;
+  const unsigned halfS = us >> 1;
+  const int* nrow = eone_s + (255 - mx);                 // nrow[s] = lut[s - max + 255] * one
+  auto quot = [&](int s) -> int {                        // (lut[d] one + S // 2) // S
+    const unsigned n = (unsigned)nrow[s] + halfS;
+    return lg > 0 ? (int)(__umulhi(n, mg) >> sh) : (int)n;
+  };
+  v16i oacc[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) oacc[ct] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  const int8_t* Vr[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) Vr[ct] = Vb + (long long)(32 * ct + l32) * a.ldv;
+  auto vload = [&](int nt, v4i* vf) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      if (32 * ct + l32 >= D) {
+        vf[ct] = v4i{0, 0, 0, 0};
+      } else {
+        const v4i lo = *reinterpret_cast<const v4i*>(Vr[ct] + nt * 32);
+        const v4i hi = *reinterpret_cast<const v4i*>(Vr[ct] + nt * 32 + 16);
+        vf[ct] = half ? v4i{lo[1], lo[3], hi[1], hi[3]} : v4i{lo[0], lo[2], hi[0], hi[2]};
+      }
+    }
+  };
+  v4i vf[CT];
+  if (w < ntiles) vload(w, vf);
+  static_for<NTW>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const int nt = w + 4 * i;
+    if (nt < ntiles) {
+      v4i vn[CT];
+      if (i + 1 < NTW && nt + 4 < ntiles) vload(nt + 4, vn);
+      int p[16];
+      if (a.causal && nt == ntiles - 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int s = sbyte(sc[i][r >> 2], r & 3);
+          const bool kept = nt * 32 + 8 * (r >> 2) + 4 * half + (r & 3) <= qrow;
+          const int q = quot(kept ? s : mx);
+          p[r] = kept ? q : 0;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = quot(sbyte(sc[i][r >> 2], r & 3));
+      }
+      v4i pf;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) pf[g] = (int)pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) oacc[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf[ct], pf, oacc[ct], 0, 0, 0);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) vf[ct] = vn[ct];
+    }
+  });
+
+  // ---- 4. sum the four partial O tiles, requant, store. Lane l holds O_w[row l % 32][32 ct + 8 g + 4 (l / 32) + e].
+  int* op = opart[w] + l32 * OROW;
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<v4i*>(op + 32 * ct + 8 * g + 4 * half) =
+          v4i{oacc[ct][4 * g], oacc[ct][4 * g + 1], oacc[ct][4 * g + 2], oacc[ct][4 * g + 3]};
+  __syncthreads();
+  constexpr int C4 = D / 4;                              // 4-column groups per row
+  int8_t* Ob = a.O + b0 * a.so0 + b1 * a.so1 + (long long)q0 * a.ldo;
+  for (int idx = t; idx < 32 * C4; idx += A_THREADS) {
+    const int row = idx / C4, c = 4 * (idx % C4);
+    v4i sum = *reinterpret_cast<const v4i*>(opart[0] + row * OROW + c);
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) sum += *reinterpret_cast<const v4i*>(opart[ww] + row * OROW + c);
+    int o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = min(max((sum[e] * a.mo + a.rndo) >> a.so, -128), 127);
+    *reinterpret_cast<unsigned*>(Ob + (long long)row * a.ldo + c) = pack4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+template <int NTW, bool S24>
+static void launch_attention(const AttnArgs& a, int D, unsigned grid, hipStream_t s) {
+  switch (D) {
+    case 16: hipLaunchKernelGGL((attention_i8<NTW, 16, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    case 32: hipLaunchKernelGGL((attention_i8<NTW, 32, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((attention_i8<NTW, 64, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    default: hipLaunchKernelGGL((attention_i8<NTW, 128, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+  }
+}
+
+template <bool S24>
+static void launch_attention_nt(const AttnArgs& a, int D, unsigned grid, hipStream_t s) {
+  const int ntw = (a.nqt + 3) / 4;                       // key tiles per wave
+  if (ntw <= 1)
+    launch_attention<1, S24>(a, D, grid, s);
+  else if (ntw <= 2)
+    launch_attention<2, S24>(a, D, grid, s);
+  else if (ntw <= 4)
+    launch_attention<4, S24>(a, D, grid, s);
+  else
+    launch_attention<8, S24>(a, D, grid, s);
+}
+
+}  // namespace anvil
+
+using namespace anvil;
+
+static bool al(const void* p, int n) { return ((uintptr_t)p % n) == 0; }
+
+extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const int8_t* Vt, int8_t* O,
+                                  int batch0, int batch1, int T, int D, const int64_t* strides, int32_t m_s, int s_s,
+                                  const int32_t* lut, int32_t one, int causal, int32_t m_o, int s_o, int flags) {
+  if (!Q || !K || !Vt || !O || !strides || !lut) return set_error(ANVIL_E_VALUE, "anvil_attention_i8: null pointer");
+  if (!(flags & ANVIL_OP_UNCHECKED) || (flags & ~(ANVIL_OP_UNCHECKED | ANVIL_ATTN_S24)))
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: flags must hold ANVIL_OP_UNCHECKED (a proven graph)");
+  if (batch0 < 1 || batch1 < 1 || T < 32 || T % 32 || T > 1024)
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: T=%d must be a multiple of 32 in [32, 1024]", T);
+  if (D != 16 && D != 32 && D != 64 && D != 128)
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: head dim %d not in {16, 32, 64, 128}", D);
+  if (s_s < 0 || s_s > 31 || s_o < 0 || s_o > 31) return set_error(ANVIL_E_VALUE, "shift outside [0, 31]");
+  if (one < 1 || one > 127) return set_error(ANVIL_E_VALUE, "one=%d does not fit int8", one);
+  if ((flags & ANVIL_ATTN_S24) && (m_s >= (1 << 23) || m_s <= -(1 << 23)))
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: ANVIL_ATTN_S24 with |m_s| >= 2^23");
+  const int64_t* st = strides;
+  for (int i = 0; i < 12; ++i)                     // Q, K, V^T: 16-byte loads; O: 4-byte stores
+    if (st[i] < 0 || st[i] % (i < 9 ? 16 : 4))
+      return set_error(ANVIL_E_VALUE, "anvil_attention_i8: stride %d (%lld) not a multiple of %d", i,
+                       (long long)st[i], i < 9 ? 16 : 4);
+  if (!al(Q, 16) || !al(K, 16) || !al(Vt, 16) || !al(O, 4))
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: operand not aligned");
+  if ((long long)batch0 * batch1 * (T / 32) > (1ll << 31) - 1)
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: too many heads");
+  if (int r = check_ctx(ctx)) return r;
+  AttnArgs a;
+  a.Q = Q;
+  a.K = K;
+  a.V = Vt;
+  a.O = O;
+  a.batch1 = batch1;
+  a.T = T;
+  a.D = D;
+  a.sq0 = st[0], a.sq1 = st[1], a.ldq = st[2];
+  a.sk0 = st[3], a.sk1 = st[4], a.ldk = st[5];
+  a.sv0 = st[6], a.sv1 = st[7], a.ldv = st[8];
+  a.so0 = st[9], a.so1 = st[10], a.ldo = st[11];
+  a.ms = m_s, a.ss = s_s, a.rnds = s_s ? 1 << (s_s - 1) : 0;
+  a.lut = lut;
+  a.one = one, a.causal = causal ? 1 : 0;
+  a.mo = m_o, a.so = s_o, a.rndo = s_o ? 1 << (s_o - 1) : 0;
+  a.nqt = T / 32;
+  const unsigned grid = (unsigned)((long long)batch0 * batch1 * a.nqt);
+  if (flags & ANVIL_ATTN_S24)
+    launch_attention_nt<true>(a, D, grid, ctx->stream);
+  else
+    launch_attention_nt<false>(a, D, grid, ctx->stream);
+  ANVIL_LAUNCHED();
+  return ANVIL_OK;
+}

@@ -124,6 +124,22 @@ int anvil_softmax_lut(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int32
 int anvil_softmax_lut_ex(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int32_t one, int causal, int64_t batch,
                          int t1, int t2, void* out, int out_dtype, int flags);
 
+/* The attention chain of a proven graph, fused (reference anvil/interp/graph.py:62-73 evaluating
+ * qmatmul -> softmax_lut -> qmatmul through anvil/semantics.py:95-103 and the three-stage softmax of
+ * anvil/lower/graph_to_tensor.py:352-398), per (b0, b1) of batch0 x batch1 heads:
+ *   scores = clamp_i8((Q K^T * m_s + 2^(s_s-1)) >> s_s);  p = softmax_lut(scores, lut, one, causal) (int8);
+ *   O      = clamp_i8((p V * m_o + 2^(s_o-1)) >> s_o)
+ * bit-exact with the three ops, without writing scores or p. Q, K: (T, D) rows; Vt: V transposed, (D, T) rows;
+ * O: (T, D) rows. strides = {sq0, sq1, ldq, sk0, sk1, ldk, sv0, sv1, ldv, so0, so1, ldo} in elements (bytes): the
+ * first nine and Q, K, Vt multiples of 16, the O strides and O multiples of 4. T a multiple of 32 in [32, 1024];
+ * D in {16, 32, 64, 128}; 1 <= one <= 127; lut int32[256] with every entry >= 0 and lut[255] >= 1.
+ * flags must hold ANVIL_OP_UNCHECKED: the caller has proven every int32 intermediate of the three ops in range;
+ * ANVIL_ATTN_S24 adds that every |Q K^T| and |m_s| is below 2^23 (the score requant multiply is then 24-bit). */
+enum anvil_attn_flags { ANVIL_ATTN_S24 = 2 };
+int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const int8_t* Vt, int8_t* O, int batch0,
+                       int batch1, int T, int D, const int64_t* strides, int32_t m_s, int s_s, const int32_t* lut,
+                       int32_t one, int causal, int32_t m_o, int s_o, int flags);
+
 /* add_requant (reference anvil/semantics.py:106-115, golden.residual_add):
  *   out = clamp_out((a * ma + b * mb + 2^(shift-1)) >> shift), a and b ANVIL_I8 or ANVIL_I16, n elements. */
 int anvil_add_requant(anvil_ctx* ctx, const void* a, int a_dtype, const void* b, int b_dtype, int32_t ma, int32_t mb,

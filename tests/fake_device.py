@@ -101,6 +101,23 @@ class FakeDevice:
         if out is not None:
             self.store(Cp, out_dtype, (b0, b1, M, N), (sc0, sc1, ldc, 1), out)
 
+    def attention_i8(self, Q, K, Vt, O, b0, b1, T, D, strides, ms, ss, lut, one, causal, mo, so, flags):
+        """The three ops the fused kernel replaces, over the same strided operands."""
+        self.calls.append(("attention", b0, b1, T, D, tuple(strides), flags))
+        st = strides
+        q = self.view(Q, "i8", (b0, b1, T, D), (st[0], st[1], st[2], 1)).astype(np.int64)
+        k = self.view(K, "i8", (b0, b1, T, D), (st[3], st[4], st[5], 1)).astype(np.int64)
+        vt = self.view(Vt, "i8", (b0, b1, D, T), (st[6], st[7], st[8], 1)).astype(np.int64)
+        lv = self.view(lut, "i32", (256,), (1,)).astype(np.int64)
+
+        def chain():
+            scores = sem.qmatmul(q, np.swapaxes(k, -1, -2), ms, ss)
+            p = sem.softmax_lut(scores, lv, one, causal)
+            return sem.qmatmul(p, np.swapaxes(vt, -1, -2), mo, so)
+        r = self._guard(chain)
+        if r is not None:
+            self.store(O, "i8", (b0, b1, T, D), (st[9], st[10], st[11], 1), r)
+
     def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out, flags=0):
         self.calls.append(("rmsnorm", rows, cols, flags))
         xv = self.view(x, x_dtype, (rows, cols), (cols, 1)).astype(np.int64)

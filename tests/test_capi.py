@@ -76,3 +76,24 @@ def test_no_gpu_here_is_a_runtime_error():
     out = C.c_void_p()
     with pytest.raises((RuntimeError, ValueError)):
         rt.library().call("anvil_init", 0, C.byref(out))
+
+
+def test_attention_argument_validation_precedes_the_device():
+    lib = rt.library()
+    st = (C.c_int64 * 12)(*[64 * 64, 64, 64] * 3 + [64 * 64, 64, 64])
+    p = C.c_void_p(4096)
+    att = lambda T, D, one, flags, s=st: lib.call("anvil_attention_i8", None, p, p, p, p, 1, 1, T, D, s, 1, 3, p,  # noqa: E731
+                                                  one, 1, 1, 3, flags)
+    with pytest.raises(ValueError, match="ANVIL_OP_UNCHECKED"):
+        att(64, 64, 127, 0)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        att(48, 64, 127, 1)
+    with pytest.raises(ValueError, match="head dim"):
+        att(64, 48, 127, 1)
+    with pytest.raises(ValueError, match="does not fit int8"):
+        att(64, 64, 128, 1)
+    bad = (C.c_int64 * 12)(*[64 * 64, 64, 72] + [64 * 64, 64, 64] * 3)
+    with pytest.raises(ValueError, match="stride 2"):
+        att(64, 64, 127, 1, bad)
+    with pytest.raises(ValueError, match="null context"):
+        att(64, 64, 127, 1)

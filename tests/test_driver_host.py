@@ -42,10 +42,28 @@ def test_planner_matches_oracle_on_config1(fake, cfg1):
     assert gemms[3][7] == 1 | 8 and gemms[4][7] == 1 | 4 | 8
 
 
-def test_keep_outputs_plan_skips_masked_score_tiles(fake, cfg1):
+def test_keep_outputs_plan_fuses_attention(fake, cfg1):
+    """Scores and p are not returned with keep="outputs": QK^T, softmax and P.V become one fused launch over the
+    strided q, k, v^T and head-merged o buffers."""
     cm = anvil_mi355x.compile(cfg1)
     x = models.eval_inputs(cfg1.spec, 2, 6)
+    a = cm.run(x, "mi355x", batch=True, keep="outputs")
+    kinds = [c[0] for c in fake.calls]
+    assert kinds.count("attention") == 1 and kinds.count("softmax") == 0 and kinds.count("gemm") == 6
+    att = [c for c in fake.calls if c[0] == "attention"][0]
+    assert att[1:5] == (2, 4, 32, 16)                                 # batch 2 x 4 heads, T 32, head dim 16
+    assert att[5] == (32 * 64, 16, 64, 32 * 64, 16, 64, 64 * 32, 16 * 32, 32, 32 * 64, 16, 64)
+    assert "scores" not in a.ints and "p" not in a.ints
+    b = cm.run(x, "mi355x", batch=True, keep="all").ints["out"]
+    assert np.array_equal(a.ints["out"], b)
+
+
+def test_unproven_keep_outputs_plan_skips_masked_score_tiles(fake, cfg1):
+    """Without the overflow proof the chain is not fused; the scores GEMM still skips tiles no softmax reads."""
+    cm = anvil_mi355x.compile((cfg1.module, cfg1.consts), prove=False)
+    x = models.eval_inputs(cfg1.spec, 2, 6)
     a = cm.run(x, "mi355x", batch=True, keep="outputs").ints["out"]
+    assert "attention" not in [c[0] for c in fake.calls]
     scores = [c for c in fake.calls if c[0] == "gemm"][3]
     assert scores[7] & 2                                              # causal tile skip when scores are not kept
     b = cm.run(x, "mi355x", batch=True, keep="all").ints["out"]
