@@ -97,6 +97,7 @@ class _Plan:
         self.views: dict = {}
         self.steps: list = []          # (label, fn, args)
         self.works: list = []          # per step: (kind, algorithmic int ops, algorithmic HBM bytes)
+        self.fused_adds: set = set()   # add_requant ops computed in a GEMM epilogue
 
     def buf(self, nbytes, name=""):
         b = Buf(nbytes, name)
@@ -257,8 +258,9 @@ class CompiledModel:
 
         fused = self._attention_chains(keep)
         skip = {o for s_op, sm in fused.values() for o in (s_op, sm)}
+        adds = self._residual_fusions(keep)
         for op in self.ops:
-            if op in skip:
+            if op in skip or op in P.fused_adds:
                 continue
             r = op.results[0]
             t = g.qt(r)
@@ -287,7 +289,7 @@ class CompiledModel:
                 views[r] = self._plan_attention(P, op, *fused[op], views, nb, label, dense, step, keep)
                 continue
             if isinstance(op, (g.QMatmulOp, g.QLinearOp)):
-                views[r] = self._plan_matmul(P, op, views, out_dims, label, dense, step, keep)
+                views[r] = self._plan_matmul(P, op, views, out_dims, label, dense, step, keep, add=adds.get(op))
                 continue
             if isinstance(op, g.SoftmaxLutOp):
                 views[r] = self._plan_softmax(P, op, views, out_dims, label, dense, step)
@@ -446,7 +448,33 @@ class CompiledModel:
         op = value.owner
         return op.value if op.value is not None else self.consts[op.sym_str]
 
-    def _plan_matmul(self, P, op, views, out_dims, label, dense, step, keep, out=None):
+    def _residual_fusions(self, keep) -> dict:
+        """{matmul: add_requant} for int8 matmul results y that feed an add_requant of int8 operands with a residual
+        computed earlier in the graph, in a proven graph: the add runs in the GEMM's epilogue (y itself is still
+        written when it is returned or read elsewhere)."""
+        if not self.proven:
+            return {}
+        order = {op: i for i, op in enumerate(self.ops)}
+        found, taken = {}, set()
+        for op in self.ops:
+            if not isinstance(op, (g.QMatmulOp, g.QLinearOp)) or g.qt(op.result).dtype != "i8" or op.result in self.phys:
+                continue
+            for u in self.users.get(op.result, []):
+                if (not isinstance(u, g.AddRequantOp) or u in taken or g.qt(u.result).dtype != "i8"
+                        or g.qt(u.a).dtype != "i8" or g.qt(u.b).dtype != "i8" or u.a is u.b):
+                    continue
+                other = u.b if u.a is op.result else u.a
+                own = other.owner
+                if other in self.is_const or order.get(own, len(order)) > order[op]:
+                    continue
+                if g.qt(other).dims != g.qt(op.result).dims:
+                    continue
+                found[op] = u
+                taken.add(u)
+                break
+        return found
+
+    def _plan_matmul(self, P, op, views, out_dims, label, dense, step, keep, out=None, add=None):
         t = g.qt(op.result)
         M, N = out_dims[-2], out_dims[-1]
         K = g.qt(op.a).dims[-1]
@@ -492,6 +520,9 @@ class CompiledModel:
             c2 = c.reshape((math.prod(c.dims[:-1]), Nx))
             if r1 is not None and c2 is not None and (r1.strides[-1] == 1 or K == 1):
                 strides = [0, 0, r1.strides[0], 0, 0, rows2.strides[-2], 0, 0, c2.strides[0]]
+                if add is not None and self._plan_fused_add(P, op, add, views, r1, rows2, c2, strides, lut, flags,
+                                                            label, step, keep):
+                    return out
                 step(label, _call_gemm, self.dev, r1, rows2, c2, 1, 1, r1.dims[0], Nx, K, strides, op, lut, t.dtype,
                      flags)
                 return out
@@ -513,6 +544,28 @@ class CompiledModel:
         strides = [sa0, sa1, rows1.strides[-2], sb0, sb1, rows2.strides[-2], sc0, sc1, c.strides[-2]]
         step(label, _call_gemm, self.dev, rows1, rows2, c, b0, b1, Mx, Nx, K, strides, op, lut, t.dtype, flags)
         return out
+
+    def _plan_fused_add(self, P, op, add, views, a2, bt, c2, strides, lut, flags, label, step, keep) -> bool:
+        """Plan y = op(...) with add_requant(y, R) in its epilogue over the 2-D (rows, N) views; False when the views
+        do not allow it (the add is then planned as its own launch)."""
+        rows, N = c2.dims
+        K = a2.dims[-1]
+        y_first = add.a is op.result
+        other = add.b if y_first else add.a
+        rv = views[other].reshape((rows, N))
+        ok16 = lambda v: v % 16 == 0                                         # noqa: E731
+        if (rv is None or rv.strides[-1] != 1 or K % 16 or not ok16(a2.strides[0]) or not ok16(bt.strides[-2])
+                or not ok16(a2.offset) or not ok16(bt.offset) or 256 * max(a2.strides[0], bt.strides[-2]) >= 1 << 31):
+            return False
+        d = P.dense((rows, N), "i8", (add.sym_str or "add"))
+        store_y = keep == "all" or op.result in self.output_values or len(self.users.get(op.result, [])) > 1
+        ma, mb = (int(add.Mb), int(add.Ma)) if y_first else (int(add.Ma), int(add.Mb))   # (residual, y)
+        rstrides = [0, 0, rv.strides[0], 0, 0, d.strides[0]]
+        step(label, _call_gemm_add, self.dev, a2, bt, c2 if store_y else None, rows, N, K, strides, op, lut, rv, ma,
+             mb, int(add.s), d, rstrides, flags)
+        views[add.result] = d.reshape(tuple(views[other].dims))
+        P.fused_adds.add(add)
+        return True
 
     def _causal_skip_ok(self, op, keep) -> bool:
         """Scores read only by causal softmaxes, and not returned: tiles above the diagonal are never read."""
@@ -708,6 +761,9 @@ def _work(fn, args):
         nb = b0 * b1
         b_batches = nb if (strides[3] or strides[4]) else 1
         return "gemm", 2 * nb * M * N * K, nb * M * K + b_batches * N * K + nb * M * N * isz[dt]
+    if fn is _call_gemm_add:
+        _, a, bt, c, M, N, K = args[:7]
+        return "gemm", 2 * M * N * K, M * K + N * K + M * N * (3 if c is not None else 2)
     if fn is _call_attention:
         _, q, k, v, o, b0, b1, T, D = args[:9]
         nb = b0 * b1
@@ -741,6 +797,12 @@ def _call_attention(dev, q: View, k: View, v: View, o: View, b0, b1, T, D, strid
                     flags):
     dev.attention_i8(q.ptr, k.ptr, v.ptr, o.ptr, b0, b1, T, D, strides, int(s_op.M), int(s_op.s), lut.ptr,
                      int(sm.one), bool(sm.causal), int(o_op.M), int(o_op.s), flags)
+
+
+def _call_gemm_add(dev, a: View, bt: View, c, M, N, K, strides, op, lut, r: View, ma, mb, shift2, d: View, rstrides,
+                   flags):
+    dev.gemm_i8_add(a.ptr, bt.ptr, None if c is None else c.ptr, 1, 1, M, N, K, strides, int(op.M), int(op.s),
+                    None if lut is None else lut.ptr, r.ptr, ma, mb, shift2, d.ptr, rstrides, flags)
 
 
 def _swap_last2(n):

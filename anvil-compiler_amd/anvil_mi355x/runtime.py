@@ -49,6 +49,7 @@ SIGNATURES = {
     "anvil_event_elapsed": [_p, _i, _i, C.POINTER(C.c_float)],
     "anvil_gemm_i8": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i],
     "anvil_gemm_i8_ex": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _i],
+    "anvil_gemm_i8_add": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _p, _i32, _i32, _i, _p, _p, _i],
     "anvil_rmsnorm_int": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p],
     "anvil_rmsnorm_int_ex": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p, _i],
     "anvil_softmax_lut": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i],
@@ -182,6 +183,15 @@ class Device:
         self.lib.call("anvil_gemm_i8_ex", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)), C.c_void_p(_ptr(Cp)),
                       batch0, batch1, M, N, K, st, int(mult), shift, C.c_void_p(_ptr(lut) if lut is not None else 0),
                       DTYPE_CODE[out_dtype], int(flags))
+
+    def gemm_i8_add(self, A, Bt, Cp, batch0, batch1, M, N, K, strides, mult, shift, lut, R, ma, mb, shift2, D,
+                    rstrides, flags):
+        st = (C.c_int64 * 9)(*[int(s) for s in strides])
+        rs = (C.c_int64 * 6)(*[int(s) for s in rstrides])
+        self.lib.call("anvil_gemm_i8_add", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)),
+                      C.c_void_p(_ptr(Cp) if Cp is not None else 0), batch0, batch1, M, N, K, st, int(mult), shift,
+                      C.c_void_p(_ptr(lut) if lut is not None else 0), C.c_void_p(_ptr(R)), int(ma), int(mb), shift2,
+                      C.c_void_p(_ptr(D)), rs, int(flags))
 
     def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out, flags=0):
         self.lib.call("anvil_rmsnorm_int_ex", self.ctx, C.c_void_p(_ptr(x)), DTYPE_CODE[x_dtype], C.c_void_p(_ptr(w)),

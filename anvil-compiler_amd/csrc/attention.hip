@@ -83,17 +83,17 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   constexpr int CT = (D + 31) / 32;         // 32-wide output column tiles
   constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
   __shared__ int lut_s[256];
-  __shared__ int eone_s[256];               // lut[d] * one
+  __shared__ unsigned eone_s[256];          // 2 lut[d] one (< 2^32: lut * one fits int32)
   __shared__ int red_m[4][32], red_s[4][32];
   __shared__ __attribute__((aligned(16))) int opart[4][32 * OROW];
 
   const int t = threadIdx.x;
-  const int lane = t & 63, w = t >> 6;
+  const int lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int l32 = lane & 31, half = lane >> 5;
   {
     const int v = a.lut[t];
     lut_s[t] = v;
-    eone_s[t] = v * a.one;                   // proven: lut * one fits int32
+    eone_s[t] = 2u * (unsigned)(v * a.one);  // proven: lut * one fits int32
   }
 
   // XCD-aware order: consecutive logical tiles on one XCD (its L2 holds the head's K and V), each head's query tiles
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
       if (a.causal && nt == ntiles - 1) {             // the diagonal tile: keys past the row are masked
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (nt * 32 + 8 * (r >> 2) + 4 * half + (r & 3) <= qrow) mx = max(mx, v[r]);
+          mx = max(mx, nt * 32 + 8 * (r >> 2) + 4 * half + (r & 3) <= qrow ? v[r] : -128);
       } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = max(mx, v[r]);
@@ -186,15 +186,14 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   S = red_s[0][l32] + red_s[1][l32] + red_s[2][l32] + red_s[3][l32];
 
   // ---- 3. probabilities, O_w = P V over this wave's tiles
+  // floor(n / S) = floor(n m / 2^(31+lg)) = mulhi(2 n, m) >> lg for n < 2^31, with no case for S = 1
   const unsigned us = (unsigned)S;                       // >= lut[255] >= 1: the row maximum maps to d = 255
   const int lg = 32 - __clz(us - 1);                     // ceil(log2 S)
   const unsigned mg = (unsigned)(((1ull << (31 + lg)) + us - 1) / us);
-  const int sh = lg > 0 ? lg - 1 : 0;
-  const unsigned halfS = us >> 1;
-  const int* nrow = eone_s + (255 - mx);                 // nrow[s] = lut[s - max + 255] * one
+  const unsigned half2 = us & ~1u;                       // 2 (S // 2)
+  const unsigned* nrow = eone_s + (255 - mx);            // nrow[s] = 2 lut[s - max + 255] one
   auto quot = [&](int s) -> int {                        // (lut[d] one + S // 2) // S
-    const unsigned n = (unsigned)nrow[s] + halfS;
-    return lg > 0 ? (int)(__umulhi(n, mg) >> sh) : (int)n;
+    return (int)(__umulhi(nrow[s] + half2, mg) >> lg);
   };
   v16i oacc[CT];
 #pragma unroll

@@ -94,6 +94,17 @@ int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C,
                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
                      int flags);
 
+/* A qlinear / qmatmul whose int8 result y feeds an add_requant with an int8 residual R, fused in the GEMM's
+ * epilogue (reference anvil/semantics.py:95-103, then add_requant :106-115):
+ *   y = clamp_i8((acc * mult + 2^(shift-1)) >> shift) [-> lut];  D = clamp_i8((R * ma + y * mb + 2^(shift2-1)) >> shift2)
+ * D (and R) have C's dims; rstrides = {sr0, sr1, ldr, sd0, sd1, ldd}. y is also written to C unless C is NULL.
+ * flags must hold ANVIL_GEMM_UNCHECKED (every intermediate of both ops proven in int32; ANVIL_GEMM_MUL24 allowed, no
+ * causal mode); A and Bt 16-byte aligned with K and their row strides multiples of 16. */
+int anvil_gemm_i8_add(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, int8_t* C, int batch0, int batch1, int M,
+                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut,
+                      const int8_t* R, int32_t ma, int32_t mb, int shift2, int8_t* D, const int64_t* rstrides,
+                      int flags);
+
 /* rmsnorm_int over rows of `cols` elements (reference anvil/semantics.py:158-182, golden.rmsnorm_int):
  *   ss = ss_init + sum_j ((x_j^2 + 2^(ss_shift-1)) >> ss_shift); (i, k) = rsqrt_index(ss, lut_len);
  *   out_j = clamp_i8((x_j * w_j * lut[i] * mult + 2^(shift+k-1)) >> (shift + k)).

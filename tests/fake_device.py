@@ -101,6 +101,26 @@ class FakeDevice:
         if out is not None:
             self.store(Cp, out_dtype, (b0, b1, M, N), (sc0, sc1, ldc, 1), out)
 
+    def gemm_i8_add(self, A, Bt, Cp, b0, b1, M, N, K, strides, mult, shift, lut, R, ma, mb, shift2, D, rstrides,
+                    flags):
+        """y = qmatmul epilogue, D = add_requant of the residual R (times ma) and y (times mb)."""
+        self.calls.append(("gemm_add", b0, b1, M, N, K, tuple(strides), flags, Cp is not None))
+        sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc = strides
+        sr0, sr1, ldr, sd0, sd1, ldd = rstrides
+        a = self.view(A, "i8", (b0, b1, M, K), (sa0, sa1, lda, 1)).astype(np.int64)
+        bt = self.view(Bt, "i8", (b0, b1, N, K), (sb0, sb1, ldb, 1)).astype(np.int64)
+        lt = None if lut is None else self.view(lut, "i8", (256,), (1,)).astype(np.int64)
+        r = self.view(R, "i8", (b0, b1, M, N), (sr0, sr1, ldr, 1)).astype(np.int64)
+
+        def both():
+            y = sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, "i8")
+            return y, sem.add_requant(r, y, ma, mb, shift2, "i8")
+        out = self._guard(both)
+        if out is not None:
+            if Cp is not None:
+                self.store(Cp, "i8", (b0, b1, M, N), (sc0, sc1, ldc, 1), out[0])
+            self.store(D, "i8", (b0, b1, M, N), (sd0, sd1, ldd, 1), out[1])
+
     def attention_i8(self, Q, K, Vt, O, b0, b1, T, D, strides, ms, ss, lut, one, causal, mo, so, flags):
         """The three ops the fused kernel replaces, over the same strided operands."""
         self.calls.append(("attention", b0, b1, T, D, tuple(strides), flags))

@@ -34,7 +34,10 @@ def test_planner_matches_oracle_on_config1(fake, cfg1):
         if k not in cfg1.consts:
             assert np.array_equal(res.ints[k], v), k
     kinds = [c[0] for c in fake.calls]
-    assert kinds.count("gemm") == 8 and kinds.count("copy") == 0     # no layout op is materialised
+    assert kinds.count("copy") == 0                                  # no layout op is materialised
+    # both residual adds run in the epilogues of the y and proj GEMMs; keep="all" still stores y and proj
+    assert kinds.count("gemm") == 6 and kinds.count("gemm_add") == 2 and kinds.count("add") == 0
+    assert all(c[8] for c in fake.calls if c[0] == "gemm_add")
     gemms = [c for c in fake.calls if c[0] == "gemm"]
     assert all(c[1:4] == (1, 1, 96) for c in gemms[:2])              # q, k: batch and T fold into one M = 3 * 32
     assert gemms[2][1:6] == (1, 3, 64, 32, 64)                       # v is computed transposed, per sequence
@@ -49,7 +52,8 @@ def test_keep_outputs_plan_fuses_attention(fake, cfg1):
     x = models.eval_inputs(cfg1.spec, 2, 6)
     a = cm.run(x, "mi355x", batch=True, keep="outputs")
     kinds = [c[0] for c in fake.calls]
-    assert kinds.count("attention") == 1 and kinds.count("softmax") == 0 and kinds.count("gemm") == 6
+    assert kinds.count("attention") == 1 and kinds.count("softmax") == 0 and kinds.count("gemm") == 4
+    assert [c[8] for c in fake.calls if c[0] == "gemm_add"] == [False, False]   # y and proj are not returned
     att = [c for c in fake.calls if c[0] == "attention"][0]
     assert att[1:5] == (2, 4, 32, 16)                                 # batch 2 x 4 heads, T 32, head dim 16
     assert att[5] == (32 * 64, 16, 64, 32 * 64, 16, 64, 64 * 32, 16 * 32, 32, 32 * 64, 16, 64)

@@ -279,3 +279,28 @@ def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
         dev.sync()
         got = out.download((B, T, C), np.int8).astype(np.int64)
         assert np.array_equal(got, want), (seed, np.argwhere(got != want)[:5])
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 768, 768), (300, 64, 200), (33, 48, 72), (1024, 256, 384)])
+@pytest.mark.parametrize("store_y", [True, False])
+def test_gemm_with_fused_residual_add(dev, M, K, N, store_y):
+    """anvil_gemm_i8_add: y = qlinear(a, w) [LUT] and D = add_requant(r, y) in one launch, bit-exact with the two ops;
+    N not a multiple of 16 takes the per-byte epilogue."""
+    rng = np.random.default_rng([31, M, K, N, int(store_y)])
+    a, w, r = rng.integers(-128, 128, (M, K)), rng.integers(-128, 128, (K, N)), rng.integers(-128, 128, (M, N))
+    m, s = 3, 16
+    lut = rng.integers(-128, 128, 256) if N == 200 else None
+    ma, mb, s2 = 300, -200, 9
+    y = sem.qmatmul(a, w, m, s, lut)
+    want = sem.add_requant(r, y, ma, mb, s2)
+    c = dev.alloc(M * N) if store_y else None
+    d = dev.alloc(M * N)
+    wt = np.ascontiguousarray(w.T)
+    flags = rt.GEMM_UNCHECKED | rt.GEMM_MUL24
+    dev.gemm_i8_add(up(dev, a, "i8"), up(dev, wt, "i8"), c, 1, 1, M, N, K, [0, 0, K, 0, 0, K, 0, 0, N], m, s,
+                    None if lut is None else up(dev, lut, "i8"), up(dev, r, "i8"), ma, mb, s2, d,
+                    [0, 0, N, 0, 0, N], flags)
+    dev.sync()
+    assert np.array_equal(d.download((M, N), np.int8).astype(np.int64), want)
+    if store_y:
+        assert np.array_equal(c.download((M, N), np.int8).astype(np.int64), y)
