@@ -36,6 +36,9 @@ def main():
     ap.add_argument("--config", type=int, default=5, choices=[1, 3, 4, 5])
     ap.add_argument("--keep", default="outputs", choices=["outputs", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a contiguous 1 GiB device copy: the known-size kernel that scales the FETCH_SIZE / "
+                         "WRITE_SIZE counters behind roofline.traffic")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -45,6 +48,8 @@ def main():
         sys.exit(2)
     if args.steps < 1 or args.warmup < 0:
         sys.exit("bench.py: --steps must be >= 1 and --warmup >= 0")
+    if args.copy_calibration:
+        return copy_calibration()
 
     import numpy as np
 
@@ -102,7 +107,7 @@ def main():
     value = tokens / wall_s
 
     kind, ops, nbytes = plan.works[dom]
-    if kind == "gemm":
+    if kind in ("gemm", "attention"):
         achieved = ops / (dom_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "kernel": steps[dom][0], "achieved": round(achieved, 1), "peak": round(PEAK_INT8_TOPS),
                 "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
@@ -113,14 +118,21 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                 "algorithmic_bytes": nbytes, "avg_us": round(dom_ms * 1e3, 2)}
 
+    roof["traffic"], src = measured_traffic(args.config, args.keep, steps[dom][0])
+    if src:
+        roof["traffic_source"] = src
+
     kernels, g_ops, g_ms = {}, 0, 0.0
     for i, (label, _, _) in enumerate(steps):
         k_, o_, b_ = plan.works[i]
         ms = per[i]
         e = {"kind": k_, "us": round(ms * 1e3, 2)}
-        if k_ == "gemm":
+        if k_ in ("gemm", "attention"):
             e["TOPS"] = round(o_ / (ms * 1e-3) / 1e12, 1)
             e["frac_mfma"] = round(e["TOPS"] / PEAK_INT8_TOPS, 4)
+            if k_ == "attention":                 # MFMA work actually issued: 32-key tiles up to the diagonal
+                e["executed_ops"] = attention_executed_ops(steps[i][2])
+                e["GBs"] = round(b_ / (ms * 1e-3) / 1e9, 1)
             g_ops += o_
             g_ms += ms
         else:
@@ -144,12 +156,58 @@ def main():
                    "layers": spec.layers},
         "device_ms_per_step": round(device_ms / K, 4),
         "gemm": {"TOPS": round(gemm_tops, 1), "frac_of_peak": round(gemm_tops / PEAK_INT8_TOPS, 4),
-                 "ops_per_step": g_ops, "us_per_step": round(g_ms * 1e3, 2)},
+                 "ops_per_step": g_ops, "us_per_step": round(g_ms * 1e3, 2),
+                 "covers": "every qlinear/qmatmul of the step at 2 M N K ops (attention dense T x T); the fused "
+                           "attention kernel's time, softmax included, counts as GEMM time"},
         "roofline": roof,
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def measured_traffic(config, keep, label):
+    """HBM bytes per launch of kernel `label` at this workload, as measured with rocprofv3 FETCH_SIZE and WRITE_SIZE
+    passes (scaled by the copy-kernel factor) and recorded in a profiles/*.md line
+    "bench-traffic: config<N>/<keep> <label> bytes=<B>"; None when no measurement of that kernel is recorded."""
+    import re
+    for f in sorted((ROOT / "profiles").glob("*.md")):
+        for line in f.read_text().splitlines():
+            m = re.match(r"\s*bench-traffic: config(\d+)/(\w+) (\S+) bytes=(\d+)", line)
+            if m and int(m[1]) == config and m[2] == keep and m[3] == label:
+                return int(m[4]), f.name
+    return None, None
+
+
+def copy_calibration():
+    """A contiguous 1 GiB copy on the library's own copy kernel, 5 launches: FETCH_SIZE / WRITE_SIZE per launch
+    against the 1 GiB it must read and write gives the factor that turns those counters into bytes."""
+    from anvil_mi355x import runtime as rt
+    dev = rt.device(0)
+    n = 1 << 30
+    src, dst = dev.alloc(n), dev.alloc(n)
+    dev.zero(src, n)
+    dev.copy_strided(src, dst, 4, [n // 4], [1])
+    dev.sync()
+    dev.record(0)
+    for _ in range(5):
+        dev.copy_strided(src, dst, 4, [n // 4], [1])
+    dev.record(1)
+    dev.sync()
+    ms = dev.elapsed_ms(0, 1) / 5
+    print(json.dumps({"copy_calibration": {"bytes_read": n, "bytes_written": n, "launches": 6,
+                                           "avg_us": round(ms * 1e3, 1), "GBs": round(2 * n / (ms * 1e-3) / 1e9, 1)}}),
+          flush=True)
+
+
+def attention_executed_ops(args):
+    """MFMA ops the fused attention kernel issues: per (batch, head) and 32-row query tile, the 32-key tiles up to the
+    diagonal (all of them without the causal mask), each a 32 x 32 x D QK^T and a 32 x D x 32 P.V."""
+    _, _, _, _, _, b0, b1, T, D = args[:9]
+    causal = bool(args[11].causal)
+    nt = T // 32
+    tiles = nt * (nt + 1) // 2 if causal else nt * nt
+    return 2 * 2 * 32 * 32 * D * tiles * b0 * b1
 
 
 def cpu_baseline(built, xq, cm, plan):
