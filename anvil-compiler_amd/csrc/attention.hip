@@ -15,12 +15,13 @@
 //      row q0 + l % 32 and, of each tile, the keys 8 g + 4 (l / 32) + e (g, e = 0..3) in dword g, byte e. Partial
 //      row maxima (init -128, kept keys only) meet in LDS.
 //   2. Partial sums of lut[s - max + 255] (lut staged in LDS) meet in LDS.
-//   3. p = (lut[d] one + S // 2) // S, d = s - max + 255, by an exact multiply-shift division (the divisor is fixed
-//      per row; Granlund and Montgomery, "Division by invariant integers using multiplication", 1994, thm 4.2: for
-//      2^(l-1) < S <= 2^l and m = ceil(2^(31+l) / S), floor(n / S) = floor(n m / 2^(31+l)) for 0 <= n < 2^31;
-//      lut[d] one is tabled in LDS once per workgroup). O_w = P V over the wave's tiles on MFMA, P straight from
-//      registers: the MFMA's K order only has to agree between its two operands, so the V fragment is read in the
-//      packed P's key order (dwords 2 g + l / 32 of each 32-key group).
+//   3. p = (lut[d] one + S // 2) // S, d = s - max + 255, exactly, in float64 (full rate on CDNA4): with per-row
+//      A = fl(one / S) and B = fl((S // 2) / S + 2^-40), y = fma(lut[d], A, B) is within 2^-45 of n / S + 2^-40
+//      (n = lut[d] one + S // 2 < 2^31, n / S < 128, three roundings of 2^-53 relative), and n / S is either an
+//      integer or at least 1 / S > 2^-31 away from one, so trunc(y) = n // S. The LUT is staged in LDS as doubles.
+//      O_w = P V over the wave's tiles on MFMA, P straight from registers: the MFMA's K order only has to agree
+//      between its two operands, so the V fragment is read in the packed P's key order (dwords 2 g + l / 32 of each
+//      32-key group).
 //   4. The four partial O tiles (int32) are summed through LDS; o = clamp((O M_o + rnd(s_o)) >> s_o), 4-byte
 //      stores.
 // Every product is proven to fit int32 (prove_no_overflow), so the requants run in 32 bits; with S24 the score
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   constexpr int CT = (D + 31) / 32;         // 32-wide output column tiles
   constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
   __shared__ int lut_s[256];
-  __shared__ unsigned eone_s[256];          // 2 lut[d] one (< 2^32: lut * one fits int32)
+  __shared__ double lutd_s[256];            // lut[d] as float64
   __shared__ int red_m[4][32], red_s[4][32];
   __shared__ __attribute__((aligned(16))) int opart[4][32 * OROW];
 
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   {
     const int v = a.lut[t];
     lut_s[t] = v;
-    eone_s[t] = 2u * (unsigned)(v * a.one);  // proven: lut * one fits int32
+    lutd_s[t] = (double)v;
   }
 
   // XCD-aware order: consecutive logical tiles on one XCD (its L2 holds the head's K and V), each head's query tiles
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   });
   mx = max(mx, __shfl_xor(mx, 32, 64));
   if (half == 0) red_m[w][l32] = mx;
-  __syncthreads();                                        // also publishes lut_s / eone_s
+  __syncthreads();                                        // also publishes lut_s / lutd_s
   mx = max(max(red_m[0][l32], red_m[1][l32]), max(red_m[2][l32], red_m[3][l32]));
 
   // ---- 2. partial exp sums over the kept keys
@@ -186,14 +187,12 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   S = red_s[0][l32] + red_s[1][l32] + red_s[2][l32] + red_s[3][l32];
 
   // ---- 3. probabilities, O_w = P V over this wave's tiles
-  // floor(n / S) = floor(n m / 2^(31+lg)) = mulhi(2 n, m) >> lg for n < 2^31, with no case for S = 1
-  const unsigned us = (unsigned)S;                       // >= lut[255] >= 1: the row maximum maps to d = 255
-  const int lg = 32 - __clz(us - 1);                     // ceil(log2 S)
-  const unsigned mg = (unsigned)(((1ull << (31 + lg)) + us - 1) / us);
-  const unsigned half2 = us & ~1u;                       // 2 (S // 2)
-  const unsigned* nrow = eone_s + (255 - mx);            // nrow[s] = 2 lut[s - max + 255] one
+  const double Sd = (double)S;                           // S >= lut[255] >= 1: the row maximum maps to d = 255
+  const double qa = (double)a.one / Sd;
+  const double qb = (double)(S >> 1) / Sd + 0x1p-40;
+  const double* drow = lutd_s + (255 - mx);              // drow[s] = lut[s - max + 255]
   auto quot = [&](int s) -> int {                        // (lut[d] one + S // 2) // S
-    return (int)(__umulhi(nrow[s] + half2, mg) >> lg);
+    return (int)__builtin_fma(drow[s], qa, qb);
   };
   v16i oacc[CT];
 #pragma unroll

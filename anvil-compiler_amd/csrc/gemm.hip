@@ -25,6 +25,8 @@
 //
 // causal = 1: tiles strictly above the diagonal (every n > every m) are skipped (their values are never read);
 // causal = 2: the K loop stops at m0 + BM (A[m][k] = 0 for k > m, e.g. a causal softmax output).
+#include <type_traits>
+
 #include "common.h"
 
 namespace anvil {
@@ -318,8 +320,13 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
 }
 
+// workgroups per CU the register budget is sized for: 3 for 128 x 128, 2 for 256 x 128 / 128 x 256 (AGPR + VGPR <= 256
+// a lane, two waves a SIMD), 1 for 256 x 256
+template <int BM, int BN>
+constexpr int fast_occupancy() { return BM * BN <= 128 * 128 ? 3 : (BM * BN <= 256 * 128 ? 2 : 1); }
+
 template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24>
-__global__ __launch_bounds__(G_THREADS) void gemm_i8_fast(GemmArgs g) {
+__global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8_fast(GemmArgs g) {
   constexpr int BK = 64, CPR = BK / 16;
   constexpr int WGN = 4 / WGM;
   constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
@@ -482,31 +489,44 @@ __global__ __launch_bounds__(G_THREADS) void gemm_i8_fast(GemmArgs g) {
     if (NS == 3 || r < 3 * RPA) return L2 + (r - 2 * RPA) * SROW;
     return L3 + (r - 3 * RPA) * SROW;
   };
+  // the LUT choice is made once, outside the loops: a per-element branch would split the requant into basic blocks
+  // that each wait for their LDS reads
+  int8_t* rowp[TM];
 #pragma unroll
-  for (int j = 0; j < TM; ++j) {
-    int8_t* rowp = srow(wm * WM + j * 32 + l32);
+  for (int j = 0; j < TM; ++j) rowp[j] = srow(wm * WM + j * 32 + l32);
+  const int mult = g.mult, rnd = g.rnd, shift = g.shift;
+  auto stage = [&](auto lut_c) {
+    constexpr bool LUT = decltype(lut_c)::value;
 #pragma unroll
-    for (int i = 0; i < TN; ++i)
+    for (int j = 0; j < TM; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n_l = wn * WN + i * 32 + 8 * q + 4 * half;
-        int v[4];
+      for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int a = acc[i][j][4 * q + e];
-          const int x = MUL24 ? (__mul24(a, g.mult) + g.rnd) : (a * g.mult + g.rnd);
-          v[e] = min(max(x >> g.shift, lo), hi);
-          if (OSZ == 1 && g.lut) v[e] = lut_s[v[e] + 128];
+        for (int q = 0; q < 4; ++q) {
+          const int n_l = wn * WN + i * 32 + 8 * q + 4 * half;
+          int v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int a = acc[i][j][4 * q + e];
+            const int x = MUL24 ? (__mul24(a, mult) + rnd) : (a * mult + rnd);
+            v[e] = min(max(x >> shift, lo), hi);
+            if (LUT) v[e] = lut_s[v[e] + 128];
+          }
+          if (OSZ == 1) {
+            const unsigned t01 = __builtin_amdgcn_perm((unsigned)v[1], (unsigned)v[0], 0x0c0c0400u);
+            const unsigned t23 = __builtin_amdgcn_perm((unsigned)v[3], (unsigned)v[2], 0x0c0c0400u);
+            *reinterpret_cast<unsigned*>(rowp[j] + n_l) = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+          } else {
+            *reinterpret_cast<unsigned*>(rowp[j] + 2 * n_l) = __builtin_amdgcn_perm((unsigned)v[1], (unsigned)v[0], 0x05040100u);
+            *reinterpret_cast<unsigned*>(rowp[j] + 2 * n_l + 4) =
+                __builtin_amdgcn_perm((unsigned)v[3], (unsigned)v[2], 0x05040100u);
+          }
         }
-        if (OSZ == 1) {
-          *reinterpret_cast<unsigned*>(rowp + n_l) =
-              (unsigned)(v[0] & 255) | ((unsigned)(v[1] & 255) << 8) | ((unsigned)(v[2] & 255) << 16) | ((unsigned)v[3] << 24);
-        } else {
-          *reinterpret_cast<unsigned*>(rowp + 2 * n_l) = (unsigned)(v[0] & 0xffff) | ((unsigned)v[1] << 16);
-          *reinterpret_cast<unsigned*>(rowp + 2 * n_l + 4) = (unsigned)(v[2] & 0xffff) | ((unsigned)v[3] << 16);
-        }
-      }
-  }
+  };
+  if (OSZ == 1 && g.lut)
+    stage(std::true_type{});
+  else
+    stage(std::false_type{});
   __syncthreads();
 
   constexpr int CH_ROW = BN * OSZ / 16;
@@ -515,7 +535,54 @@ __global__ __launch_bounds__(G_THREADS) void gemm_i8_fast(GemmArgs g) {
   char* Cb = reinterpret_cast<char*>(g.C) + (b0 * g.sc0 + b1 * g.sc1) * OSZ;
   const int cols_valid = min(BN, g.N - n0);
   const int cfirst = cc * 16 / OSZ;
-  for (int rr = rr0; rr < BM; rr += ROWS_PER_PASS) {
+  static_assert(BM % ROWS_PER_PASS == 0, "whole store passes");
+  constexpr int PASSES = BM / ROWS_PER_PASS;
+  // interior tile: every chunk is read from LDS (and the residual from memory) before the first store, so the
+  // reads' latencies overlap instead of serialising pass by pass
+  const bool full = m0 + BM <= g.M && cols_valid == BN && (OSZ == 1 && g.res ? g.vec_res != 0 : g.vec_store != 0) &&
+                    (!(OSZ == 1 && g.res) || !g.store_y || g.vec_store);
+  if (full) {
+    v4i ch[PASSES];
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass)
+      ch[pass] = *reinterpret_cast<const v4i*>(srow(rr0 + pass * ROWS_PER_PASS) + cc * 16);
+    if (OSZ == 1 && g.res) {
+      const int8_t* Rb = g.R + b0 * g.sr0 + b1 * g.sr1 + (long long)(m0 + rr0) * g.ldr + n0 + cfirst;
+      int8_t* Db = g.D + b0 * g.sd0 + b1 * g.sd1 + (long long)(m0 + rr0) * g.ldd + n0 + cfirst;
+      v4i rv[PASSES];
+#pragma unroll
+      for (int pass = 0; pass < PASSES; ++pass)
+        rv[pass] = *reinterpret_cast<const v4i*>(Rb + (long long)pass * ROWS_PER_PASS * g.ldr);
+      const int ma = g.ma, mb = g.mb, rnd2 = g.rnd2, sh2 = g.shift2;
+#pragma unroll
+      for (int pass = 0; pass < PASSES; ++pass) {
+        v4i ov;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          int o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int y = (int)(int8_t)((unsigned)ch[pass][q] >> (8 * e));
+            const int r = (int)(int8_t)((unsigned)rv[pass][q] >> (8 * e));
+            o[e] = min(max((r * ma + y * mb + rnd2) >> sh2, -128), 127);      // proven inside int32
+          }
+          const unsigned t01 = __builtin_amdgcn_perm((unsigned)o[1], (unsigned)o[0], 0x0c0c0400u);
+          const unsigned t23 = __builtin_amdgcn_perm((unsigned)o[3], (unsigned)o[2], 0x0c0c0400u);
+          ov[q] = (int)__builtin_amdgcn_perm(t23, t01, 0x05040100u);
+        }
+        *reinterpret_cast<v4i*>(Db + (long long)pass * ROWS_PER_PASS * g.ldd) = ov;
+      }
+      if (!g.store_y) return;
+    }
+    char* Cr = Cb + ((long long)(m0 + rr0) * g.ldc + n0 + cfirst) * OSZ;
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass)
+      *reinterpret_cast<v4i*>(Cr + (long long)pass * ROWS_PER_PASS * g.ldc * OSZ) = ch[pass];
+    return;
+  }
+#pragma unroll
+  for (int pass = 0; pass < PASSES; ++pass) {
+    const int rr = rr0 + pass * ROWS_PER_PASS;
     const int m = m0 + rr;
     if (m >= g.M) break;
     const int8_t* src = srow(rr) + cc * 16;
@@ -586,10 +653,11 @@ static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s,
     case 17: return launch_fast<128, 256, 2, 3, MUL24>(g, osz, batch, s);
     default: break;
   }
-  // measured on MI355X: three 128 x 128 workgroups per CU (48 KiB LDS each) hide each other's barriers and
-  // epilogues best; only long-K products (L2 traffic per MFMA halves with the 256 x 256 tile) prefer the big tile
-  if (g.K >= 2048 && g.M >= 1024 && g.N >= 256)
-    launch_fast<256, 256, 2, 4, MUL24>(g, osz, batch, s);
+  // measured on MI355X (block GEMM shapes, K 768 and 3072): 256 x 128 tiles with three LDS stages (72 KiB) and at
+  // most 256 registers a lane run two workgroups per CU, which hide each other's pipeline fill and epilogue, at 2/3
+  // of the 128 x 128 tile's L2 traffic per MFMA; small problems keep the 128 x 128 tile (more workgroups)
+  if ((long long)g.M * g.N * batch >= 256ll * 128 * 512 && g.M >= 256 && g.N >= 128)
+    launch_fast<256, 128, 2, 3, MUL24>(g, osz, batch, s);
   else
     launch_fast<128, 128, 2, 3, MUL24>(g, osz, batch, s);
 }
