@@ -124,8 +124,12 @@ __global__ __launch_bounds__(R_THREADS) void softmax_fast(const int8_t* __restri
 }
 
 // ------------------------------------------------------------------------------------- fast rmsnorm_int
-// For proven graphs with i8 rows (ss_shift = ss_init = 0) of a multiple of 16 bytes and at most 1024: one wavefront
-// per row, lane l holds 16 consecutive entries, the sum of squares is v_dot4 of each dword with itself.
+// For proven graphs with i8 rows (ss_shift = ss_init = 0) of a multiple of 16 bytes and at most 1024: a wavefront
+// takes RMS_ROWS rows at a time, lane l holding 16 consecutive entries of each; every row's load (and then every
+// row's rsqrt-LUT read) is issued before any is used, so their latencies overlap. The sum of squares is v_dot4 of
+// each dword with itself.
+constexpr int RMS_ROWS = 4;
+
 __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
                                                            const int* __restrict__ lut, int lut_len, int mult,
                                                            int shift, long long rows, int cols,
@@ -135,31 +139,45 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
   const bool active = lane < chunks;
   v4i wv = {0, 0, 0, 0};
   if (active) wv = *reinterpret_cast<const v4i*>(w + 16 * lane);
-  for (long long row = (long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6); row < rows;
-       row += (long long)gridDim.x * R_WAVES) {
-    v4i xv = {0, 0, 0, 0};
-    if (active) xv = *reinterpret_cast<const v4i*>(x + row * cols + 16 * lane);
-    int ss = 0;
+  const long long step = (long long)gridDim.x * R_WAVES * RMS_ROWS;
+  for (long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * RMS_ROWS; row0 < rows;
+       row0 += step) {
+    v4i xv[RMS_ROWS];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[q], xv[q], ss, false);
-    ss = wave_sum32(ss);
-    int k = 0;
-    while (ss >= lut_len) {
-      ss >>= 2;
-      ++k;
+    for (int j = 0; j < RMS_ROWS; ++j) {
+      xv[j] = v4i{0, 0, 0, 0};
+      if (active && row0 + j < rows) xv[j] = *reinterpret_cast<const v4i*>(x + (row0 + j) * cols + 16 * lane);
     }
-    const int r = lut[ss];
-    const int sh = shift + k;
-    const int rnd = sh ? (1 << (sh - 1)) : 0;
-    if (active) {
+    int idx[RMS_ROWS], sh[RMS_ROWS];
+#pragma unroll
+    for (int j = 0; j < RMS_ROWS; ++j) {
+      int ss = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[j][q], xv[j][q], ss, false);
+      ss = wave_sum32(ss);
+      int k = 0;
+      while (ss >= lut_len) {
+        ss >>= 2;
+        ++k;
+      }
+      idx[j] = ss;
+      sh[j] = shift + k;
+    }
+    int r[RMS_ROWS];
+#pragma unroll
+    for (int j = 0; j < RMS_ROWS; ++j) r[j] = lut[idx[j]];
+#pragma unroll
+    for (int j = 0; j < RMS_ROWS; ++j) {
+      if (!active || row0 + j >= rows) continue;
+      const int rnd = sh[j] ? (1 << (sh[j] - 1)) : 0;
       unsigned ov[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int b = 0; b < 16; ++b) {
-        const int xwr = sbyte(xv, b) * sbyte(wv, b) * r;        // proven: x w r and x w r M + rnd fit int32
-        const int v = min(max((xwr * mult + rnd) >> sh, -128), 127);
+        const int xwr = sbyte(xv[j], b) * sbyte(wv, b) * r[j];   // proven: x w r and x w r M + rnd fit int32
+        const int v = min(max((xwr * mult + rnd) >> sh[j], -128), 127);
         ov[b >> 2] |= (unsigned)(v & 255) << (8 * (b & 3));
       }
-      *reinterpret_cast<v4i*>(out + row * cols + 16 * lane) = v4i{(int)ov[0], (int)ov[1], (int)ov[2], (int)ov[3]};
+      *reinterpret_cast<v4i*>(out + (row0 + j) * cols + 16 * lane) = v4i{(int)ov[0], (int)ov[1], (int)ov[2], (int)ov[3]};
     }
   }
 }
@@ -290,7 +308,8 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
   if (blocks > (1ll << 31) - 1) return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: too many rows");
   if ((flags & ANVIL_OP_UNCHECKED) && x_dtype == ANVIL_I8 && ss_shift == 0 && ss_init == 0 && cols % 16 == 0 &&
       cols <= 1024 && al16(x) && al16(w) && al16(out)) {
-    hipLaunchKernelGGL(rmsnorm_fast, dim3(row_grid(rows, ctx->num_cu)), dim3(R_THREADS), 0, ctx->stream,
+    hipLaunchKernelGGL(rmsnorm_fast, dim3(row_grid((rows + RMS_ROWS - 1) / RMS_ROWS, ctx->num_cu)), dim3(R_THREADS), 0,
+                       ctx->stream,
                        (const int8_t*)x, w, lut, lut_len, mult, shift, (long long)rows, cols, out);
   } else if (x_dtype == ANVIL_I8) {
     hipLaunchKernelGGL(rmsnorm_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
