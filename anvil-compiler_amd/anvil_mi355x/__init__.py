@@ -1,7 +1,8 @@
 """anvil_mi355x: an MI355X (gfx950) backend for the int8 graph evaluation that Anvil's interpreter defines.
 
     import anvil_mi355x as anvil
-    cm = anvil.compile((module, consts))         # a graph built with anvil_mi355x.ir.GraphBuilder (or loaded)
+    cm = anvil.compile((module, consts))         # built with GraphBuilder, or anvil.parse_ir(text) of the
+                                                 # reference's printed IR
     res = cm.run(x, "mi355x")                    # res.output, res.outputs, res.ints[sym], res.cycles
 
 Mirrors the reference's public surface (anvil/__init__.py:9-12 -> anvil/driver.py:330-335) for the graph path:
@@ -10,7 +11,7 @@ compile / CompiledModel.run / RunOutput (anvil/driver.py), with "mi355x" as the 
 hand-written HIP kernel for gfx950 through the C ABI of libanvil_mi355x.so (include/anvil_mi355x.h).
 """
 from . import ir
-from .ir import GraphBuilder, QTensorType, VerifyException
+from .ir import GraphBuilder, QTensorType, VerifyException, parse_ir, print_ir
 
 
 def compile(*args, **kw):  # noqa: A001  (the public entry point shadows the builtin inside this package only)
@@ -19,4 +20,4 @@ def compile(*args, **kw):  # noqa: A001  (the public entry point shadows the bui
     return _compile(*args, **kw)
 
 
-__all__ = ["compile", "ir", "GraphBuilder", "QTensorType", "VerifyException"]
+__all__ = ["compile", "ir", "GraphBuilder", "QTensorType", "VerifyException", "parse_ir", "print_ir"]

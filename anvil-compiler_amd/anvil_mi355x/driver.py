@@ -64,14 +64,17 @@ def _graph_meta(module):
 
 def _resolve_model(model, consts, prove=True):
     from .models import Built
+    from .ir_text import parse_ir
     if isinstance(model, Built):
         return model.module, dict(model.consts)
-    if isinstance(model, tuple) and len(model) == 2 and isinstance(model[0], g.Module):
-        return _checked_graph(model[0], dict(model[1]), prove)
+    if isinstance(model, tuple) and len(model) == 2 and isinstance(model[0], (g.Module, str)):
+        model, consts = model
+    if isinstance(model, str):                  # the reference's printed IR (anvil.ir.print_ir)
+        model = parse_ir(model)
     if isinstance(model, g.Module):
         return _checked_graph(model, dict(consts or {}), prove)
-    raise TypeError(f"cannot compile a {type(model).__name__}: expected an anvil graph module, (module, consts) or "
-                    "a built model (the torch capture frontend is not part of this backend)")
+    raise TypeError(f"cannot compile a {type(model).__name__}: expected an anvil graph module or its printed IR, "
+                    "(module, consts) or a built model (the torch capture frontend is not part of this backend)")
 
 
 def _checked_graph(module, consts, prove=True):

@@ -428,3 +428,15 @@ class GraphBuilder:
         if self._module is None:
             self._module = Module(self.func)
         return self._module
+
+
+def print_ir(module) -> str:
+    """The module in the reference's textual (MLIR generic) form (anvil/ir/__init__.py:22-25)."""
+    from .ir_text import print_ir as _print
+    return _print(module)
+
+
+def parse_ir(text: str):
+    """A module from the reference's textual form (anvil/ir/__init__.py:28-31)."""
+    from .ir_text import parse_ir as _parse
+    return _parse(text)

@@ -8,6 +8,8 @@ with T1 != T2 and an i32 softmax output. A draw the oracle rejects (int32 overfl
 from __future__ import annotations
 
 import ctypes as C
+import gzip
+import json
 import subprocess
 from pathlib import Path
 
@@ -227,3 +229,14 @@ def scalar_run(m, inputs, consts, batch=False):
         if op.sym_str is not None:
             vals[op.sym_str] = val
     return vals
+
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def reference_model(name):
+    """(IR text, consts, held-out input or None) of the reference's frozen model file tests/golden/model_graph_<name>."""
+    body = json.load(gzip.open(GOLDEN / f"model_graph_{name}.json.gz", "rt"))
+    consts = {k: np.asarray(v, dtype=np.int64).reshape(body["shapes"][k]) for k, v in body["consts"].items()}
+    x = np.asarray(body["x"], dtype=np.int64) if "x" in body else None
+    return body["ir"], consts, x

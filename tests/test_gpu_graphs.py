@@ -107,3 +107,23 @@ def test_keep_outputs_equals_keep_all_and_runs_repeat():
     assert set(b.ints) == {"x", "out"}
     assert np.array_equal(a.ints["out"], b.ints["out"]) and np.array_equal(b.ints["out"], c.ints["out"])
     assert np.allclose(b.output, b.ints["out"] * built.scales["out"])
+
+
+@pytest.mark.parametrize("name", ["v1", "v2"])
+@pytest.mark.parametrize("keep", ["all", "outputs"])
+def test_reference_frozen_model(name, keep):
+    """The reference's frozen 2-layer model files, loaded from their printed IR: v2 (i16 residual stream, wide
+    rmsnorm) on its held-out input and on seeded inputs of the full i16 range, v1 (int8) on seeded int8 inputs."""
+    text, consts, x = helpers.reference_model(name)
+    m = anvil_mi355x.parse_ir(text)
+    cm = anvil_mi355x.compile((m, consts))
+    rng = np.random.default_rng(11)
+    lo, hi = (-32768, 32768) if name == "v2" else (-128, 128)
+    xs = rng.integers(lo, hi, (6, 16, 32))
+    if x is not None:
+        xs[0] = x
+    want = interp.run(m, {"x": xs}, consts, batch=True)
+    res = cm.run(xs, "mi355x", quantized=True, batch=True, keep=keep)
+    if keep == "all":
+        _check_all(res.ints, want.values, consts)
+    assert np.array_equal(res.ints["L1.out"], want.values["L1.out"])
