@@ -51,17 +51,6 @@ struct AttnArgs {
 
 constexpr int A_THREADS = 256;
 
-// f(std::integral_constant<int, i>) for i = 0 .. N-1, expanded at compile time: register arrays indexed by i stay in
-// registers (a loop the unroller declines would index them dynamically, through scratch).
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 __device__ __forceinline__ int sbyte(unsigned v, int e) { return (int)(int8_t)(v >> (8 * e)); }
 
 // low bytes of four ints -> one dword (three v_perm_b32)
@@ -83,19 +72,17 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   constexpr int KS = (D + 31) / 32;         // 32-wide MFMA k-steps over the head dim
   constexpr int CT = (D + 31) / 32;         // 32-wide output column tiles
   constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
-  __shared__ int lut_s[256];
-  __shared__ double lutd_s[256];            // lut[d] as float64
+  static_assert(4 * 32 * OROW * 4 >= 32 * 272, "the per-row p tables fit in the partial-O space");
+  __shared__ __attribute__((aligned(16))) int lut_s[256];
+  __shared__ __attribute__((aligned(16))) int lutc_s[16];  // lut[16 k + 15]: the coarse level of the threshold search
   __shared__ int red_m[4][32], red_s[4][32];
   __shared__ __attribute__((aligned(16))) int opart[4][32 * OROW];
 
   const int t = threadIdx.x;
   const int lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int l32 = lane & 31, half = lane >> 5;
-  {
-    const int v = a.lut[t];
-    lut_s[t] = v;
-    lutd_s[t] = (double)v;
-  }
+  lut_s[t] = a.lut[t];
+  if (t < 16) lutc_s[t] = a.lut[16 * t + 15];
 
   // XCD-aware order: consecutive logical tiles on one XCD (its L2 holds the head's K and V), each head's query tiles
   // together, the longest (last) query tile of a head first
@@ -110,7 +97,9 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   const int ntiles = a.causal ? qt + 1 : a.nqt;
 
   const int8_t* Qr = a.Q + b0 * a.sq0 + b1 * a.sq1 + (long long)qrow * a.ldq;
-  const int8_t* Kb = a.K + b0 * a.sk0 + b1 * a.sk1 + (long long)l32 * a.ldk;
+  // key rows enter the score MFMA in bperm order: score accumulator r of lane l is then key 16 (l / 32) + r of the
+  // tile, so a lane's 16 probabilities are 16 consecutive keys and its V^T fragment is one contiguous 16-byte load
+  const int8_t* Kb = a.K + b0 * a.sk0 + b1 * a.sk1 + (long long)bperm(l32) * a.ldk;
   const int8_t* Vb = a.V + b0 * a.sv0 + b1 * a.sv1;
 
   v4i qf[KS];
@@ -124,14 +113,16 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = chunk16<D>(Kb + (long long)nt * 32 * a.ldk, 2 * ks + half);
   };
-  v4i kf[KS];
+  // K tiles are loaded two tiles ahead of their MFMAs
+  v4i kf[KS], kn[KS];
   if (w < ntiles) kload(w, kf);
+  if (NTW > 1 && w + 4 < ntiles) kload(w + 4, kn);
   static_for<NTW>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
     if (nt < ntiles) {
-      v4i kn[KS];
-      if (i + 1 < NTW && nt + 4 < ntiles) kload(nt + 4, kn);
+      v4i kn2[KS];
+      if (i + 2 < NTW && nt + 8 < ntiles) kload(nt + 8, kn2);
       v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[ks], qf[ks], acc, 0, 0, 0);
@@ -144,7 +135,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
       if (a.causal && nt == ntiles - 1) {             // the diagonal tile: keys past the row are masked
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          mx = max(mx, nt * 32 + 8 * (r >> 2) + 4 * half + (r & 3) <= qrow ? v[r] : -128);
+          mx = max(mx, nt * 32 + 16 * half + r <= qrow ? v[r] : -128);
       } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = max(mx, v[r]);
@@ -152,12 +143,28 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) sc[i][g] = pack4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = kn[ks];
+      for (int ks = 0; ks < KS; ++ks) {
+        kf[ks] = kn[ks];
+        kn[ks] = kn2[ks];
+      }
     }
   });
+
+  // the first two V^T tiles load while the row maxima are reduced and the sums run
+  const int8_t* Vr[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) Vr[ct] = Vb + (long long)(32 * ct + l32) * a.ldv + 16 * half;
+  auto vload = [&](int nt, v4i* vf) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+      vf[ct] = 32 * ct + l32 >= D ? v4i{0, 0, 0, 0} : *reinterpret_cast<const v4i*>(Vr[ct] + nt * 32);
+  };
+  v4i vf[CT], vn[CT];
+  if (w < ntiles) vload(w, vf);
+  if (NTW > 1 && w + 4 < ntiles) vload(w + 4, vn);
   mx = max(mx, __shfl_xor(mx, 32, 64));
   if (half == 0) red_m[w][l32] = mx;
-  __syncthreads();                                        // also publishes lut_s / lutd_s
+  __syncthreads();                                        // also publishes lut_s
   mx = max(max(red_m[0][l32], red_m[1][l32]), max(red_m[2][l32], red_m[3][l32]));
 
   // ---- 2. partial exp sums over the kept keys
@@ -171,7 +178,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int s = sbyte(sc[i][r >> 2], r & 3);
-          const bool kept = nt * 32 + 8 * (r >> 2) + 4 * half + (r & 3) <= qrow;
+          const bool kept = nt * 32 + 16 * half + r <= qrow;
           const int e = erow[kept ? s : mx];              // a masked score may exceed the max: read inside the table
           S += kept ? e : 0;
         }
@@ -183,55 +190,75 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   });
   S += __shfl_xor(S, 32, 64);
   if (half == 0) red_s[w][l32] = S;
-  __syncthreads();
+  const bool mono = __syncthreads_and(t == 255 || lut_s[t] <= lut_s[t + 1]) != 0;   // lut_s is visible here
   S = red_s[0][l32] + red_s[1][l32] + red_s[2][l32] + red_s[3][l32];
 
   // ---- 3. probabilities, O_w = P V over this wave's tiles
+  // p depends on the row and the score only, so each row gets a byte table prow[s] = (lut[d] one + S // 2) // S,
+  // d = s - max + 255, built in the partial-O space (free until this phase ends). With a non-decreasing table the
+  // quotient is 0 below the first d where lut[d] one + S // 2 >= S, and only the entries from there up are divided;
+  // otherwise every entry is.
   const double Sd = (double)S;                           // S >= lut[255] >= 1: the row maximum maps to d = 255
   const double qa = (double)a.one / Sd;
   const double qb = (double)(S >> 1) / Sd + 0x1p-40;
-  const double* drow = lutd_s + (255 - mx);              // drow[s] = lut[s - max + 255]
-  auto quot = [&](int s) -> int {                        // (lut[d] one + S // 2) // S
-    return (int)__builtin_fma(drow[s], qa, qb);
-  };
+  int d0 = 0;
+  if (mono) {
+    // lut[d] one + S // 2 >= S  <=>  lut[d] >= e0 = ceil((S - S // 2) / one); d0 = #{d : lut[d] < e0}, counted over
+    // 16 blocks of 16 and then inside the first block that reaches e0
+    const int need = S - (S >> 1);
+    const int e0 = (need + a.one - 1) / a.one;
+    auto below16 = [&](const int* p16) {
+      int n = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const v4i v = reinterpret_cast<const v4i*>(p16)[q];
+        n += (v[0] < e0) + (v[1] < e0) + (v[2] < e0) + (v[3] < e0);
+      }
+      return n;
+    };
+    const int blk = below16(lutc_s);
+    d0 = blk == 16 ? 256 : 16 * blk + below16(lut_s + 16 * blk);
+  }
+  constexpr int PT = 272;                                // table row stride (bytes), 16-byte aligned
+  int8_t* ptab = reinterpret_cast<int8_t*>(&opart[0][0]);
+  {
+    const int part = 2 * w + half;                       // this lane's eighth of its row's table
+    int8_t* zp = ptab + l32 * PT + 32 * part;
+    *reinterpret_cast<v4i*>(zp) = v4i{0, 0, 0, 0};
+    *reinterpret_cast<v4i*>(zp + 16) = v4i{0, 0, 0, 0};
+    __syncthreads();
+    const int dlow = max(d0, 127 - mx);                  // d below 127 - max needs s < -128
+    for (int d = 255 - part; d >= dlow; d -= 32) {      // four independent entries per pass
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int du = d - 8 * u;
+        if (du >= dlow) ptab[l32 * PT + (du + mx - 255 + 128)] = (int8_t)(int)__builtin_fma((double)lut_s[du], qa, qb);
+      }
+    }
+    __syncthreads();
+  }
+  const int8_t* prow = ptab + l32 * PT + 128;
   v16i oacc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) oacc[ct] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  const int8_t* Vr[CT];
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct) Vr[ct] = Vb + (long long)(32 * ct + l32) * a.ldv;
-  auto vload = [&](int nt, v4i* vf) {
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      if (32 * ct + l32 >= D) {
-        vf[ct] = v4i{0, 0, 0, 0};
-      } else {
-        const v4i lo = *reinterpret_cast<const v4i*>(Vr[ct] + nt * 32);
-        const v4i hi = *reinterpret_cast<const v4i*>(Vr[ct] + nt * 32 + 16);
-        vf[ct] = half ? v4i{lo[1], lo[3], hi[1], hi[3]} : v4i{lo[0], lo[2], hi[0], hi[2]};
-      }
-    }
-  };
-  v4i vf[CT];
-  if (w < ntiles) vload(w, vf);
   static_for<NTW>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
     if (nt < ntiles) {
-      v4i vn[CT];
-      if (i + 1 < NTW && nt + 4 < ntiles) vload(nt + 4, vn);
+      v4i vn2[CT];
+      if (i + 2 < NTW && nt + 8 < ntiles) vload(nt + 8, vn2);
       int p[16];
       if (a.causal && nt == ntiles - 1) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int s = sbyte(sc[i][r >> 2], r & 3);
-          const bool kept = nt * 32 + 8 * (r >> 2) + 4 * half + (r & 3) <= qrow;
-          const int q = quot(kept ? s : mx);
+          const bool kept = nt * 32 + 16 * half + r <= qrow;
+          const int q = prow[kept ? s : mx];
           p[r] = kept ? q : 0;
         }
       } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = quot(sbyte(sc[i][r >> 2], r & 3));
+        for (int r = 0; r < 16; ++r) p[r] = prow[sbyte(sc[i][r >> 2], r & 3)];
       }
       v4i pf;
 #pragma unroll
@@ -239,11 +266,15 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) oacc[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf[ct], pf, oacc[ct], 0, 0, 0);
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) vf[ct] = vn[ct];
+      for (int ct = 0; ct < CT; ++ct) {
+        vf[ct] = vn[ct];
+        vn[ct] = vn2[ct];
+      }
     }
   });
 
   // ---- 4. sum the four partial O tiles, requant, store. Lane l holds O_w[row l % 32][32 ct + 8 g + 4 (l / 32) + e].
+  __syncthreads();                                       // every wave is done with the p tables
   int* op = opart[w] + l32 * OROW;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct)

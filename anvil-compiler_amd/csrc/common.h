@@ -6,6 +6,8 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
+#include <utility>
 
 #include "../../include/anvil_mi355x.h"
 
@@ -46,6 +48,22 @@ int check_ctx(anvil_ctx* ctx);
     hipError_t e_ = hipGetLastError();                                        \
     if (e_ != hipSuccess) return ::anvil::hip_fail(e_, "kernel launch");      \
   } while (0)
+
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, expanded at compile time: register arrays indexed by i stay in
+// registers (a loop the unroller declines would index them dynamically, through scratch).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Row order for the first operand of v_mfma_i32_32x32x32_i8 (the one whose rows become accumulator rows): feeding
+// row bperm(c) at operand row c makes accumulator r of lane l hold result row 16 (l / 32) + r, so each lane owns 16
+// consecutive rows of its column.
+__device__ __forceinline__ int bperm(int c) { return 16 * ((c >> 2) & 1) + 4 * (c >> 3) + (c & 3); }
 
 constexpr long long I32_MIN = -(1ll << 31);
 constexpr long long I32_MAX = (1ll << 31) - 1;

@@ -243,9 +243,11 @@ def test_quantize_input(dev, f64):
     assert np.array_equal(out.download((x.size,), np.int8).astype(np.int64), want)
 
 
-def _attention_case(B, H, T, D, causal, seed, ms_sign=1):
+def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127):
     """Random q, k, v (B, T, H D) i8 with scores and output requants that spread over int8, the reference chain
-    qmatmul -> softmax_lut -> qmatmul evaluated by the oracle, and the head-split views the fused kernel reads."""
+    qmatmul -> softmax_lut -> qmatmul evaluated by the oracle, and the head-split views the fused kernel reads.
+    lut_kind: "exp" (the quantizer's table), "steep" (an exp table with a run of zeros at the low end) or "random"
+    (positive and not monotone, so no threshold shortcut applies)."""
     rng = np.random.default_rng([21, B, H, T, D, int(causal), seed])
     C = H * D
     q, k, v = (rng.integers(-128, 128, (B, T, C)) for _ in range(3))
@@ -254,10 +256,13 @@ def _attention_case(B, H, T, D, causal, seed, ms_sign=1):
         q[-1, :, -D:], k[-1, :, -D:] = 127, -128             # a head of scores clamped to -128: max = -128
     ms = ms_sign * max(1, round(40 / (74.0 ** 2 * np.sqrt(D)) * (1 << 16)))
     ss, mo, so = 16, 1, 7
-    lut = Q.exp_lut(0.05, T)
+    if lut_kind == "random":
+        lut = rng.integers(1, 1 << 20, 256)
+    else:
+        lut = Q.exp_lut(0.5 if lut_kind == "steep" else 0.05, T, one)
     split = lambda a: a.reshape(B, T, H, D).transpose(0, 2, 1, 3)       # noqa: E731
     scores = sem.qmatmul(split(q), np.swapaxes(split(k), -1, -2), ms, ss, fast=True)
-    p = sem.softmax_lut(scores, lut, 127, causal)
+    p = sem.softmax_lut(scores, lut, one, causal)
     o = sem.qmatmul(p, split(v), mo, so, fast=True)          # (B, H, T, D)
     return q, k, v, (ms, ss, mo, so), lut, o.transpose(0, 2, 1, 3).reshape(B, T, C)
 
@@ -267,18 +272,23 @@ def _attention_case(B, H, T, D, causal, seed, ms_sign=1):
 @pytest.mark.parametrize("causal", [True, False])
 def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
     """anvil_attention_i8 over q, k (B, T, H D), v^T (B, H D, T) and o (B, T, H D), as the planner lays them out,
-    bit-exact with the oracle's scores -> softmax -> P.V chain."""
-    for seed, sign in ((0, 1), (1, -1)):
-        q, k, v, (ms, ss, mo, so), lut, want = _attention_case(B, H, T, D, causal, seed, sign)
+    bit-exact with the oracle's scores -> softmax -> P.V chain, for the quantizer's exp table, a table with a zero run
+    and a non-monotone one, and one = 127 or 100."""
+    for seed, sign, kind, one in ((0, 1, "exp", 127), (1, -1, "exp", 127), (2, 1, "random", 127), (3, 1, "steep", 100)):
+        q, k, v, (ms, ss, mo, so), lut, want = _attention_case(B, H, T, D, causal, seed, sign, kind, one)
+        if kind == "steep":
+            assert (lut == 0).any() and np.all(np.diff(lut) >= 0)
+        if kind == "random":
+            assert np.any(np.diff(lut) < 0)
         C = H * D
         vt = np.ascontiguousarray(np.swapaxes(v, 1, 2))      # (B, C, T)
         out = dev.alloc(B * T * C)
         strides = [T * C, D, C, T * C, D, C, C * T, D * T, T, T * C, D, C]
         dev.attention_i8(up(dev, q, "i8"), up(dev, k, "i8"), up(dev, vt, "i8"), out, B, H, T, D, strides, ms, ss,
-                         up(dev, lut, "i32"), 127, causal, mo, so, rt.OP_UNCHECKED)
+                         up(dev, lut, "i32"), one, causal, mo, so, rt.OP_UNCHECKED)
         dev.sync()
         got = out.download((B, T, C), np.int8).astype(np.int64)
-        assert np.array_equal(got, want), (seed, np.argwhere(got != want)[:5])
+        assert np.array_equal(got, want), (seed, kind, np.argwhere(got != want)[:5])
 
 
 @pytest.mark.parametrize("M,K,N", [(256, 768, 768), (300, 64, 200), (33, 48, 72), (1024, 256, 384)])
