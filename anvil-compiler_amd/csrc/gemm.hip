@@ -25,6 +25,7 @@
 //
 // causal = 1: tiles strictly above the diagonal (every n > every m) are skipped (their values are never read);
 // causal = 2: the K loop stops at m0 + BM (A[m][k] = 0 for k > m, e.g. a causal softmax output).
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -53,6 +54,7 @@ struct GemmArgs {
   long long sr0, sr1, ldr, sd0, sd1, ldd;
   int ma, mb, shift2, rnd2;
   int res, store_y, vec_res;
+  int nbatch;                     // batch0 * batch1 (persistent kernel)
 };
 
 constexpr int G_THREADS = 256;
@@ -283,6 +285,16 @@ __global__ __launch_bounds__(G_THREADS) void gemm_i8_kernel(GemmArgs g) {
 constexpr unsigned RSRC_DW3 = 0x00020000u;               // raw buffer, 32-bit data format (gfx9 family)
 constexpr unsigned OOB = 0xFFFFFFF0u;
 
+// A raw buffer resource over [base, base + bytes). Its fields pass through readfirstlane: they are uniform, and
+// saying so keeps the descriptor in SGPRs (a descriptor the compiler places in VGPRs costs every buffer load a
+// waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, int bytes) {
+  const unsigned long long a = (unsigned long long)base;
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a), hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+  void* p = (void*)(((unsigned long long)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, __builtin_amdgcn_readfirstlane(bytes), RSRC_DW3);
+}
+
 // 16 bytes per lane from buffer offset voff into LDS at lds + 16 * lane (lds must be wave-uniform)
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, int8_t* lds, unsigned voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
@@ -324,6 +336,114 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // a lane, two waves a SIMD), 1 for 256 x 256
 template <int BM, int BN>
 constexpr int fast_occupancy() { return BM * BN <= 128 * 128 ? 3 : (BM * BN <= 256 * 128 ? 2 : 1); }
+
+// requant (+ LUT) of one lane's 16 accumulators into 16 results
+template <int OSZ, bool MUL24, bool LUT>
+__device__ __forceinline__ void requant16(const v16i& a, int mult, int rnd, int shift, const int8_t* lut_s, int v[16]) {
+  const int lo = OSZ == 1 ? -128 : -32768, hi = OSZ == 1 ? 127 : 32767;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int x = MUL24 ? (__mul24(a[e], mult) + rnd) : (a[e] * mult + rnd);
+    v[e] = min(max(x >> shift, lo), hi);
+    if (LUT) v[e] = lut_s[v[e] + 128];
+  }
+}
+
+__device__ __forceinline__ unsigned pack4_i8(int a, int b, int c, int d) {
+  const unsigned t01 = __builtin_amdgcn_perm((unsigned)b, (unsigned)a, 0x0c0c0400u);
+  const unsigned t23 = __builtin_amdgcn_perm((unsigned)d, (unsigned)c, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+}
+
+// Epilogue from registers: tile (i, j) of this lane is row mrow + 32 j, columns ncol + 32 i .. + 15. Interior tiles
+// issue every residual load first, then requantize and store 16 bytes a lane; edge tiles store element by element.
+template <int BM, int BN, int WM, int WN, int TM, int TN, int OSZ, bool MUL24>
+__device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&acc)[TN][TM], const int8_t* lut_s,
+                                                int mrow, int ncol, int m0, int n0, int b0, int b1) {
+  char* Cb = reinterpret_cast<char*>(g.C) + (b0 * g.sc0 + b1 * g.sc1) * OSZ;
+  const bool res = OSZ == 1 && g.res;
+  const int8_t* Rb = g.R + b0 * g.sr0 + b1 * g.sr1;
+  int8_t* Db = g.D + b0 * g.sd0 + b1 * g.sd1;
+  const bool interior = m0 + BM <= g.M && n0 + BN <= g.N &&
+                        (res ? (g.vec_res != 0 && (!g.store_y || g.vec_store != 0)) : g.vec_store != 0);
+  const int mult = g.mult, rnd = g.rnd, shift = g.shift;
+  auto run = [&](auto lut_c, auto full_c) {
+    constexpr bool LUT = decltype(lut_c)::value, FULL = decltype(full_c)::value;
+    v4i rv[TM][TN];
+    if (FULL && res) {
+#pragma unroll
+      for (int j = 0; j < TM; ++j)
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+          rv[j][i] = *reinterpret_cast<const v4i*>(Rb + (long long)(mrow + 32 * j) * g.ldr + ncol + 32 * i);
+    }
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int m = mrow + 32 * j;
+#pragma unroll
+      for (int i = 0; i < TN; ++i) {
+        const int n = ncol + 32 * i;
+        int v[16];
+        requant16<OSZ, MUL24, LUT>(acc[i][j], mult, rnd, shift, lut_s, v);
+        if (FULL) {
+          if (res) {
+            const int ma = g.ma, mb = g.mb, rnd2 = g.rnd2, sh2 = g.shift2;
+            v4i ov;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              int o[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int r = (int)(int8_t)((unsigned)rv[j][i][q] >> (8 * e));
+                o[e] = min(max((r * ma + v[4 * q + e] * mb + rnd2) >> sh2, -128), 127);   // proven inside int32
+              }
+              ov[q] = (int)pack4_i8(o[0], o[1], o[2], o[3]);
+            }
+            *reinterpret_cast<v4i*>(Db + (long long)m * g.ldd + n) = ov;
+            if (!g.store_y) continue;
+          }
+          if (OSZ == 1) {
+            v4i w;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w[q] = (int)pack4_i8(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            *reinterpret_cast<v4i*>(Cb + (long long)m * g.ldc + n) = w;
+          } else {
+            v4i w0, w1;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              w0[q] = (int)__builtin_amdgcn_perm((unsigned)v[2 * q + 1], (unsigned)v[2 * q], 0x05040100u);
+              w1[q] = (int)__builtin_amdgcn_perm((unsigned)v[2 * q + 9], (unsigned)v[2 * q + 8], 0x05040100u);
+            }
+            char* d = Cb + ((long long)m * g.ldc + n) * 2;
+            *reinterpret_cast<v4i*>(d) = w0;
+            *reinterpret_cast<v4i*>(d + 16) = w1;
+          }
+        } else if (m < g.M) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            if (n + e >= g.N) break;
+            if (res) {
+              const int r = Rb[(long long)m * g.ldr + n + e];
+              Db[(long long)m * g.ldd + n + e] =
+                  (int8_t)min(max((r * g.ma + v[e] * g.mb + g.rnd2) >> g.shift2, -128), 127);
+              if (!g.store_y) continue;
+            }
+            if (OSZ == 1)
+              Cb[(long long)m * g.ldc + n + e] = (int8_t)v[e];
+            else
+              reinterpret_cast<int16_t*>(Cb)[(long long)m * g.ldc + n + e] = (int16_t)v[e];
+          }
+        }
+      }
+    }
+  };
+  const bool lut = OSZ == 1 && g.lut;
+  if (interior) {
+    if (lut) run(std::true_type{}, std::true_type{}); else run(std::false_type{}, std::true_type{});
+  } else {
+    if (lut) run(std::true_type{}, std::false_type{}); else run(std::false_type{}, std::false_type{});
+  }
+}
 
 template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24>
 __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8_fast(GemmArgs g) {
@@ -367,8 +487,8 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
   const int8_t* Bb = g.B + b0 * g.sb0 + b1 * g.sb1 + (long long)n0 * g.ldb;
   const int rows_a = min(g.M - m0, BM), rows_b = min(g.N - n0, BN);
   const int K = g.causal == 2 ? min(g.K, m0 + BM) : g.K;
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, (int)(rows_a * g.lda), RSRC_DW3);
-  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, (int)(rows_b * g.ldb), RSRC_DW3);
+  const __amdgpu_buffer_rsrc_t ra = uniform_rsrc(Ab, (int)(rows_a * g.lda));
+  const __amdgpu_buffer_rsrc_t rb = uniform_rsrc(Bb, (int)(rows_b * g.ldb));
 
   if (g.lut) lut_s[t] = g.lut[t];
 
@@ -628,7 +748,197 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
   }
 }
 
+// Persistent kernel with a register epilogue. Bt rows are loaded into LDS permuted within each 32-row group (LDS row c
+// holds Bt row bperm(c)), so accumulator r of lane l is output column 16 (l / 32) + r of its 32 x 32 tile: each lane
+// owns 16 consecutive columns of one row and writes them with one 16-byte store (two for i16), with no LDS staging.
+// gridDim.x workgroups (a multiple of 8) walk every tile of every batch entry. XCD x (workgroups x, x + 8, ...) owns the contiguous logical tile range
+// [x * chunk, (x + 1) * chunk) and its workgroups take consecutive tiles of it, so the tiles in flight on one XCD share
+// A row bands and B column panels in that XCD's L2. The LDS pipeline runs on across tiles: the last two stages of a
+// tile issue the next tile's first two stages, and the epilogue (registers only) runs while they load. A tile's K
+// loop must be a whole number of array rotations (nk % NS == 0), so every tile starts in L0.
+template <int BM, int BN, int BK, int NS>
+constexpr int persist_occupancy() { return NS * (BM + BN) * BK + 256 <= 80 * 1024 ? 2 : 1; }
+
+// NW waves in a (NW / WGN) x WGN grid over the BM x BN tile
+template <int BM, int BN, int BK, int NS, int NW, int WGN, int OSZ, bool MUL24>
+__global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) void gemm_i8_persist(GemmArgs g) {
+  constexpr int CPR = BK / 16, KS = BK / 32, WGM = NW / WGN;
+  static_assert(NS >= 3 && NS <= 6, "three to six LDS stages");
+  constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+  static_assert(WGM * WGN == NW && TM >= 1 && TN >= 1, "wave grid");
+  static_assert(KS % 2 == 0, "fragment sets alternate within a stage");
+  constexpr int IA = BM * CPR / 64, IB = BN * CPR / 64;
+  static_assert(IA % NW == 0 && IB % NW == 0, "each wave issues an equal share of a stage");
+  constexpr int JA = IA / NW, JB = IB / NW, G = JA + JB;
+  constexpr int STAGE = (BM + BN) * BK;
+  __shared__ __attribute__((aligned(1024))) int8_t L0[STAGE];
+  __shared__ __attribute__((aligned(1024))) int8_t L1[STAGE];
+  __shared__ __attribute__((aligned(1024))) int8_t L2[STAGE];
+  __shared__ __attribute__((aligned(1024))) int8_t L3[NS > 3 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) int8_t L4[NS > 4 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) int8_t L5[NS > 5 ? STAGE : 16];
+  __shared__ int8_t lut_s[256];
+  // the array of pipeline stage u (mod NS), chosen at compile time so that every LDS access has a known array
+  auto arr = [&](auto u) -> int8_t* {
+    constexpr int U = decltype(u)::value % NS;
+    if constexpr (U == 0) return L0;
+    else if constexpr (U == 1) return L1;
+    else if constexpr (U == 2) return L2;
+    else if constexpr (U == 3) return L3;
+    else if constexpr (U == 4) return L4;
+    else return L5;
+  };
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int half = lane >> 5, l32 = lane & 31;
+
+  const int per_batch = g.tiles_m * g.tiles_n, total = per_batch * g.nbatch;
+  const int per_xcd = gridDim.x >> 3, xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int chunk = (total + 7) >> 3, lo_t = xcd * chunk, hi_t = min(total, lo_t + chunk);
+  const int in_group = GROUP_M * g.tiles_n;
+  struct Tile {
+    int m0, n0, b0, b1;
+    bool valid;
+  };
+  auto tile_of = [&](int it) {
+    Tile T;
+    const int L = lo_t + it * per_xcd + slot;
+    T.valid = L < hi_t;
+    const int b = T.valid ? L / per_batch : 0, pid = T.valid ? L % per_batch : 0;
+    const int first_m = (pid / in_group) * GROUP_M;
+    const int gsize = min(g.tiles_m - first_m, GROUP_M);
+    T.m0 = (first_m + (pid % in_group) % gsize) * BM;
+    T.n0 = ((pid % in_group) / gsize) * BN;
+    T.b0 = b / g.batch1;
+    T.b1 = b % g.batch1;
+    return T;
+  };
+  // an invalid tile gets empty descriptors: its loads read zeros and are never used
+  auto rsrc_a = [&](const Tile& T) {
+    return uniform_rsrc(g.A + T.b0 * g.sa0 + T.b1 * g.sa1 + (long long)T.m0 * g.lda,
+                        T.valid ? (int)(min(g.M - T.m0, BM) * g.lda) : 0);
+  };
+  auto rsrc_b = [&](const Tile& T) {
+    return uniform_rsrc(g.B + T.b0 * g.sb0 + T.b1 * g.sb1 + (long long)T.n0 * g.ldb,
+                        T.valid ? (int)(min(g.N - T.n0, BN) * g.ldb) : 0);
+  };
+
+  Tile cur = tile_of(0);
+  if (!cur.valid) return;
+  if (g.lut && t < 256) lut_s[t] = g.lut[t];
+
+  unsigned offa[JA], offb[JB];
+  int ka[JA], kb[JB];
+#pragma unroll
+  for (int j = 0; j < JA; ++j) {
+    const int P = (wave + NW * j) * 64 + lane, row = P / CPR, c = swz<BK>(row, P % CPR);
+    offa[j] = (unsigned)(row * g.lda + c * 16);
+    ka[j] = c * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    const int P = (wave + NW * j) * 64 + lane, row = P / CPR, c = swz<BK>(row, P % CPR);
+    offb[j] = (unsigned)(((row & ~31) | bperm(row & 31)) * g.ldb + c * 16);
+    kb[j] = c * 16;
+  }
+  const int K = g.K;
+  auto issue = [&](int8_t* arr, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int k0) {
+#pragma unroll
+    for (int j = 0; j < JA; ++j) dma16(ra, arr + (wave + NW * j) * 1024, k0 + ka[j] < K ? offa[j] + k0 : OOB);
+#pragma unroll
+    for (int j = 0; j < JB; ++j) dma16(rb, arr + BM * BK + (wave + NW * j) * 1024, k0 + kb[j] < K ? offb[j] + k0 : OOB);
+  };
+
+  v16i acc[TN][TM];
+  v4i af[2][TM], bf[2][TN];
+  auto load_frags = [&](int set, const int8_t* arr, int ks) {
+    const int ch = ks * 2 + half;
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int r = wm * WM + j * 32 + l32;
+      af[set][j] = *reinterpret_cast<const v4i*>(arr + r * BK + (swz<BK>(r, ch) << 4));
+    }
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+      const int r = wn * WN + i * 32 + l32;
+      bf[set][i] = *reinterpret_cast<const v4i*>(arr + BM * BK + r * BK + (swz<BK>(r, ch) << 4));
+    }
+  };
+  auto mm = [&](int set) {
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[set][i], af[set][j], acc[i][j], 0, 0, 0);
+  };
+  const int nk = (K + BK - 1) / BK;
+  __amdgpu_buffer_rsrc_t ra = rsrc_a(cur), rb = rsrc_b(cur);
+  // one pipeline step, as in gemm_i8_fast; stage kt + 2 belongs to the next tile once it passes this tile's K
+  auto step = [&](int kt, const int8_t* curA, int8_t* nxt, const int8_t* next, __amdgpu_buffer_rsrc_t ran,
+                  __amdgpu_buffer_rsrc_t rbn) {
+    const bool over = kt + NS - 1 >= nk;
+    issue(nxt, over ? ran : ra, over ? rbn : rb, (over ? kt + NS - 1 - nk : kt + NS - 1) * BK);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < KS - 1; ++ks) {
+      load_frags((ks + 1) & 1, curA, ks + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mm(ks & 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vm_lgkm0<(NS - 2) * G>();
+    stage_barrier();
+    load_frags(0, next, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mm((KS - 1) & 1);
+  };
+
+  static_for<NS - 1>([&](auto u) { issue(arr(u), ra, rb, decltype(u)::value * BK); });
+  wait_vm_lgkm0<(NS - 2) * G>();
+  stage_barrier();
+  load_frags(0, L0, 0);
+  for (int it = 0;; ++it) {
+    const Tile nt = tile_of(it + 1);
+    const __amdgpu_buffer_rsrc_t ran = rsrc_a(nt), rbn = rsrc_b(nt);
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    for (int kt = 0; kt < nk; kt += NS) {
+      static_for<NS>([&](auto u) {
+        constexpr int U = decltype(u)::value;
+        step(kt + U, arr(u), arr(std::integral_constant<int, U + NS - 1>{}), arr(std::integral_constant<int, U + 1>{}),
+             ran, rbn);
+      });
+    }
+    direct_epilogue<BM, BN, WM, WN, TM, TN, OSZ, MUL24>(g, acc, lut_s, cur.m0 + wm * WM + l32,
+                                                        cur.n0 + wn * WN + 16 * half, cur.m0, cur.n0, cur.b0, cur.b1);
+    if (!nt.valid) break;
+    cur = nt;
+    ra = ran;
+    rb = rbn;
+  }
+  wait_vmcnt(0);   // the trailing zero loads land in LDS before the workgroup's LDS is released
+}
+
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <int BM, int BN, int BK, int NS, bool MUL24, int NW = 4, int WGN = 2>
+static void launch_persist(GemmArgs& g, int osz, int batch, int num_cu, hipStream_t s) {
+  g.tiles_m = (g.M + BM - 1) / BM;
+  g.tiles_n = (g.N + BN - 1) / BN;
+  g.nbatch = batch;
+  const long long total = (long long)g.tiles_m * g.tiles_n * batch;
+  const int slots = 8 * ((num_cu * persist_occupancy<BM, BN, BK, NS>()) / 8);
+  const int nwg = (int)std::min<long long>(slots, 8 * ((total + 7) / 8));
+  if (osz == 1)
+    hipLaunchKernelGGL((gemm_i8_persist<BM, BN, BK, NS, NW, WGN, 1, MUL24>), dim3(nwg), dim3(NW * 64), 0, s, g);
+  else
+    hipLaunchKernelGGL((gemm_i8_persist<BM, BN, BK, NS, NW, WGN, 2, MUL24>), dim3(nwg), dim3(NW * 64), 0, s, g);
+}
 
 template <int BM, int BN, int WGM, int NS, bool MUL24>
 static void launch_fast(GemmArgs& g, int osz, int batch, hipStream_t s) {
@@ -642,8 +952,12 @@ static void launch_fast(GemmArgs& g, int osz, int batch, hipStream_t s) {
 }
 
 template <bool MUL24>
-static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s, int cfg) {
+static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s, int cfg, int num_cu) {
+  // the persistent 256 x 256 kernel: one workgroup of 8 waves per CU, four 32 KiB LDS stages, wave tiles 64 x 128
+  const bool persist_ok = g.causal == 0 && ((g.K + 63) / 64) % 4 == 0;
+  auto persist = [&] { launch_persist<256, 256, 64, 4, MUL24, 8, 2>(g, osz, batch, num_cu, s); };
   switch (cfg) {
+    case 39: if (persist_ok) return persist(); break;
     case 11: return launch_fast<256, 256, 2, 3, MUL24>(g, osz, batch, s);
     case 12: return launch_fast<256, 256, 2, 4, MUL24>(g, osz, batch, s);
     case 13: return launch_fast<128, 128, 2, 3, MUL24>(g, osz, batch, s);
@@ -653,9 +967,12 @@ static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s,
     case 17: return launch_fast<128, 256, 2, 3, MUL24>(g, osz, batch, s);
     default: break;
   }
-  // measured on MI355X (block GEMM shapes, K 768 and 3072): 256 x 128 tiles with three LDS stages (72 KiB) and at
-  // most 256 registers a lane run two workgroups per CU, which hide each other's pipeline fill and epilogue, at 2/3
-  // of the 128 x 128 tile's L2 traffic per MFMA; small problems keep the 128 x 128 tile (more workgroups)
+  // measured on MI355X (block GEMM shapes, K 768 and 3072): wide products with at least six 256 x 256 tiles per CU
+  // take the persistent kernel (it halves the L2 traffic per MFMA of the 256 x 128 tile); 256 x 128 tiles with three
+  // LDS stages (72 KiB) run two workgroups per CU, which hide each other's pipeline fill and epilogue; small problems
+  // keep the 128 x 128 tile (more workgroups)
+  const long long tiles256 = (long long)((g.M + 255) / 256) * ((g.N + 255) / 256) * batch;
+  if (persist_ok && g.N >= 2048 && tiles256 >= 6ll * num_cu) return persist();
   if ((long long)g.M * g.N * batch >= 256ll * 128 * 512 && g.M >= 256 && g.N >= 128)
     launch_fast<256, 128, 2, 3, MUL24>(g, osz, batch, s);
   else
@@ -789,9 +1106,9 @@ static int gemm_entry(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C
   }
   if (fast) {
     if (flags & ANVIL_GEMM_MUL24)
-      launch_fast_by_shape<true>(g, osz, batch0 * batch1, ctx->stream, ctx->gemm_cfg);
+      launch_fast_by_shape<true>(g, osz, batch0 * batch1, ctx->stream, ctx->gemm_cfg, ctx->num_cu);
     else
-      launch_fast_by_shape<false>(g, osz, batch0 * batch1, ctx->stream, ctx->gemm_cfg);
+      launch_fast_by_shape<false>(g, osz, batch0 * batch1, ctx->stream, ctx->gemm_cfg, ctx->num_cu);
   } else {
     launch_gemm(g, checked, osz, vec, batch0 * batch1, ctx->stream, ctx->gemm_cfg);
   }

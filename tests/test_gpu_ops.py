@@ -314,3 +314,38 @@ def test_gemm_with_fused_residual_add(dev, M, K, N, store_y):
     assert np.array_equal(d.download((M, N), np.int8).astype(np.int64), want)
     if store_y:
         assert np.array_equal(c.download((M, N), np.int8).astype(np.int64), y)
+
+
+@pytest.mark.parametrize("M,N,K,dtype,lut,add", [(32768, 3072, 768, "i8", True, False),
+                                                 (49115, 2080, 768, "i16", False, False),
+                                                 (32768, 3072, 3072, "i8", False, False),
+                                                 (32768, 3072, 768, "i8", False, True)])
+def test_gemm_wide_products_take_the_persistent_kernel(dev, M, N, K, dtype, lut, add):
+    """Products with N >= 2048 and at least six 256 x 256 tiles per CU run on the persistent kernel (register epilogue,
+    permuted B rows). Checked on sampled rows, the first and last 256 among them (edge rows and columns included)."""
+    rng = np.random.default_rng([41, M, N, K])
+    a, w = rng.integers(-128, 128, (M, K), dtype=np.int8), rng.integers(-128, 128, (K, N), dtype=np.int8)
+    rows = np.unique(np.concatenate([np.arange(256), np.arange(M - 256, M), rng.integers(0, M, 512)]))
+    acc = a[rows].astype(np.int64) @ w.astype(np.int64)
+    s = 20
+    m = int(min(((1 << 31) - 1 - (1 << (s - 1))) // int(np.abs(acc).max() * 2), (1 << 23) - 1))
+    L = rng.integers(-128, 128, 256) if lut else None
+    flags = rt.GEMM_UNCHECKED | rt.GEMM_MUL24
+    wt = np.ascontiguousarray(w.T)
+    c = dev.alloc(M * N * rt.ITEMSIZE[dtype])
+    st = [0, 0, K, 0, 0, K, 0, 0, N]
+    y = sem.qmatmul(a[rows].astype(np.int64), w.astype(np.int64), m, s, L, dtype=dtype)
+    if add:
+        r = rng.integers(-128, 128, (M, N), dtype=np.int8)
+        d = dev.alloc(M * N)
+        dev.gemm_i8_add(up(dev, a, "i8"), up(dev, wt, "i8"), c, 1, 1, M, N, K, st, m, s, None, up(dev, r, "i8"), 300,
+                        -200, 9, d, [0, 0, N, 0, 0, N], flags)
+    else:
+        dev.gemm_i8(up(dev, a, "i8"), up(dev, wt, "i8"), c, 1, 1, M, N, K, st, m, s,
+                    None if L is None else up(dev, L, "i8"), dtype, flags)
+    dev.sync()
+    got = c.download((M, N), rt.NP_DTYPE[dtype])[rows].astype(np.int64)
+    assert np.array_equal(got, y), np.argwhere(got != y)[:5]
+    if add:
+        want = sem.add_requant(r[rows].astype(np.int64), y, 300, -200, 9)
+        assert np.array_equal(d.download((M, N), np.int8)[rows].astype(np.int64), want)
