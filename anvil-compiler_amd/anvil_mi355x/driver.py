@@ -304,9 +304,13 @@ class CompiledModel:
                 lut = self._const_views[op.lut] if op.lut in self._const_views else dense(views[op.lut], label)
                 w = dense(views[op.w], label + ".w")
                 rows = math.prod(x.dims[:-1])
+                flags = rt.OP_UNCHECKED if self.proven else 0
+                lut_vals = self._const_array(op.lut)
+                if flags and lut_vals is not None and int(np.abs(lut_vals).max()) * abs(int(op.M)) < (1 << 23):
+                    flags |= rt.RMS_S24                          # x w (lut M) + rnd as one 24-bit multiply-add
                 step(label, _call_ptrs, dev.rmsnorm_int, [x, g.qt(op.x).dtype, w, lut, lut.size, int(op.M),
                                                           int(op.s), op.ss_shift_int, op.ss_init_int, rows,
-                                                          x.dims[-1], out, rt.OP_UNCHECKED if self.proven else 0])
+                                                          x.dims[-1], out, flags])
             elif isinstance(op, g.AddRequantOp):
                 a = dense(views[op.a], label + ".a")
                 b = dense(views[op.b], label + ".b")

@@ -53,13 +53,6 @@ constexpr int A_THREADS = 256;
 
 __device__ __forceinline__ int sbyte(unsigned v, int e) { return (int)(int8_t)(v >> (8 * e)); }
 
-// low bytes of four ints -> one dword (three v_perm_b32)
-__device__ __forceinline__ unsigned pack4(int v0, int v1, int v2, int v3) {
-  const unsigned t01 = __builtin_amdgcn_perm((unsigned)v1, (unsigned)v0, 0x0c0c0400u);
-  const unsigned t23 = __builtin_amdgcn_perm((unsigned)v3, (unsigned)v2, 0x0c0c0400u);
-  return __builtin_amdgcn_perm(t23, t01, 0x05040100u);
-}
-
 // One 16-byte chunk of a K-contiguous operand row; zero past the head dim.
 template <int D>
 __device__ __forceinline__ v4i chunk16(const int8_t* row, int chunk) {

@@ -65,6 +65,13 @@ __device__ __forceinline__ void static_for(F&& f) {
 // consecutive rows of its column.
 __device__ __forceinline__ int bperm(int c) { return 16 * ((c >> 2) & 1) + 4 * (c >> 3) + (c & 3); }
 
+// the low bytes of four ints, in order, as one dword
+__device__ __forceinline__ unsigned pack4(int v0, int v1, int v2, int v3) {
+  const unsigned t01 = __builtin_amdgcn_perm((unsigned)v1, (unsigned)v0, 0x0c0c0400u);
+  const unsigned t23 = __builtin_amdgcn_perm((unsigned)v3, (unsigned)v2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+}
+
 constexpr long long I32_MIN = -(1ll << 31);
 constexpr long long I32_MAX = (1ll << 31) - 1;
 

@@ -349,11 +349,6 @@ __device__ __forceinline__ void requant16(const v16i& a, int mult, int rnd, int 
   }
 }
 
-__device__ __forceinline__ unsigned pack4_i8(int a, int b, int c, int d) {
-  const unsigned t01 = __builtin_amdgcn_perm((unsigned)b, (unsigned)a, 0x0c0c0400u);
-  const unsigned t23 = __builtin_amdgcn_perm((unsigned)d, (unsigned)c, 0x0c0c0400u);
-  return __builtin_amdgcn_perm(t23, t01, 0x05040100u);
-}
 
 // Epilogue from registers: tile (i, j) of this lane is row mrow + 32 j, columns ncol + 32 i .. + 15. Interior tiles
 // issue every residual load first, then requantize and store 16 bytes a lane; edge tiles store element by element.
@@ -397,7 +392,7 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
                 const int r = (int)(int8_t)((unsigned)rv[j][i][q] >> (8 * e));
                 o[e] = min(max((r * ma + v[4 * q + e] * mb + rnd2) >> sh2, -128), 127);   // proven inside int32
               }
-              ov[q] = (int)pack4_i8(o[0], o[1], o[2], o[3]);
+              ov[q] = (int)pack4(o[0], o[1], o[2], o[3]);
             }
             *reinterpret_cast<v4i*>(Db + (long long)m * g.ldd + n) = ov;
             if (!g.store_y) continue;
@@ -405,7 +400,7 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
           if (OSZ == 1) {
             v4i w;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) w[q] = (int)pack4_i8(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            for (int q = 0; q < 4; ++q) w[q] = (int)pack4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
             *reinterpret_cast<v4i*>(Cb + (long long)m * g.ldc + n) = w;
           } else {
             v4i w0, w1;

@@ -130,6 +130,10 @@ __global__ __launch_bounds__(R_THREADS) void softmax_fast(const int8_t* __restri
 // each dword with itself.
 constexpr int RMS_ROWS = 4;
 
+// S24: every |lut[i] * mult| is below 2^23 (host-checked), so x w (lut[i] mult) + rnd -- the same integer as
+// x w lut[i] mult + rnd, which is proven to fit int32 -- is one 24-bit multiply-add per element, with lut[i] mult
+// formed once per row; otherwise two 32-bit multiplies per element.
+template <bool S24>
 __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
                                                            const int* __restrict__ lut, int lut_len, int mult,
                                                            int shift, long long rows, int cols,
@@ -139,6 +143,9 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
   const bool active = lane < chunks;
   v4i wv = {0, 0, 0, 0};
   if (active) wv = *reinterpret_cast<const v4i*>(w + 16 * lane);
+  int wb[16];                                                   // this lane's 16 weights, sign-extended once
+#pragma unroll
+  for (int b = 0; b < 16; ++b) wb[b] = sbyte(wv, b);
   const long long step = (long long)gridDim.x * R_WAVES * RMS_ROWS;
   for (long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * RMS_ROWS; row0 < rows;
        row0 += step) {
@@ -170,14 +177,18 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
     for (int j = 0; j < RMS_ROWS; ++j) {
       if (!active || row0 + j >= rows) continue;
       const int rnd = sh[j] ? (1 << (sh[j] - 1)) : 0;
-      unsigned ov[4] = {0, 0, 0, 0};
+      const int rm = S24 ? r[j] * mult : 0;
+      int v[16];
 #pragma unroll
       for (int b = 0; b < 16; ++b) {
-        const int xwr = sbyte(xv[j], b) * sbyte(wv, b) * r[j];   // proven: x w r and x w r M + rnd fit int32
-        const int v = min(max((xwr * mult + rnd) >> sh[j], -128), 127);
-        ov[b >> 2] |= (unsigned)(v & 255) << (8 * (b & 3));
+        const int xw = sbyte(xv[j], b) * wb[b];
+        // proven: x w r and x w r M + rnd fit int32
+        const int acc = S24 ? __mul24(xw, rm) + rnd : xw * r[j] * mult + rnd;
+        v[b] = min(max(acc >> sh[j], -128), 127);
       }
-      *reinterpret_cast<v4i*>(out + (row0 + j) * cols + 16 * lane) = v4i{(int)ov[0], (int)ov[1], (int)ov[2], (int)ov[3]};
+      *reinterpret_cast<v4i*>(out + (row0 + j) * cols + 16 * lane) =
+          v4i{(int)pack4(v[0], v[1], v[2], v[3]), (int)pack4(v[4], v[5], v[6], v[7]),
+              (int)pack4(v[8], v[9], v[10], v[11]), (int)pack4(v[12], v[13], v[14], v[15])};
     }
   }
 }
@@ -301,16 +312,23 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
   if (shift < 0 || shift > 31) return set_error(ANVIL_E_VALUE, "shift %d outside [0, 31]", shift);
   if (ss_shift < 0 || ss_shift > 30) return set_error(ANVIL_E_VALUE, "ss_shift %d outside [0, 30]", ss_shift);
   if (ss_init < 0) return set_error(ANVIL_E_VALUE, "ss_init %d negative", ss_init);
-  if (flags & ~ANVIL_OP_UNCHECKED) return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: unknown flags %d", flags);
+  if (flags & ~(ANVIL_OP_UNCHECKED | ANVIL_RMS_S24))
+    return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: unknown flags %d", flags);
+  if ((flags & ANVIL_RMS_S24) && !(flags & ANVIL_OP_UNCHECKED))
+    return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: ANVIL_RMS_S24 needs ANVIL_OP_UNCHECKED");
   if (int r = check_ctx(ctx)) return r;
   if (rows == 0) return ANVIL_OK;
   const long long blocks = (rows + R_WAVES - 1) / R_WAVES;
   if (blocks > (1ll << 31) - 1) return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: too many rows");
   if ((flags & ANVIL_OP_UNCHECKED) && x_dtype == ANVIL_I8 && ss_shift == 0 && ss_init == 0 && cols % 16 == 0 &&
       cols <= 1024 && al16(x) && al16(w) && al16(out)) {
-    hipLaunchKernelGGL(rmsnorm_fast, dim3(row_grid((rows + RMS_ROWS - 1) / RMS_ROWS, ctx->num_cu)), dim3(R_THREADS), 0,
-                       ctx->stream,
-                       (const int8_t*)x, w, lut, lut_len, mult, shift, (long long)rows, cols, out);
+    const dim3 grid(row_grid((rows + RMS_ROWS - 1) / RMS_ROWS, ctx->num_cu));
+    if (flags & ANVIL_RMS_S24)
+      hipLaunchKernelGGL(rmsnorm_fast<true>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
+                         mult, shift, (long long)rows, cols, out);
+    else
+      hipLaunchKernelGGL(rmsnorm_fast<false>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
+                         mult, shift, (long long)rows, cols, out);
   } else if (x_dtype == ANVIL_I8) {
     hipLaunchKernelGGL(rmsnorm_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
                        (const int8_t*)x, w, lut, lut_len, mult, shift, ss_shift, ss_init, (long long)rows, cols, out,

@@ -119,7 +119,10 @@ int anvil_rmsnorm_int(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* 
  *                       without the 64-bit range checks; without the flag, violations are reported by anvil_sync. */
 enum anvil_op_flags { ANVIL_OP_UNCHECKED = 1 };
 
-/* anvil_rmsnorm_int with flags (same reference op, anvil/semantics.py:158-182). */
+/* anvil_rmsnorm_int with flags (same reference op, anvil/semantics.py:158-182). ANVIL_RMS_S24 (with
+ * ANVIL_OP_UNCHECKED) adds that every |lut[i] * mult| is below 2^23: each element's x w lut[i] mult + rnd is then one
+ * 24-bit multiply-add. */
+enum anvil_rms_flags { ANVIL_RMS_S24 = 2 };
 int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* w, const int32_t* lut,
                          int lut_len, int32_t mult, int shift, int ss_shift, int32_t ss_init, int64_t rows, int cols,
                          int8_t* out, int flags);

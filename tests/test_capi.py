@@ -97,3 +97,15 @@ def test_attention_argument_validation_precedes_the_device():
         att(64, 64, 127, 1, bad)
     with pytest.raises(ValueError, match="null context"):
         att(64, 64, 127, 1)
+
+
+def test_rmsnorm_flag_validation_precedes_the_device():
+    lib = rt.library()
+    p = C.c_void_p(4096)
+    rms = lambda flags: lib.call("anvil_rmsnorm_int_ex", None, p, 1, p, p, 1024, 1, 14, 0, 0, 4, 768, p, flags)  # noqa: E731
+    with pytest.raises(ValueError, match="unknown flags"):
+        rms(4)
+    with pytest.raises(ValueError, match="needs ANVIL_OP_UNCHECKED"):
+        rms(rt.RMS_S24)
+    with pytest.raises(ValueError, match="null context"):
+        rms(rt.OP_UNCHECKED | rt.RMS_S24)

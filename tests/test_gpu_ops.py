@@ -111,17 +111,19 @@ def _rms(dev, x, xdt, w, lut, m, s, c=0, e=0, flags=0):
     return out.download((rows, d), np.int8).astype(np.int64)
 
 
-@pytest.mark.parametrize("flags", [0, rt.OP_UNCHECKED])
+@pytest.mark.parametrize("flags", [0, rt.OP_UNCHECKED, rt.OP_UNCHECKED | rt.RMS_S24])
 @pytest.mark.parametrize("d", [8, 64, 256, 768, 1000, 1024])
 def test_rmsnorm_i8(dev, d, flags):
-    """flags=UNCHECKED selects the one-wave-per-row dot4 kernel where d is a multiple of 16 up to 1024 (the
-    proof's bounds hold for m = 1 and these LUTs); results are the same bits either way."""
+    """flags=UNCHECKED selects the dot4 kernel with four rows a wave where d is a multiple of 16 up to 1024 (the
+    proof's bounds hold for m = 1 and these LUTs), RMS_S24 its 24-bit multiply-add (every |lut m| < 2^23 here);
+    results are the same bits either way."""
     rng = np.random.default_rng([6, d])
     w = rng.integers(-127, 128, d)
     lut, s = Q.rmsnorm_lut(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
     x = np.concatenate([rng.integers(-128, 128, (200, d)), np.full((1, d), -128), np.zeros((1, d), int),
                         np.full((1, d), 127), np.rint(rng.standard_normal((50, d)) * 3).astype(int)])
     want = sem.rmsnorm_int(x, w, lut, 1, s)
+    assert int(np.abs(lut).max()) < (1 << 23)
     assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s, flags=flags), want)
 
 
