@@ -1,6 +1,8 @@
 // Row reductions of the graph: rmsnorm_int and softmax_lut. One wavefront (64 lanes) per row; the row
 // statistics (sum of squares, max, exp sum) are reduced across the wave with DPP-backed shuffles, so every lane
 // ends with the same exact integer and the per-element pass needs no LDS round trip.
+#include <algorithm>
+
 #include "common.h"
 
 namespace anvil {
@@ -147,14 +149,22 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
 #pragma unroll
   for (int b = 0; b < 16; ++b) wb[b] = sbyte(wv, b);
   const long long step = (long long)gridDim.x * R_WAVES * RMS_ROWS;
-  for (long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * RMS_ROWS; row0 < rows;
-       row0 += step) {
-    v4i xv[RMS_ROWS];
+  // the next group's rows are loaded while this group's are requantized and stored
+  auto load = [&](long long r0, v4i* xv) {
 #pragma unroll
     for (int j = 0; j < RMS_ROWS; ++j) {
       xv[j] = v4i{0, 0, 0, 0};
-      if (active && row0 + j < rows) xv[j] = *reinterpret_cast<const v4i*>(x + (row0 + j) * cols + 16 * lane);
+      if (active && r0 + j < rows) xv[j] = *reinterpret_cast<const v4i*>(x + (r0 + j) * cols + 16 * lane);
     }
+  };
+  long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * RMS_ROWS;
+  v4i xn[RMS_ROWS];
+  load(row0, xn);
+  for (; row0 < rows; row0 += step) {
+    v4i xv[RMS_ROWS];
+#pragma unroll
+    for (int j = 0; j < RMS_ROWS; ++j) xv[j] = xn[j];
+    load(row0 + step, xn);
     int idx[RMS_ROWS], sh[RMS_ROWS];
 #pragma unroll
     for (int j = 0; j < RMS_ROWS; ++j) {
@@ -322,7 +332,9 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
   if (blocks > (1ll << 31) - 1) return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: too many rows");
   if ((flags & ANVIL_OP_UNCHECKED) && x_dtype == ANVIL_I8 && ss_shift == 0 && ss_init == 0 && cols % 16 == 0 &&
       cols <= 1024 && al16(x) && al16(w) && al16(out)) {
-    const dim3 grid(row_grid((rows + RMS_ROWS - 1) / RMS_ROWS, ctx->num_cu));
+    // four workgroups per CU, each wave walking row groups with the next group's loads in flight
+    const long long groups = (rows + RMS_ROWS - 1) / RMS_ROWS;
+    const dim3 grid((unsigned)std::min<long long>((groups + R_WAVES - 1) / R_WAVES, 4ll * ctx->num_cu));
     if (flags & ANVIL_RMS_S24)
       hipLaunchKernelGGL(rmsnorm_fast<true>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
                          mult, shift, (long long)rows, cols, out);
