@@ -101,6 +101,7 @@ class _Plan:
         self.steps: list = []          # (label, fn, args)
         self.works: list = []          # per step: (kind, algorithmic int ops, algorithmic HBM bytes)
         self.fused_adds: set = set()   # add_requant ops computed in a GEMM epilogue
+        self.stage: dict = {}          # device staging buffers of float inputs and token ids
 
     def buf(self, nbytes, name=""):
         b = Buf(nbytes, name)
@@ -144,6 +145,8 @@ class CompiledModel:
             Q.prove_no_overflow(module, self.consts, acc_bounds=self.acc_bounds)
         self.device_index = device
         self.dev = None
+        self.embedding = None             # (wte, wpe) float32 host tables of a token model
+        self._embed_dev = None
         self._const_views = {}
         self._const_bt = {}
         self._plans = {}
@@ -627,6 +630,33 @@ class CompiledModel:
         s = self.scale(sym)
         return np.asarray(ints, dtype=np.float64) * (1.0 if s is None else s)
 
+    def set_embedding(self, wte, wpe):
+        """Token and position tables of a token model (float32 (vocab, C), (>= T, C)); the graph's single input is
+        x = wte[ids] + wpe[positions]."""
+        if len(self.inputs) != 1:
+            raise ValueError("a token embedding needs a graph with exactly one input")
+        wte, wpe = np.asarray(wte, dtype=np.float32), np.asarray(wpe, dtype=np.float32)
+        dims = self.meta[self.inputs[0]][1]
+        if len(dims) != 2 or wte.ndim != 2 or wpe.ndim != 2 or wte.shape[1] != dims[1] or wpe.shape[1] != dims[1] \
+                or wpe.shape[0] < dims[0]:
+            raise ValueError(f"embedding tables {wte.shape}, {wpe.shape} do not fit the input {tuple(dims)}")
+        self.embedding = (np.ascontiguousarray(wte), np.ascontiguousarray(wpe))
+        self._embed_dev = None
+
+    def _bind_tokens(self, ids, batch):
+        """Token ids for the embedding prelude: (T,) or, with batch=True, (batch, T) integers."""
+        if self.embedding is None:
+            raise ValueError("tokens=True needs embedding tables: compile(..., embedding=(wte, wpe))")
+        ids = np.asarray(ids)
+        T = self.meta[self.inputs[0]][1][0]
+        if ids.dtype.kind not in "iu":
+            raise ValueError(f"token ids must be integers, got dtype {ids.dtype}")
+        want = 2 if batch else 1
+        if ids.ndim != want or ids.shape[-1] != T:
+            raise ValueError(f"token ids of shape {ids.shape}: expected {'(batch, ' if batch else '('}{T})")
+        ids = ids.astype(np.int64).reshape(-1, T)
+        return ids, ids.shape[0]
+
     def _bind_inputs(self, x, quantized, batch):
         """Reference driver.py:248-280, plus batch=True: every input has one extra leading batch dim."""
         xs = list(x) if isinstance(x, (list, tuple)) else [x]
@@ -650,9 +680,13 @@ class CompiledModel:
             if quantized:
                 out[sym] = self._check_int_input(sym, v)
             else:
-                if not np.all(np.isfinite(np.asarray(v, dtype=np.float64))):
+                if self.scale(sym) is None:
+                    raise ValueError(f"input {sym!r} has no scale: pass integer inputs with quantized=True")
+                if v.dtype.kind == "f" and not np.all(np.isfinite(v)):
                     raise ValueError(f"input {sym!r} has NaN or infinite values")
-                out[sym] = self.quantize_input(v, sym)
+                # quantized on the device (clamp(rint(x / scale)) in float64, as quantize_input does on the host)
+                out[sym] = _FloatInput(np.ascontiguousarray(v, dtype=np.float32 if v.dtype == np.float32
+                                                            else np.float64))
             if not batch:
                 out[sym] = out[sym][None]
         return out, (nb if batch else 1)
@@ -680,9 +714,38 @@ class CompiledModel:
         return [s for s in dict.fromkeys(syms) if s is not None]
 
     def upload_inputs(self, plan, ints: dict):
+        """Integer inputs, or float inputs (quantized on the device), into the plan's input buffers."""
         for op in self.input_ops:
             v = plan.views[op.result]
-            v.buf.mem.upload(np.ascontiguousarray(ints[op.sym_str]).astype(rt.NP_DTYPE[v.dtype]))
+            x = ints[op.sym_str]
+            if isinstance(x, _FloatInput):
+                f = x.a
+                stage = self._stage(plan, op.sym_str + ".float", f.nbytes)
+                stage.upload(f)
+                self.dev.quantize(stage, f.dtype == np.float64, self.scale(op.sym_str), f.size, v.ptr, v.dtype)
+            else:
+                v.buf.mem.upload(np.ascontiguousarray(x).astype(rt.NP_DTYPE[v.dtype]))
+
+    def upload_tokens(self, plan, ids):
+        """Token ids through the embedding prelude into the input buffer: gather, add and quantize on the device."""
+        if self._embed_dev is None:
+            wte, wpe = self.embedding
+            self._embed_dev = (self.dev.upload(wte), self.dev.upload(wpe), wte.shape[0])
+        wte_d, wpe_d, vocab = self._embed_dev
+        sym = self.inputs[0]
+        v = plan.views[self.input_ops[0].result]
+        T, Cdim = self.meta[sym][1]
+        stage = self._stage(plan, sym + ".ids", ids.nbytes)
+        stage.upload(np.ascontiguousarray(ids, dtype=np.int64))
+        self.dev.embed_quantize(stage, ids.size, T, Cdim, wte_d, vocab, wpe_d, self.scale(sym), v.ptr, v.dtype)
+
+    def _stage(self, plan, key, nbytes):
+        """A device staging buffer of the plan, kept for later runs of the same size."""
+        b = plan.stage.get(key)
+        if b is None or b.nbytes < nbytes:
+            b = self.dev.alloc(max(nbytes, 16))
+            plan.stage[key] = b
+        return b
 
     def launch(self, plan, profile=False):
         """Enqueue every kernel of the plan on the device stream (asynchronous unless profile)."""
@@ -711,17 +774,25 @@ class CompiledModel:
         return out
 
     def run(self, x, backend: str = "mi355x", *, quantized=False, keep="outputs", batch=False, profile=False,
-            **run_kw) -> RunOutput:
-        """Quantize x (unless quantized=True), run the graph on the GPU, read back (reference driver.py:305-322)."""
+            tokens=False, **run_kw) -> RunOutput:
+        """Quantize x (unless quantized=True), run the graph on the GPU, read back (reference driver.py:305-322).
+        Float inputs are quantized on the device. tokens=True: x holds token ids of a model compiled with embedding
+        tables, gathered and quantized on the device."""
         if backend not in BACKENDS:
             raise ValueError(f"unknown backend {backend!r}: {', '.join(BACKENDS)}")
         if run_kw:
             raise TypeError(f"run() got unexpected keyword argument(s) {sorted(run_kw)}")
         syms = self.readable(keep)
-        ints_in, nb = self._bind_inputs(x, quantized, batch)
+        if tokens:
+            ids, nb = self._bind_tokens(x, batch)
+        else:
+            ints_in, nb = self._bind_inputs(x, quantized, batch)
         plan = self.plan(nb, keep)
         with self.dev.lock:
-            self.upload_inputs(plan, ints_in)
+            if tokens:
+                self.upload_tokens(plan, ids)
+            else:
+                self.upload_inputs(plan, ints_in)
             self.dev.record(2)
             times = self.launch(plan, profile)
             self.dev.record(3)
@@ -740,6 +811,16 @@ class CompiledModel:
 
 
 # ------------------------------------------------------------------------------------------ launch helpers
+
+class _FloatInput:
+    """A float input array (float32 or float64, batch dim included) to be quantized on the device."""
+
+    def __init__(self, a):
+        self.a = a
+
+    def __getitem__(self, idx):
+        return _FloatInput(self.a[idx])
+
 
 def _p(v):
     return v.ptr if isinstance(v, View) else v
@@ -817,14 +898,22 @@ def _swap_last2(n):
 
 
 def compile(model, example_inputs=None, calib_inputs=None, params=None, schedules=None, *, consts=None,
-            device: int = 0, prove: bool = True, **kw) -> CompiledModel:   # noqa: A001  (mirrors anvil.compile)
+            device: int = 0, prove: bool = True, embedding=None, **kw) -> CompiledModel:   # noqa: A001
     """anvil.compile for the mi355x backend (reference anvil/driver.py:330-335). params / schedules configure the
     reference's tiny-gpu targets and are ignored here; example_inputs / calib_inputs only apply to torch modules,
     which this backend does not capture. prove=False skips the static int32 proof for a hand-built graph, as the
     reference's graph-level Vortex-V compile does (anvil/vortexv/__init__.py:117-123): every kernel still checks
-    each intermediate on the device, so a run that leaves int32 raises OverflowError like the interpreter."""
+    each intermediate on the device, so a run that leaves int32 raises OverflowError like the interpreter.
+    embedding=(wte, wpe): the token and position tables (float32, (vocab, C) and (>= T, C)) of a token model whose
+    graph input is x = wte[ids] + wpe[positions]; cm.run(ids, tokens=True) then gathers and quantizes on the device.
+    A built token model (models.config(4)) brings its own tables."""
     if kw:
         raise TypeError(f"compile() got unexpected keyword argument(s) {sorted(kw)}")
     module, cs = _resolve_model(model, consts, prove)
     from .models import Built
-    return CompiledModel(module, cs, device=device, proven=prove or isinstance(model, Built))
+    cm = CompiledModel(module, cs, device=device, proven=prove or isinstance(model, Built))
+    if embedding is None and isinstance(model, Built) and model.spec.vocab:
+        embedding = (model.params["wte"], model.params["wpe"])
+    if embedding is not None:
+        cm.set_embedding(*embedding)
+    return cm

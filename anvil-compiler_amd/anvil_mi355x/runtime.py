@@ -60,6 +60,7 @@ SIGNATURES = {
     "anvil_lut_mul": [_p, _p, _p, _p, _i32, _i, _i64, _p],
     "anvil_copy_strided": [_p, _p, _p, _i, _i, _p, _p],
     "anvil_quantize": [_p, _p, _i, _f64, _i64, _p, _i],
+    "anvil_embed_quantize": [_p, _p, _i64, _i, _i, _p, _i, _p, _f64, _p, _i],
 }
 
 _lib = None
@@ -229,6 +230,11 @@ class Device:
     def quantize(self, x, x_is_f64, scale, n, out, out_dtype):
         self.lib.call("anvil_quantize", self.ctx, C.c_void_p(_ptr(x)), int(bool(x_is_f64)), float(scale), n,
                       C.c_void_p(_ptr(out)), DTYPE_CODE[out_dtype])
+
+    def embed_quantize(self, ids, rows, T, Cdim, wte, vocab, wpe, scale, out, out_dtype):
+        self.lib.call("anvil_embed_quantize", self.ctx, C.c_void_p(_ptr(ids)), int(rows), int(T), int(Cdim),
+                      C.c_void_p(_ptr(wte)), int(vocab), C.c_void_p(_ptr(wpe)), float(scale), C.c_void_p(_ptr(out)),
+                      DTYPE_CODE[out_dtype])
 
 
 _devices = {}

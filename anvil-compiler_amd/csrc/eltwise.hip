@@ -1,5 +1,7 @@
 // Elementwise graph ops (add_requant, lut, lut_mul), the strided copy that materialises a layout view, and
 // input quantization. All are HBM-bound grid-stride loops; LUTs are staged in LDS once per workgroup.
+#include <cmath>
+
 #include "common.h"
 
 namespace anvil {
@@ -85,6 +87,31 @@ __global__ __launch_bounds__(E_THREADS) void quantize_kernel(const TI* __restric
                                                               TO* __restrict__ out, int lo, int hi) {
   for (long long i = (long long)blockIdx.x * E_THREADS + threadIdx.x; i < n; i += (long long)gridDim.x * E_THREADS) {
     double v = rint((double)x[i] / scale);
+    v = v < lo ? lo : (v > hi ? hi : v);
+    out[i] = (TO)v;
+  }
+}
+
+// the float prelude of a token model: out[r][c] = clamp_out(rint((wte[ids[r]][c] + wpe[r % T][c]) / scale)), the
+// float32 tables read as float64, as the host computes x = wte[ids] + wpe[positions] in float64 and quantizes it
+template <typename TO>
+__global__ __launch_bounds__(E_THREADS) void embed_quantize_kernel(const int64_t* __restrict__ ids,
+                                                                   const float* __restrict__ wte,
+                                                                   const float* __restrict__ wpe, long long rows,
+                                                                   int T, int C, int vocab, double scale,
+                                                                   TO* __restrict__ out, int lo, int hi,
+                                                                   unsigned* flags) {
+  const long long n = rows * C;
+  for (long long i = (long long)blockIdx.x * E_THREADS + threadIdx.x; i < n; i += (long long)gridDim.x * E_THREADS) {
+    const long long r = i / C;
+    const int c = (int)(i - r * C);
+    const long long id = ids[r];
+    if (id < 0 || id >= vocab) {
+      raise_flag(flags, FLAG_RANGE);
+      out[i] = 0;
+      continue;
+    }
+    double v = rint(((double)wte[id * C + c] + (double)wpe[(r % T) * C + c]) / scale);
     v = v < lo ? lo : (v > hi ? hi : v);
     out[i] = (TO)v;
   }
@@ -207,6 +234,30 @@ int anvil_quantize(anvil_ctx* ctx, const void* x, int x_is_f64, double scale, in
   else
     hipLaunchKernelGGL((quantize_kernel<float, int16_t>), gr, bl, 0, ctx->stream, (const float*)x, scale,
                        (long long)n, (int16_t*)out, lo, hi);
+  ANVIL_LAUNCHED();
+  return ANVIL_OK;
+}
+
+int anvil_embed_quantize(anvil_ctx* ctx, const int64_t* ids, int64_t rows, int T, int C, const float* wte,
+                         int vocab, const float* wpe, double scale, void* out, int out_dtype) {
+  if (!ids || !wte || !wpe || !out) return set_error(ANVIL_E_VALUE, "anvil_embed_quantize: null pointer");
+  if (rows < 0 || T < 1 || C < 1 || vocab < 1 || rows % T)
+    return set_error(ANVIL_E_VALUE, "anvil_embed_quantize: rows %lld must be a multiple of T %d (C %d, vocab %d)",
+                     (long long)rows, T, C, vocab);
+  if (!(scale > 0) || scale == HUGE_VAL) return set_error(ANVIL_E_VALUE, "anvil_embed_quantize: scale must be > 0");
+  if (out_dtype != ANVIL_I8 && out_dtype != ANVIL_I16)
+    return set_error(ANVIL_E_VALUE, "anvil_embed_quantize: result dtype must be i8 or i16");
+  if (rows * C / C != rows) return set_error(ANVIL_E_VALUE, "anvil_embed_quantize: size overflow");
+  if (int r = check_ctx(ctx)) return r;
+  if (rows == 0) return ANVIL_OK;
+  const long long n = rows * C;
+  const int lo = dtype_lo(out_dtype), hi = dtype_hi(out_dtype);
+  if (out_dtype == ANVIL_I8)
+    hipLaunchKernelGGL(embed_quantize_kernel<int8_t>, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, ids, wte, wpe,
+                       (long long)rows, T, C, vocab, scale, (int8_t*)out, lo, hi, ctx->flags);
+  else
+    hipLaunchKernelGGL(embed_quantize_kernel<int16_t>, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, ids, wte,
+                       wpe, (long long)rows, T, C, vocab, scale, (int16_t*)out, lo, hi, ctx->flags);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }

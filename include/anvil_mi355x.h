@@ -175,6 +175,14 @@ int anvil_copy_strided(anvil_ctx* ctx, const void* src, void* dst, int elem_size
  * to even, x float32 or float64 (x_is_f64), out ANVIL_I8 or ANVIL_I16. */
 int anvil_quantize(anvil_ctx* ctx, const void* x, int x_is_f64, double scale, int64_t n, void* out, int out_dtype);
 
+/* The float prelude of a token model, on the device: rows = batch * T token ids (int64), float32 tables wte
+ * (vocab, C) and wpe (>= T, C); out[r][c] = clamp_out(rint((wte[ids[r]][c] + wpe[r % T][c]) / scale)) in float64,
+ * round half to even, ANVIL_I8 or ANVIL_I16. It replaces the host's x = wte[ids] + wpe[positions] (float64) followed
+ * by CompiledModel.quantize_input (reference anvil/driver.py:233-241). An id outside [0, vocab) is reported by
+ * anvil_sync as ANVIL_E_VALUE. */
+int anvil_embed_quantize(anvil_ctx* ctx, const int64_t* ids, int64_t rows, int T, int C, const float* wte, int vocab,
+                         const float* wpe, double scale, void* out, int out_dtype);
+
 #ifdef __cplusplus
 }
 #endif

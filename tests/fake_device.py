@@ -182,3 +182,26 @@ class FakeDevice:
         dt = {1: "i8", 2: "i16", 4: "i32"}[elem_size]
         v = self.view(src, dt, dims, src_strides).copy()
         self.store(dst, dt, dims, [int(np.prod(dims[i + 1:])) for i in range(len(dims))], v)
+
+    def _raw(self, ptr, dtype, n):
+        ptr = ptr.ptr if hasattr(ptr, "ptr") else int(ptr)
+        return self.heap[ptr - BASE:ptr - BASE + n * np.dtype(dtype).itemsize].view(dtype)
+
+    def quantize(self, x, x_is_f64, scale, n, out, out_dtype):
+        """clamp(rint(float64(x) / scale)), as the host's quantize_input."""
+        self.calls.append(("quantize", n, bool(x_is_f64)))
+        v = self._raw(x, np.float64 if x_is_f64 else np.float32, n).astype(np.float64)
+        lo, hi = {"i8": (-128, 127), "i16": (-32768, 32767)}[out_dtype]
+        self.store(out, out_dtype, (n,), (1,), np.clip(np.rint(v / scale), lo, hi))
+
+    def embed_quantize(self, ids, rows, T, Cdim, wte, vocab, wpe, scale, out, out_dtype):
+        self.calls.append(("embed", rows, T, Cdim))
+        idv = self._raw(ids, np.int64, rows)
+        if idv.size and (idv.min() < 0 or idv.max() >= vocab):
+            self.flags = ValueError
+            return
+        te = self._raw(wte, np.float32, vocab * Cdim).reshape(vocab, Cdim).astype(np.float64)
+        pe = self._raw(wpe, np.float32, T * Cdim).reshape(T, Cdim).astype(np.float64)
+        x = te[idv] + pe[np.arange(rows) % T]
+        lo, hi = {"i8": (-128, 127), "i16": (-32768, 32767)}[out_dtype]
+        self.store(out, out_dtype, (rows * Cdim,), (1,), np.clip(np.rint(x / scale), lo, hi).reshape(-1))

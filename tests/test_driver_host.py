@@ -177,3 +177,49 @@ def test_layout_choice_makes_head_merge_free(cfg1):
     cm = anvil_mi355x.driver.CompiledModel(cfg1.module, cfg1.consts)
     phys = {v.owner.sym_str: p for v, p in cm.phys.items()}
     assert phys == {"o": [1, 0, 2], "v": [1, 0]}     # o stored head-merged, v stored transposed for P.V
+
+
+@pytest.fixture(scope="module")
+def cfg4():
+    return models.config(4)[0]
+
+
+def test_token_prelude_matches_the_host_embedding(fake, cfg4):
+    """compile() of a token model attaches its tables; run(ids, tokens=True) gathers, adds and quantizes on the
+    device and gives the same values as the host's float64 embedding followed by quantize_input."""
+    cm = anvil_mi355x.compile(cfg4)
+    ids = models.eval_inputs(cfg4.spec, 2, 9)
+    a = cm.run(ids, tokens=True, batch=True, keep="all")
+    x = models.to_float_input(cfg4.spec, cfg4.params, ids)
+    b = cm.run(x, batch=True, keep="all")
+    assert a.ints.keys() == b.ints.keys()
+    assert all(np.array_equal(a.ints[k], b.ints[k]) for k in a.ints)
+    assert np.array_equal(a.ints["x"], cm.quantize_input(x))
+    assert [c for c in fake.calls if c[0] == "embed"][0][1:] == (2 * cfg4.spec.seq, cfg4.spec.seq, cfg4.spec.n_embd)
+    with pytest.raises(ValueError):
+        bad = ids.copy()
+        bad[1, 3] = cfg4.spec.vocab
+        cm.run(bad, tokens=True, batch=True)
+    with pytest.raises(ValueError, match="expected"):
+        cm.run(ids, tokens=True)
+    with pytest.raises(ValueError, match="integers"):
+        cm.run(ids.astype(float), tokens=True, batch=True)
+
+
+def test_tokens_need_embedding_tables(fake, cfg1):
+    cm = anvil_mi355x.compile(cfg1)
+    with pytest.raises(ValueError, match="embedding tables"):
+        cm.run(np.zeros((1, 32), int), tokens=True, batch=True)
+    with pytest.raises(ValueError, match="do not fit"):
+        cm.set_embedding(np.zeros((10, 8), np.float32), np.zeros((32, 64), np.float32))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_float_inputs_are_quantized_on_the_device_as_on_the_host(fake, cfg1, dtype):
+    cm = anvil_mi355x.compile(cfg1)
+    x = models.eval_inputs(cfg1.spec, 3, 12).astype(dtype)
+    s = cm.scale("x")
+    x[0, 0, :4] = np.array([0.5, 1.5, -2.5, 1e9]) * s                  # ties round to even; saturation
+    r = cm.run(x, batch=True, keep="all")
+    assert np.array_equal(r.ints["x"], cm.quantize_input(x))
+    assert [c for c in fake.calls if c[0] == "quantize"][0][2] == (dtype == np.float64)

@@ -127,3 +127,24 @@ def test_reference_frozen_model(name, keep):
     if keep == "all":
         _check_all(res.ints, want.values, consts)
     assert np.array_equal(res.ints["L1.out"], want.values["L1.out"])
+
+
+def test_config4_from_token_ids():
+    """The two-layer token model run from its token ids: the embedding gather, add and quantization run on the
+    device, bit-exact with the host's float64 embedding and the oracle; an id past the vocabulary is a ValueError."""
+    built, nb = models.config(4)
+    cm = anvil_mi355x.compile(built)
+    ids = models.eval_inputs(built.spec, nb, models.config_tag(4))
+    res = cm.run(ids, "mi355x", tokens=True, batch=True, keep="all")
+    x = models.to_float_input(built.spec, built.params, ids)
+    xq = cm.quantize_input(x)
+    assert np.array_equal(res.ints["x"], xq)
+    for i in (0, nb - 1):
+        want = interp.run(built.module, {"x": xq[i:i + 1]}, built.consts, batch=True, fast=True)
+        _check_all({k: v[i:i + 1] for k, v in res.ints.items()}, want.values, built.consts)
+    bad = ids.copy()
+    bad[-1, -1] = built.spec.vocab
+    with pytest.raises(ValueError):
+        cm.run(bad, "mi355x", tokens=True, batch=True)
+    again = cm.run(ids, "mi355x", tokens=True, batch=True)          # the context is usable after the error
+    assert np.array_equal(again.ints[cm.outputs[0]], res.ints[cm.outputs[0]])

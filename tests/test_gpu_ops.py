@@ -328,7 +328,7 @@ def test_gemm_wide_products_take_the_persistent_kernel(dev, M, N, K, dtype, lut,
     rng = np.random.default_rng([41, M, N, K])
     a, w = rng.integers(-128, 128, (M, K), dtype=np.int8), rng.integers(-128, 128, (K, N), dtype=np.int8)
     rows = np.unique(np.concatenate([np.arange(256), np.arange(M - 256, M), rng.integers(0, M, 512)]))
-    acc = a[rows].astype(np.int64) @ w.astype(np.int64)
+    acc = sem.matmul_i8(a[rows].astype(np.int64), w.astype(np.int64), fast=True)   # float64 BLAS, exact here
     s = 20
     m = int(min(((1 << 31) - 1 - (1 << (s - 1))) // int(np.abs(acc).max() * 2), (1 << 23) - 1))
     L = rng.integers(-128, 128, 256) if lut else None
@@ -336,7 +336,7 @@ def test_gemm_wide_products_take_the_persistent_kernel(dev, M, N, K, dtype, lut,
     wt = np.ascontiguousarray(w.T)
     c = dev.alloc(M * N * rt.ITEMSIZE[dtype])
     st = [0, 0, K, 0, 0, K, 0, 0, N]
-    y = sem.qmatmul(a[rows].astype(np.int64), w.astype(np.int64), m, s, L, dtype=dtype)
+    y = sem.qmatmul(a[rows].astype(np.int64), w.astype(np.int64), m, s, L, dtype=dtype, fast=True)
     if add:
         r = rng.integers(-128, 128, (M, N), dtype=np.int8)
         d = dev.alloc(M * N)
@@ -351,3 +351,23 @@ def test_gemm_wide_products_take_the_persistent_kernel(dev, M, N, K, dtype, lut,
     if add:
         want = sem.add_requant(r[rows].astype(np.int64), y, 300, -200, 9)
         assert np.array_equal(d.download((M, N), np.int8)[rows].astype(np.int64), want)
+
+
+@pytest.mark.parametrize("dtype", ["i8", "i16"])
+def test_embed_quantize(dev, dtype):
+    """anvil_embed_quantize: clamp(rint((wte[id] + wpe[t]) / scale)) in float64, as the host computes it."""
+    rng = np.random.default_rng([51, dtype == "i8"])
+    vocab, T, C, B = 300, 40, 48, 3
+    wte = rng.normal(0, 0.02, (vocab, C)).astype(np.float32)
+    wpe = rng.normal(0, 0.02, (T + 5, C)).astype(np.float32)
+    ids = rng.integers(0, vocab, (B, T))
+    scale = 0.0004 if dtype == "i8" else 1e-6
+    x = wte.astype(np.float64)[ids] + wpe.astype(np.float64)[None, :T]
+    lo, hi = (-128, 127) if dtype == "i8" else (-32768, 32767)
+    want = np.clip(np.rint(x / scale), lo, hi).astype(np.int64)
+    out = dev.alloc(B * T * C * rt.ITEMSIZE[dtype])
+    dev.embed_quantize(dev.upload(ids.astype(np.int64)), B * T, T, C, dev.upload(wte), vocab, dev.upload(wpe), scale,
+                       out, dtype)
+    dev.sync()
+    assert np.array_equal(out.download((B, T, C), rt.NP_DTYPE[dtype]).astype(np.int64), want)
+    assert (want == lo).any() and (want == hi).any()           # saturation on both sides is exercised
