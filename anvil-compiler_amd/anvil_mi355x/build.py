@@ -22,6 +22,9 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
           "-packed-fp32-ops", "-Wno-unused-command-line-argument", f"-I{INCLUDE}"]
+# Per-source flags. attention.hip: MFMA accumulators in VGPRs. Its score tiles feed VALU requant code right after
+# each MFMA, and with the accumulators in AGPRs every value would first need a v_accvgpr_read.
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def sources():
@@ -35,7 +38,7 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
 
     def cc(src: Path):
         obj = objdir / (src.stem + ".o")
-        cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)

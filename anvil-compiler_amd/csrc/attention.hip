@@ -12,20 +12,22 @@
 // Workgroup: 4 waves on 32 query rows q0 .. q0 + 31; wave w takes the 32-key tiles w, w + 4, w + 8, ... up to the
 // causal diagonal, so the waves share the row's keys evenly and each holds at most T / 128 tiles of scores.
 //   1. S = Q K^T per tile on v_mfma_i32_32x32x32_i8, requantised to int8 and kept packed in registers: lane l holds
-//      row q0 + l % 32 and, of each tile, the keys 8 g + 4 (l / 32) + e (g, e = 0..3) in dword g, byte e. Partial
+//      row q0 + l % 32 and, of each tile, the keys 16 (l / 32) + 4 g + e (g, e = 0..3) in dword g, byte e. Partial
 //      row maxima (init -128, kept keys only) meet in LDS.
 //   2. Partial sums of lut[s - max + 255] (lut staged in LDS) meet in LDS.
 //   3. p = (lut[d] one + S // 2) // S, d = s - max + 255, exactly, in float64 (full rate on CDNA4): with per-row
 //      A = fl(one / S) and B = fl((S // 2) / S + 2^-40), y = fma(lut[d], A, B) is within 2^-45 of n / S + 2^-40
 //      (n = lut[d] one + S // 2 < 2^31, n / S < 128, three roundings of 2^-53 relative), and n / S is either an
-//      integer or at least 1 / S > 2^-31 away from one, so trunc(y) = n // S. The LUT is staged in LDS as doubles.
-//      O_w = P V over the wave's tiles on MFMA, P straight from registers: the MFMA's K order only has to agree
-//      between its two operands, so the V fragment is read in the packed P's key order (dwords 2 g + l / 32 of each
-//      32-key group).
+//      integer or at least 1 / S > 2^-31 away from one, so floor(y) = n // S (taken as round(y - 1/2) by adding
+//      1.5 2^52). The LUT (>= 0) is staged in LDS as doubles, and each row's p values go into a byte table indexed
+//      by score. O_w = P V over the wave's tiles on MFMA, P packed in registers: lane l's 16 probabilities of a tile
+//      are keys 16 (l / 32) .. + 15 (the key rows entered the score MFMA in bperm order), so its V^T fragment is one
+//      contiguous 16-byte load.
 //   4. The four partial O tiles (int32) are summed through LDS; o = clamp((O M_o + rnd(s_o)) >> s_o), 4-byte
 //      stores.
 // Every product is proven to fit int32 (prove_no_overflow), so the requants run in 32 bits; with S24 the score
 // requant multiply is one 24-bit multiply-add (|acc|, |M_s| < 2^23).
+#include <algorithm>
 #include <utility>
 
 #include "common.h"
@@ -43,6 +45,7 @@ struct AttnArgs {
   int batch1, T, D;
   long long sq0, sq1, ldq, sk0, sk1, ldk, sv0, sv1, ldv, so0, so1, ldo;
   int ms, ss, rnds;    // scores requant
+  int clo, chi;        // the score requant's clamp in the pre-shift domain: [-128, 127] << ss, saturated to int32
   const int* lut;
   int one, causal;
   int mo, so, rndo;    // output requant
@@ -52,6 +55,26 @@ struct AttnArgs {
 constexpr int A_THREADS = 256;
 
 __device__ __forceinline__ int sbyte(unsigned v, int e) { return (int)(int8_t)(v >> (8 * e)); }
+
+// The bytes x_e >> sh (e = 0..3) as one dword: each shift writes its low byte straight into byte lane e (SDWA
+// dst_sel), so no separate pack follows. The x_e are clamped beforehand, so each shifted value is its own byte.
+__device__ __forceinline__ unsigned sra_pack4(int x0, int x1, int x2, int x3, int sh) {
+  unsigned d;
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+      : "=v"(d) : "s"(sh), "v"(x0));
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(d) : "s"(sh), "v"(x1));
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(d) : "s"(sh), "v"(x2));
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(d) : "s"(sh), "v"(x3));
+  return d;
+}
+
+typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+
+// median of three: clamp(x, lo, hi) for runtime bounds lo <= hi, written in the form that selects v_med3_i32
+__device__ __forceinline__ int med3i(int x, int lo, int hi) { return max(min(x, lo), min(max(x, lo), hi)); }
 
 // One 16-byte chunk of a K-contiguous operand row; zero past the head dim.
 template <int D>
@@ -65,17 +88,17 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   constexpr int KS = (D + 31) / 32;         // 32-wide MFMA k-steps over the head dim
   constexpr int CT = (D + 31) / 32;         // 32-wide output column tiles
   constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
-  static_assert(4 * 32 * OROW * 4 >= 32 * 272, "the per-row p tables fit in the partial-O space");
+  static_assert(4 * 32 * OROW * 4 >= 32 * 256, "the per-row p tables fit in the partial-O space");
   __shared__ __attribute__((aligned(16))) int lut_s[256];
+  __shared__ double lutd_s[256];                            // the LUT as doubles, for the p tables
   __shared__ __attribute__((aligned(16))) int lutc_s[16];  // lut[16 k + 15]: the coarse level of the threshold search
   __shared__ int red_m[4][32], red_s[4][32];
-  __shared__ __attribute__((aligned(16))) int opart[4][32 * OROW];
+  __shared__ __attribute__((aligned(256))) int opart[4][32 * OROW];   // 256: the p-table rows
 
   const int t = threadIdx.x;
   const int lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int l32 = lane & 31, half = lane >> 5;
-  lut_s[t] = a.lut[t];
-  if (t < 16) lutc_s[t] = a.lut[16 * t + 15];
+  const int lutv = a.lut[t];       // staged in LDS after phase 1: the load's latency hides behind the score tiles
 
   // XCD-aware order: consecutive logical tiles on one XCD (its L2 holds the head's K and V), each head's query tiles
   // together, the longest (last) query tile of a head first
@@ -100,48 +123,52 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   for (int ks = 0; ks < KS; ++ks) qf[ks] = chunk16<D>(Qr, 2 * ks + half);
 
   // ---- 1. scores of this wave's tiles (w + 4 i), partial row max
+  // The requant clamps before its shift (clamp(x >> s) = clamp'(x) >> s with the bounds scaled by 2^s), so the
+  // max runs on the clamped values and each score byte is one shift written into its byte lane.
   unsigned sc[NTW][4];
-  int mx = -128;
+  int mxc = a.clo;
   auto kload = [&](int nt, v4i* kf) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = chunk16<D>(Kb + (long long)nt * 32 * a.ldk, 2 * ks + half);
   };
-  // K tiles are loaded two tiles ahead of their MFMAs
+  // K tiles are loaded two tiles ahead of their MFMAs. The buffers rotate on every pass, loaded or not, so the
+  // unrolled passes only rename registers.
   v4i kf[KS], kn[KS];
   if (w < ntiles) kload(w, kf);
   if (NTW > 1 && w + 4 < ntiles) kload(w + 4, kn);
   static_for<NTW>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
+    v4i kn2[KS];
+    if (i + 2 < NTW && nt + 8 < ntiles) kload(nt + 8, kn2);
     if (nt < ntiles) {
-      v4i kn2[KS];
-      if (i + 2 < NTW && nt + 8 < ntiles) kload(nt + 8, kn2);
       v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[ks], qf[ks], acc, 0, 0, 0);
-      int v[16];
+      int x[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int x = S24 ? __mul24(acc[r], a.ms) + a.rnds : acc[r] * a.ms + a.rnds;
-        v[r] = min(max(x >> a.ss, -128), 127);
+        const int y = S24 ? __mul24(acc[r], a.ms) + a.rnds : acc[r] * a.ms + a.rnds;
+        x[r] = med3i(y, a.clo, a.chi);
       }
       if (a.causal && nt == ntiles - 1) {             // the diagonal tile: keys past the row are masked
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          mx = max(mx, nt * 32 + 16 * half + r <= qrow ? v[r] : -128);
+          mxc = max(mxc, nt * 32 + 16 * half + r <= qrow ? x[r] : a.clo);
       } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = max(mx, v[r]);
+        for (int r = 0; r < 16; ++r) mxc = max(mxc, x[r]);
       }
 #pragma unroll
-      for (int g = 0; g < 4; ++g) sc[i][g] = pack4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+      for (int g = 0; g < 4; ++g) sc[i][g] = sra_pack4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3], a.ss);
+    }
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        kf[ks] = kn[ks];
-        kn[ks] = kn2[ks];
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = kn[ks];
+      kn[ks] = kn2[ks];
     }
   });
+  int mx = max(mxc >> a.ss, -128);
 
   // the first two V^T tiles load while the row maxima are reduced and the sums run
   const int8_t* Vr[CT];
@@ -157,7 +184,14 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   if (NTW > 1 && w + 4 < ntiles) vload(w + 4, vn);
   mx = max(mx, __shfl_xor(mx, 32, 64));
   if (half == 0) red_m[w][l32] = mx;
-  __syncthreads();                                        // also publishes lut_s
+  lut_s[t] = lutv;
+  lutd_s[t] = (double)lutv;
+  // the p tables (8 KiB of the partial-O space, filled after the next barrier) start zeroed, 32 bytes a thread
+  int8_t* ptab = reinterpret_cast<int8_t*>(&opart[0][0]);
+  *reinterpret_cast<v4i*>(ptab + 32 * t) = v4i{0, 0, 0, 0};
+  *reinterpret_cast<v4i*>(ptab + 32 * t + 16) = v4i{0, 0, 0, 0};
+  __syncthreads();                                        // also publishes lut_s and the zeroed tables
+  if (t < 16) lutc_s[t] = lut_s[16 * t + 15];            // published by the next barrier
   mx = max(max(red_m[0][l32], red_m[1][l32]), max(red_m[2][l32], red_m[3][l32]));
 
   // ---- 2. partial exp sums over the kept keys
@@ -187,13 +221,13 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   S = red_s[0][l32] + red_s[1][l32] + red_s[2][l32] + red_s[3][l32];
 
   // ---- 3. probabilities, O_w = P V over this wave's tiles
-  // p depends on the row and the score only, so each row gets a byte table prow[s] = (lut[d] one + S // 2) // S,
-  // d = s - max + 255, built in the partial-O space (free until this phase ends). With a non-decreasing table the
+  // p depends on the row and the score only, so each row gets a byte table of (lut[d] one + S // 2) // S over the
+  // scores s, d = s - max + 255, built in the partial-O space (free until this phase ends). With a non-decreasing table the
   // quotient is 0 below the first d where lut[d] one + S // 2 >= S, and only the entries from there up are divided;
   // otherwise every entry is.
   const double Sd = (double)S;                           // S >= lut[255] >= 1: the row maximum maps to d = 255
   const double qa = (double)a.one / Sd;
-  const double qb = (double)(S >> 1) / Sd + 0x1p-40;
+  const double qb = (double)(S >> 1) / Sd + 0x1p-40 - 0.5;   // the - 0.5 is exact (Sterbenz, or S = 1)
   int d0 = 0;
   if (mono) {
     // lut[d] one + S // 2 >= S  <=>  lut[d] >= e0 = ceil((S - S // 2) / one); d0 = #{d : lut[d] < e0}, counted over
@@ -212,57 +246,65 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
     const int blk = below16(lutc_s);
     d0 = blk == 16 ? 256 : 16 * blk + below16(lut_s + 16 * blk);
   }
-  constexpr int PT = 272;                                // table row stride (bytes), 16-byte aligned
-  int8_t* ptab = reinterpret_cast<int8_t*>(&opart[0][0]);
+  // The tables sit in the partial-O space, 256 bytes a row: the entry of score s in row r is at column
+  // (s & 255) ^ 4 r, so a lookup address is the row base with its low byte replaced by the swizzled score byte
+  // (one v_perm), and the 32 rows' entries for one s fall in 32 different banks.
+  // An entry is y = fma(lut[d], A, B - 1/2), within 2^-45 of n / S - 1/2 + 2^-40 and never a half-integer, so
+  // adding 1.5 2^52 rounds it to n // S, which is then the low dword of the sum: two full-rate float64 operations.
+  constexpr int PT = 256;
+  const int cx = 4 * l32;
   {
     const int part = 2 * w + half;                       // this lane's eighth of its row's table
-    int8_t* zp = ptab + l32 * PT + 32 * part;
-    *reinterpret_cast<v4i*>(zp) = v4i{0, 0, 0, 0};
-    *reinterpret_cast<v4i*>(zp + 16) = v4i{0, 0, 0, 0};
-    __syncthreads();
+    int8_t* spare = reinterpret_cast<int8_t*>(&red_m[0][0]) + t;   // red_m is free: read before the last barrier
+    int8_t* trow = ptab + l32 * PT;
     const int dlow = max(d0, 127 - mx);                  // d below 127 - max needs s < -128
-    for (int d = 255 - part; d >= dlow; d -= 32) {      // four independent entries per pass
+    for (int d = 255 - part; d >= dlow; d -= 32) {      // four independent entries per pass, reads issued together
+      double lv[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 4; ++u) lv[u] = lutd_s[max(d - 8 * u, 0)];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {                      // an entry below dlow goes to this thread's spare byte
         const int du = d - 8 * u;
-        if (du >= dlow) ptab[l32 * PT + (du + mx - 255 + 128)] = (int8_t)(int)__builtin_fma((double)lut_s[du], qa, qb);
+        const int q = __double2loint(__builtin_fma(lv[u], qa, qb) + 0x1.8p52);
+        *(du >= dlow ? trow + (((du + mx - 255) & 255) ^ cx) : spare) = (int8_t)q;
       }
     }
     __syncthreads();
   }
-  const int8_t* prow = ptab + l32 * PT + 128;
+  const unsigned rbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) int8_t*)(ptab + l32 * PT);
+  const unsigned swz = 0x01010101u * (unsigned)cx;
   v16i oacc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) oacc[ct] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   static_for<NTW>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
+    v4i vn2[CT];
+    if (i + 2 < NTW && nt + 8 < ntiles) vload(nt + 8, vn2);
     if (nt < ntiles) {
-      v4i vn2[CT];
-      if (i + 2 < NTW && nt + 8 < ntiles) vload(nt + 8, vn2);
       int p[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const unsigned sw = sc[i][g] ^ swz;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          p[4 * g + e] = *reinterpret_cast<lds_u8*>(__builtin_amdgcn_perm(rbase, sw, 0x07060500u | e));
+      }
       if (a.causal && nt == ntiles - 1) {
+        asm volatile("");                                // keeps the masking on the diagonal tile's own path
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int s = sbyte(sc[i][r >> 2], r & 3);
-          const bool kept = nt * 32 + 16 * half + r <= qrow;
-          const int q = prow[kept ? s : mx];
-          p[r] = kept ? q : 0;
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = prow[sbyte(sc[i][r >> 2], r & 3)];
+        for (int r = 0; r < 16; ++r) p[r] = nt * 32 + 16 * half + r <= qrow ? p[r] : 0;
       }
       v4i pf;
 #pragma unroll
       for (int g = 0; g < 4; ++g) pf[g] = (int)pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) oacc[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf[ct], pf, oacc[ct], 0, 0, 0);
+    }
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        vf[ct] = vn[ct];
-        vn[ct] = vn2[ct];
-      }
+    for (int ct = 0; ct < CT; ++ct) {
+      vf[ct] = vn[ct];
+      vn[ct] = vn2[ct];
     }
   });
 
@@ -356,6 +398,8 @@ extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t*
   a.sv0 = st[6], a.sv1 = st[7], a.ldv = st[8];
   a.so0 = st[9], a.so1 = st[10], a.ldo = st[11];
   a.ms = m_s, a.ss = s_s, a.rnds = s_s ? 1 << (s_s - 1) : 0;
+  a.clo = (int)std::max(-128ll * (1ll << s_s), I32_MIN);
+  a.chi = (int)std::min(128ll * (1ll << s_s) - 1, I32_MAX);
   a.lut = lut;
   a.one = one, a.causal = causal ? 1 : 0;
   a.mo = m_o, a.so = s_o, a.rndo = s_o ? 1 << (s_o - 1) : 0;
