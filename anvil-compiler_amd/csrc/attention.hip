@@ -115,7 +115,6 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   const int8_t* Qr = a.Q + b0 * a.sq0 + b1 * a.sq1 + (long long)qrow * a.ldq;
   // key rows enter the score MFMA in bperm order: score accumulator r of lane l is then key 16 (l / 32) + r of the
   // tile, so a lane's 16 probabilities are 16 consecutive keys and its V^T fragment is one contiguous 16-byte load
-  const int8_t* Kb = a.K + b0 * a.sk0 + b1 * a.sk1 + (long long)bperm(l32) * a.ldk;
   const int8_t* Vb = a.V + b0 * a.sv0 + b1 * a.sv1;
 
   v4i qf[KS];
@@ -127,61 +126,73 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   // max runs on the clamped values and each score byte is one shift written into its byte lane.
   unsigned sc[NTW][4];
   int mxc = a.clo;
+  // K and V^T tiles come through raw buffer loads; a tile past the causal diagonal (or a chunk past the head dim)
+  // gets an offset beyond the descriptor, which loads zeros without touching memory, so every pass can issue its
+  // loads whatever the wave's tile count
+  const __amdgpu_buffer_rsrc_t krs = uniform_rsrc(a.K + b0 * a.sk0 + b1 * a.sk1, (int)((long long)a.T * a.ldk));
+  const unsigned koff = (unsigned)(bperm(l32) * a.ldk) + 16 * half;
   auto kload = [&](int nt, v4i* kf) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = chunk16<D>(Kb + (long long)nt * 32 * a.ldk, 2 * ks + half);
+    for (int ks = 0; ks < KS; ++ks) {
+      const unsigned o = nt < ntiles && 32 * ks + 16 * half < D ? koff + 32 * ks + (unsigned)(nt * 32 * a.ldk) : OOB;
+      kf[ks] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(krs, o, 0, 0));
+    }
   };
-  // K tiles are loaded two tiles ahead of their MFMAs. The buffers rotate on every pass, loaded or not, so the
-  // unrolled passes only rename registers.
+  // K tiles are loaded two tiles ahead of their MFMAs. The wave's tiles are a prefix of its passes, and pass i + 1
+  // is entered from the end of pass i only (nested, not sequential, branches), each pass issuing its prefetch
+  // unconditionally: each wait then covers exactly the loads two tiles back, where a join of a path that loaded
+  // with one that did not would make it cover every load issued so far. The buffers rotate in registers.
   v4i kf[KS], kn[KS];
-  if (w < ntiles) kload(w, kf);
-  if (NTW > 1 && w + 4 < ntiles) kload(w + 4, kn);
-  static_for<NTW>([&](auto ic) {
+  kload(w, kf);
+  if (NTW > 1) kload(w + 4, kn);
+  auto pass1 = [&](auto self, auto ic) __attribute__((always_inline)) -> void {
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
     v4i kn2[KS];
-    if (i + 2 < NTW && nt + 8 < ntiles) kload(nt + 8, kn2);
-    if (nt < ntiles) {
-      v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    if (i + 2 < NTW) kload(nt + 8, kn2);
+    v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[ks], qf[ks], acc, 0, 0, 0);
-      int x[16];
+    for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[ks], qf[ks], acc, 0, 0, 0);
+    int x[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int y = S24 ? __mul24(acc[r], a.ms) + a.rnds : acc[r] * a.ms + a.rnds;
-        x[r] = med3i(y, a.clo, a.chi);
-      }
-      if (a.causal && nt == ntiles - 1) {             // the diagonal tile: keys past the row are masked
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          mxc = max(mxc, nt * 32 + 16 * half + r <= qrow ? x[r] : a.clo);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mxc = max(mxc, x[r]);
-      }
-#pragma unroll
-      for (int g = 0; g < 4; ++g) sc[i][g] = sra_pack4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3], a.ss);
+    for (int r = 0; r < 16; ++r) {
+      const int y = S24 ? __mul24(acc[r], a.ms) + a.rnds : acc[r] * a.ms + a.rnds;
+      x[r] = med3i(y, a.clo, a.chi);
     }
+    if (a.causal && nt == ntiles - 1) {               // the diagonal tile: keys past the row are masked
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        mxc = max(mxc, nt * 32 + 16 * half + r <= qrow ? x[r] : a.clo);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mxc = max(mxc, x[r]);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sc[i][g] = sra_pack4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3], a.ss);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       kf[ks] = kn[ks];
       kn[ks] = kn2[ks];
     }
-  });
+    if constexpr (i + 1 < NTW) {
+      if (nt + 4 < ntiles) self(self, std::integral_constant<int, i + 1>{});
+    }
+  };
+  if (w < ntiles) pass1(pass1, std::integral_constant<int, 0>{});
   int mx = max(mxc >> a.ss, -128);
 
   // the first two V^T tiles load while the row maxima are reduced and the sums run
-  const int8_t* Vr[CT];
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct) Vr[ct] = Vb + (long long)(32 * ct + l32) * a.ldv + 16 * half;
+  const __amdgpu_buffer_rsrc_t vrs = uniform_rsrc(Vb, (int)((long long)D * a.ldv));
   auto vload = [&](int nt, v4i* vf) {
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-      vf[ct] = 32 * ct + l32 >= D ? v4i{0, 0, 0, 0} : *reinterpret_cast<const v4i*>(Vr[ct] + nt * 32);
+    for (int ct = 0; ct < CT; ++ct) {
+      const unsigned o = nt < ntiles && 32 * ct + l32 < D ? (unsigned)((32 * ct + l32) * a.ldv + 16 * half + nt * 32) : OOB;
+      vf[ct] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(vrs, o, 0, 0));
+    }
   };
   v4i vf[CT], vn[CT];
-  if (w < ntiles) vload(w, vf);
-  if (NTW > 1 && w + 4 < ntiles) vload(w + 4, vn);
+  vload(w, vf);
+  if (NTW > 1) vload(w + 4, vn);
   mx = max(mx, __shfl_xor(mx, 32, 64));
   if (half == 0) red_m[w][l32] = mx;
   lut_s[t] = lutv;
@@ -276,37 +287,39 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   v16i oacc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) oacc[ct] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  static_for<NTW>([&](auto ic) {
+  auto pass3 = [&](auto self, auto ic) __attribute__((always_inline)) -> void {   // nested passes, as for K
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
     v4i vn2[CT];
-    if (i + 2 < NTW && nt + 8 < ntiles) vload(nt + 8, vn2);
-    if (nt < ntiles) {
-      int p[16];
+    if (i + 2 < NTW) vload(nt + 8, vn2);
+    int p[16];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const unsigned sw = sc[i][g] ^ swz;
+    for (int g = 0; g < 4; ++g) {
+      const unsigned sw = sc[i][g] ^ swz;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          p[4 * g + e] = *reinterpret_cast<lds_u8*>(__builtin_amdgcn_perm(rbase, sw, 0x07060500u | e));
-      }
-      if (a.causal && nt == ntiles - 1) {
-        asm volatile("");                                // keeps the masking on the diagonal tile's own path
-#pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = nt * 32 + 16 * half + r <= qrow ? p[r] : 0;
-      }
-      v4i pf;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) pf[g] = (int)pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) oacc[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf[ct], pf, oacc[ct], 0, 0, 0);
+      for (int e = 0; e < 4; ++e)
+        p[4 * g + e] = *reinterpret_cast<lds_u8*>(__builtin_amdgcn_perm(rbase, sw, 0x07060500u | e));
     }
+    if (a.causal && nt == ntiles - 1) {
+      asm volatile("");                                  // keeps the masking on the diagonal tile's own path
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = nt * 32 + 16 * half + r <= qrow ? p[r] : 0;
+    }
+    v4i pf;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) pf[g] = (int)pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) oacc[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf[ct], pf, oacc[ct], 0, 0, 0);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       vf[ct] = vn[ct];
       vn[ct] = vn2[ct];
     }
-  });
+    if constexpr (i + 1 < NTW) {
+      if (nt + 4 < ntiles) self(self, std::integral_constant<int, i + 1>{});
+    }
+  };
+  if (w < ntiles) pass3(pass3, std::integral_constant<int, 0>{});
 
   // ---- 4. sum the four partial O tiles, requant, store. Lane l holds O_w[row l % 32][32 ct + 8 g + 4 (l / 32) + e].
   __syncthreads();                                       // every wave is done with the p tables
@@ -384,6 +397,11 @@ extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t*
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: operand not aligned");
   if ((long long)batch0 * batch1 * (T / 32) > (1ll << 31) - 1)
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: too many heads");
+  // K and V^T are read through 32-bit buffer offsets over one head: T key rows of stride ldk (each at least D
+  // bytes apart), D rows of V^T of stride ldv (each at least T keys)
+  if (st[5] < D || st[8] < T || (long long)T * st[5] >= (1ll << 31) || (long long)D * st[8] >= (1ll << 31))
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: K row stride %lld / V^T row stride %lld out of range",
+                     (long long)st[5], (long long)st[8]);
   if (int r = check_ctx(ctx)) return r;
   AttnArgs a;
   a.Q = Q;

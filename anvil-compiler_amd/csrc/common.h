@@ -72,6 +72,19 @@ __device__ __forceinline__ unsigned pack4(int v0, int v1, int v2, int v3) {
   return __builtin_amdgcn_perm(t23, t01, 0x05040100u);
 }
 
+constexpr unsigned RSRC_DW3 = 0x00020000u;               // raw buffer, 32-bit data format (gfx9 family)
+constexpr unsigned OOB = 0xFFFFFFF0u;                    // a buffer offset past any descriptor's range: loads 0
+
+// A raw buffer resource over [base, base + bytes). Its fields pass through readfirstlane: they are uniform, and
+// saying so keeps the descriptor in SGPRs (a descriptor the compiler places in VGPRs costs every buffer load a
+// waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, int bytes) {
+  const unsigned long long a = (unsigned long long)base;
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a), hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+  void* p = (void*)(((unsigned long long)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, __builtin_amdgcn_readfirstlane(bytes), RSRC_DW3);
+}
+
 constexpr long long I32_MIN = -(1ll << 31);
 constexpr long long I32_MAX = (1ll << 31) - 1;
 

@@ -282,18 +282,6 @@ __global__ __launch_bounds__(G_THREADS) void gemm_i8_kernel(GemmArgs g) {
 // arrays as its staging tile. MUL24: every |acc| and |M| is below 2^23 (host-proven), so acc * M + rnd is one
 // 24-bit multiply-add.
 
-constexpr unsigned RSRC_DW3 = 0x00020000u;               // raw buffer, 32-bit data format (gfx9 family)
-constexpr unsigned OOB = 0xFFFFFFF0u;
-
-// A raw buffer resource over [base, base + bytes). Its fields pass through readfirstlane: they are uniform, and
-// saying so keeps the descriptor in SGPRs (a descriptor the compiler places in VGPRs costs every buffer load a
-// waterfall loop).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, int bytes) {
-  const unsigned long long a = (unsigned long long)base;
-  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a), hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
-  void* p = (void*)(((unsigned long long)hi << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, __builtin_amdgcn_readfirstlane(bytes), RSRC_DW3);
-}
 
 // 16 bytes per lane from buffer offset voff into LDS at lds + 16 * lane (lds must be wave-uniform)
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, int8_t* lds, unsigned voff) {

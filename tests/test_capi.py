@@ -95,6 +95,10 @@ def test_attention_argument_validation_precedes_the_device():
     bad = (C.c_int64 * 12)(*[64 * 64, 64, 72] + [64 * 64, 64, 64] * 3)
     with pytest.raises(ValueError, match="stride 2"):
         att(64, 64, 127, 1, bad)
+    for ldk, ldv in ((32, 64), (64, 48), (1 << 26, 64), (64, 1 << 26)):   # K rows < D apart, V^T rows < T, > 2^31
+        s = (C.c_int64 * 12)(*[64 * 64, 64, 64] + [64 * 64, 64, ldk] + [64 * 64, 64, ldv] + [64 * 64, 64, 64])
+        with pytest.raises(ValueError, match="K row stride"):
+            att(64, 64, 127, 1, s)
     with pytest.raises(ValueError, match="null context"):
         att(64, 64, 127, 1)
 
