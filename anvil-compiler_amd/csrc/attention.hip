@@ -56,25 +56,8 @@ constexpr int A_THREADS = 256;
 
 __device__ __forceinline__ int sbyte(unsigned v, int e) { return (int)(int8_t)(v >> (8 * e)); }
 
-// The bytes x_e >> sh (e = 0..3) as one dword: each shift writes its low byte straight into byte lane e (SDWA
-// dst_sel), so no separate pack follows. The x_e are clamped beforehand, so each shifted value is its own byte.
-__device__ __forceinline__ unsigned sra_pack4(int x0, int x1, int x2, int x3, int sh) {
-  unsigned d;
-  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
-      : "=v"(d) : "s"(sh), "v"(x0));
-  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-      : "+v"(d) : "s"(sh), "v"(x1));
-  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-      : "+v"(d) : "s"(sh), "v"(x2));
-  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-      : "+v"(d) : "s"(sh), "v"(x3));
-  return d;
-}
-
 typedef __attribute__((address_space(3))) const uint8_t lds_u8;
 
-// median of three: clamp(x, lo, hi) for runtime bounds lo <= hi, written in the form that selects v_med3_i32
-__device__ __forceinline__ int med3i(int x, int lo, int hi) { return max(min(x, lo), min(max(x, lo), hi)); }
 
 // One 16-byte chunk of a K-contiguous operand row; zero past the head dim.
 template <int D>

@@ -85,6 +85,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base,
   return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, __builtin_amdgcn_readfirstlane(bytes), RSRC_DW3);
 }
 
+// The bytes x_e >> sh (e = 0..3) as one dword: each shift writes its low byte straight into byte lane e (SDWA
+// dst_sel), so no separate pack follows. The x_e are clamped beforehand, so each shifted value is its own byte.
+__device__ __forceinline__ unsigned sra_pack4(int x0, int x1, int x2, int x3, int sh) {
+  unsigned d;
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+      : "=v"(d) : "s"(sh), "v"(x0));
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(d) : "s"(sh), "v"(x1));
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(d) : "s"(sh), "v"(x2));
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(d) : "s"(sh), "v"(x3));
+  return d;
+}
+
+// median of three: clamp(x, lo, hi) for runtime bounds lo <= hi, written in the form that selects v_med3_i32
+__device__ __forceinline__ int med3i(int x, int lo, int hi) { return max(min(x, lo), min(max(x, lo), hi)); }
+
 constexpr long long I32_MIN = -(1ll << 31);
 constexpr long long I32_MAX = (1ll << 31) - 1;
 

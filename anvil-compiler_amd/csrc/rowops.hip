@@ -127,51 +127,52 @@ __global__ __launch_bounds__(R_THREADS) void softmax_fast(const int8_t* __restri
 
 // ------------------------------------------------------------------------------------- fast rmsnorm_int
 // For proven graphs with i8 rows (ss_shift = ss_init = 0) of a multiple of 16 bytes and at most 1024: a wavefront
-// takes RMS_ROWS rows at a time, lane l holding 16 consecutive entries of each; every row's load (and then every
-// row's rsqrt-LUT read) is issued before any is used, so their latencies overlap. The sum of squares is v_dot4 of
-// each dword with itself.
+// takes RMS_ROWS rows at a time, lane l holding 16 consecutive entries of each, and loads the next group while it
+// requantises this one. Row loads and stores are raw buffer accesses over the group's rows: a lane past the row
+// end or a row past the last gets an offset beyond the descriptor (loads 0, stores nothing), so no access sits
+// under a branch and the next group's loads stay in flight across the whole group (a join of a path that loaded
+// with one that did not would make the compiler wait for every load at the next use). The sum of squares is
+// v_dot4 of each dword with itself; the row statistics are wave-uniform, so the rsqrt-LUT read is a scalar load.
 constexpr int RMS_ROWS = 4;
 
 // S24: every |lut[i] * mult| is below 2^23 (host-checked), so x w (lut[i] mult) + rnd -- the same integer as
 // x w lut[i] mult + rnd, which is proven to fit int32 -- is one 24-bit multiply-add per element, with lut[i] mult
-// formed once per row; otherwise two 32-bit multiplies per element.
+// formed once per row; otherwise two 32-bit multiplies per element. The requant clamps before its shift (bounds
+// scaled by 2^s), so each output byte is one shift written straight into its byte lane.
 template <bool S24>
 __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
                                                            const int* __restrict__ lut, int lut_len, int mult,
                                                            int shift, long long rows, int cols,
                                                            int8_t* __restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const int chunks = cols >> 4;
-  const bool active = lane < chunks;
+  const bool active = lane < (cols >> 4);
   v4i wv = {0, 0, 0, 0};
   if (active) wv = *reinterpret_cast<const v4i*>(w + 16 * lane);
   int wb[16];                                                   // this lane's 16 weights, sign-extended once
 #pragma unroll
   for (int b = 0; b < 16; ++b) wb[b] = sbyte(wv, b);
+  unsigned off[RMS_ROWS];                                       // row j, this lane's chunk; OOB for idle lanes
+#pragma unroll
+  for (int j = 0; j < RMS_ROWS; ++j) off[j] = active ? (unsigned)(j * cols + 16 * lane) : OOB;
   const long long step = (long long)gridDim.x * R_WAVES * RMS_ROWS;
-  // the next group's rows are loaded while this group's are requantized and stored
-  auto load = [&](long long r0, v4i* xv) {
-#pragma unroll
-    for (int j = 0; j < RMS_ROWS; ++j) {
-      xv[j] = v4i{0, 0, 0, 0};
-      if (active && r0 + j < rows) xv[j] = *reinterpret_cast<const v4i*>(x + (r0 + j) * cols + 16 * lane);
-    }
+  auto group = [&](const int8_t* base, long long r0) {        // a raw buffer over rows r0 .. of this group
+    const long long n = r0 < rows ? std::min<long long>(RMS_ROWS, rows - r0) : 0;
+    return uniform_rsrc(base + (r0 < rows ? r0 : 0) * cols, (int)(n * cols));
   };
-  long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * RMS_ROWS;
-  v4i xn[RMS_ROWS];
-  load(row0, xn);
-  for (; row0 < rows; row0 += step) {
-    v4i xv[RMS_ROWS];
+  auto load = [&](long long r0, v4i* xv) {
+    const __amdgpu_buffer_rsrc_t rs = group(x, r0);
 #pragma unroll
-    for (int j = 0; j < RMS_ROWS; ++j) xv[j] = xn[j];
-    load(row0 + step, xn);
+    for (int j = 0; j < RMS_ROWS; ++j)
+      xv[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, off[j], 0, 0));
+  };
+  auto process = [&](const v4i* xv, long long r0) {
     int idx[RMS_ROWS], sh[RMS_ROWS];
 #pragma unroll
     for (int j = 0; j < RMS_ROWS; ++j) {
       int ss = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[j][q], xv[j][q], ss, false);
-      ss = wave_sum32(ss);
+      ss = __builtin_amdgcn_readfirstlane(wave_sum32(ss));     // every lane holds the same sum
       int k = 0;
       while (ss >= lut_len) {
         ss >>= 2;
@@ -183,23 +184,42 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
     int r[RMS_ROWS];
 #pragma unroll
     for (int j = 0; j < RMS_ROWS; ++j) r[j] = lut[idx[j]];
+    const __amdgpu_buffer_rsrc_t ws = group(out, r0);
 #pragma unroll
     for (int j = 0; j < RMS_ROWS; ++j) {
-      if (!active || row0 + j >= rows) continue;
-      const int rnd = sh[j] ? (1 << (sh[j] - 1)) : 0;
+      const int s = sh[j];
+      const int rnd = s ? (1 << (s - 1)) : 0;
+      const int lo = s >= 24 ? INT32_MIN : -128 * (1 << s), hi = s >= 24 ? INT32_MAX : 128 * (1 << s) - 1;
       const int rm = S24 ? r[j] * mult : 0;
-      int v[16];
+      v4i o;
 #pragma unroll
-      for (int b = 0; b < 16; ++b) {
-        const int xw = sbyte(xv[j], b) * wb[b];
-        // proven: x w r and x w r M + rnd fit int32
-        const int acc = S24 ? __mul24(xw, rm) + rnd : xw * r[j] * mult + rnd;
-        v[b] = min(max(acc >> sh[j], -128), 127);
+      for (int q = 0; q < 4; ++q) {
+        int y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int xw = sbyte(xv[j], 4 * q + e) * wb[4 * q + e];
+          // proven: x w r and x w r M + rnd fit int32
+          y[e] = med3i(S24 ? __mul24(xw, rm) + rnd : xw * r[j] * mult + rnd, lo, hi);
+        }
+        o[q] = (int)sra_pack4(y[0], y[1], y[2], y[3], s);
       }
-      *reinterpret_cast<v4i*>(out + (row0 + j) * cols + 16 * lane) =
-          v4i{(int)pack4(v[0], v[1], v[2], v[3]), (int)pack4(v[4], v[5], v[6], v[7]),
-              (int)pack4(v[8], v[9], v[10], v[11]), (int)pack4(v[12], v[13], v[14], v[15])};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o), ws,
+                                             off[j], 0, 0);
     }
+  };
+  // two row-group buffers in turn (the loop unrolled by two), so a group's rows are never copied between registers
+  // and its loads stay in flight while the other group is requantised
+  long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * RMS_ROWS;
+  v4i xa[RMS_ROWS], xb[RMS_ROWS];
+  load(row0, xa);
+  while (row0 < rows) {
+    load(row0 + step, xb);
+    process(xa, row0);
+    row0 += step;
+    if (row0 >= rows) break;
+    load(row0 + step, xa);
+    process(xb, row0);
+    row0 += step;
   }
 }
 
@@ -332,9 +352,10 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
   if (blocks > (1ll << 31) - 1) return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: too many rows");
   if ((flags & ANVIL_OP_UNCHECKED) && x_dtype == ANVIL_I8 && ss_shift == 0 && ss_init == 0 && cols % 16 == 0 &&
       cols <= 1024 && al16(x) && al16(w) && al16(out)) {
-    // four workgroups per CU, each wave walking row groups with the next group's loads in flight
+    // up to eight workgroups per CU (one row group per wave for the block shapes), a wave walking further groups with
+    // the next group's loads in flight
     const long long groups = (rows + RMS_ROWS - 1) / RMS_ROWS;
-    const dim3 grid((unsigned)std::min<long long>((groups + R_WAVES - 1) / R_WAVES, 4ll * ctx->num_cu));
+    const dim3 grid((unsigned)std::min<long long>((groups + R_WAVES - 1) / R_WAVES, 8ll * ctx->num_cu));
     if (flags & ANVIL_RMS_S24)
       hipLaunchKernelGGL(rmsnorm_fast<true>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
                          mult, shift, (long long)rows, cols, out);

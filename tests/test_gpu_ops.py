@@ -127,6 +127,21 @@ def test_rmsnorm_i8(dev, d, flags):
     assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s, flags=flags), want)
 
 
+@pytest.mark.parametrize("flags", [rt.OP_UNCHECKED, rt.OP_UNCHECKED | rt.RMS_S24])
+def test_rmsnorm_fast_walks_many_row_groups(dev, flags):
+    """More row groups of four than the grid has waves (a cap of eight workgroups of four waves per CU): each wave
+    walks several groups through both of its row buffers (three each on MI355X's 256 CUs), and the last group is
+    ragged (rows % 4 == 3)."""
+    d = 64
+    rows = 8 * 4 * 256 * 4 * 3 + 3
+    rng = np.random.default_rng([61, rows])
+    w = rng.integers(-127, 128, d)
+    lut, s = Q.rmsnorm_lut(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
+    x = rng.integers(-128, 128, (rows, d))
+    want = sem.rmsnorm_int(x, w, lut, 1, s)
+    assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s, flags=flags), want)
+
+
 def test_rmsnorm_i16_wide(dev):
     d = 32
     rng = np.random.default_rng(8)
