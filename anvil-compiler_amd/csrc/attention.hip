@@ -74,7 +74,6 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   static_assert(4 * 32 * OROW * 4 >= 32 * 256, "the per-row p tables fit in the partial-O space");
   __shared__ __attribute__((aligned(16))) int lut_s[256];
   __shared__ double lutd_s[256];                            // the LUT as doubles, for the p tables
-  __shared__ __attribute__((aligned(16))) int lutc_s[16];  // lut[16 k + 15]: the coarse level of the threshold search
   __shared__ int red_m[4][32], red_s[4][32];
   __shared__ __attribute__((aligned(256))) int opart[4][32 * OROW];   // 256: the p-table rows
 
@@ -143,9 +142,9 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
       x[r] = med3i(y, a.clo, a.chi);
     }
     if (a.causal && nt == ntiles - 1) {               // the diagonal tile: keys past the row are masked
+      const int lim = qrow - nt * 32 - 16 * half;     // key r of this lane is kept iff r <= lim
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        mxc = max(mxc, nt * 32 + 16 * half + r <= qrow ? x[r] : a.clo);
+      for (int r = 0; r < 16; ++r) mxc = max(mxc, r <= lim ? x[r] : a.clo);
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mxc = max(mxc, x[r]);
@@ -185,7 +184,6 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   *reinterpret_cast<v4i*>(ptab + 32 * t) = v4i{0, 0, 0, 0};
   *reinterpret_cast<v4i*>(ptab + 32 * t + 16) = v4i{0, 0, 0, 0};
   __syncthreads();                                        // also publishes lut_s and the zeroed tables
-  if (t < 16) lutc_s[t] = lut_s[16 * t + 15];            // published by the next barrier
   mx = max(max(red_m[0][l32], red_m[1][l32]), max(red_m[2][l32], red_m[3][l32]));
 
   // ---- 2. partial exp sums over the kept keys
@@ -196,10 +194,11 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
     const int nt = w + 4 * i;
     if (nt < ntiles) {
       if (a.causal && nt == ntiles - 1) {
+        const int lim = qrow - nt * 32 - 16 * half;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int s = sbyte(sc[i][r >> 2], r & 3);
-          const bool kept = nt * 32 + 16 * half + r <= qrow;
+          const bool kept = r <= lim;
           const int e = erow[kept ? s : mx];              // a masked score may exceed the max: read inside the table
           S += kept ? e : 0;
         }
@@ -224,44 +223,39 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   const double qb = (double)(S >> 1) / Sd + 0x1p-40 - 0.5;   // the - 0.5 is exact (Sterbenz, or S = 1)
   int d0 = 0;
   if (mono) {
-    // lut[d] one + S // 2 >= S  <=>  lut[d] >= e0 = ceil((S - S // 2) / one); d0 = #{d : lut[d] < e0}, counted over
-    // 16 blocks of 16 and then inside the first block that reaches e0
-    const int need = S - (S >> 1);
-    const int e0 = (need + a.one - 1) / a.one;
-    auto below16 = [&](const int* p16) {
-      int n = 0;
+    // lut[d] one + S // 2 >= S  <=>  lut[d] >= e0 = ceil((S - S // 2) / one); d0 = #{d : lut[d] < e0}, by binary
+    // search over the non-decreasing table (256 when even lut[255] is below e0)
+    const int e0 = (S - (S >> 1) + a.one - 1) / a.one;
+    int pos = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const v4i v = reinterpret_cast<const v4i*>(p16)[q];
-        n += (v[0] < e0) + (v[1] < e0) + (v[2] < e0) + (v[3] < e0);
-      }
-      return n;
-    };
-    const int blk = below16(lutc_s);
-    d0 = blk == 16 ? 256 : 16 * blk + below16(lut_s + 16 * blk);
+    for (int step = 128; step >= 1; step >>= 1) pos += lut_s[pos + step - 1] < e0 ? step : 0;
+    d0 = lut_s[255] < e0 ? 256 : pos;
   }
   // The tables sit in the partial-O space, 256 bytes a row: the entry of score s in row r is at column
   // (s & 255) ^ 4 r, so a lookup address is the row base with its low byte replaced by the swizzled score byte
   // (one v_perm), and the 32 rows' entries for one s fall in 32 different banks.
   // An entry is y = fma(lut[d], A, B - 1/2), within 2^-45 of n / S - 1/2 + 2^-40 and never a half-integer, so
   // adding 1.5 2^52 rounds it to n // S, which is then the low dword of the sum: two full-rate float64 operations.
+  // The four entries of a pass are written whatever dlow is (d clamped at 0): an entry with d < dlow either has
+  // d < d0, whose quotient is exactly 0, or d < 127 - max, whose score s < -128 wraps to the column of s + 256, a
+  // score above the row maximum that no kept key reads.
   constexpr int PT = 256;
   const int cx = 4 * l32;
   {
     const int part = 2 * w + half;                       // this lane's eighth of its row's table
-    int8_t* spare = reinterpret_cast<int8_t*>(&red_m[0][0]) + t;   // red_m is free: read before the last barrier
     int8_t* trow = ptab + l32 * PT;
     const int dlow = max(d0, 127 - mx);                  // d below 127 - max needs s < -128
     for (int d = 255 - part; d >= dlow; d -= 32) {      // four independent entries per pass, reads issued together
+      int du[4];
       double lv[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) lv[u] = lutd_s[max(d - 8 * u, 0)];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {                      // an entry below dlow goes to this thread's spare byte
-        const int du = d - 8 * u;
-        const int q = __double2loint(__builtin_fma(lv[u], qa, qb) + 0x1.8p52);
-        *(du >= dlow ? trow + (((du + mx - 255) & 255) ^ cx) : spare) = (int8_t)q;
+      for (int u = 0; u < 4; ++u) {
+        du[u] = max(d - 8 * u, 0);
+        lv[u] = lutd_s[du[u]];
       }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        trow[((du[u] + mx - 255) & 255) ^ cx] = (int8_t)__double2loint(__builtin_fma(lv[u], qa, qb) + 0x1.8p52);
     }
     __syncthreads();
   }
@@ -285,8 +279,9 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
     }
     if (a.causal && nt == ntiles - 1) {
       asm volatile("");                                  // keeps the masking on the diagonal tile's own path
+      const int lim = qrow - nt * 32 - 16 * half;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = nt * 32 + 16 * half + r <= qrow ? p[r] : 0;
+      for (int r = 0; r < 16; ++r) p[r] = r <= lim ? p[r] : 0;
     }
     v4i pf;
 #pragma unroll
