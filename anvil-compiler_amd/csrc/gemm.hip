@@ -632,14 +632,15 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
     stage(std::false_type{});
   __syncthreads();
 
+  // the staged tile leaves in 16-byte chunks, chunk idx = t + pass * G_THREADS of the tile: row idx / CH_ROW,
+  // column chunk idx % CH_ROW (a thread keeps one column chunk when CH_ROW divides the thread count)
   constexpr int CH_ROW = BN * OSZ / 16;
-  constexpr int ROWS_PER_PASS = G_THREADS / CH_ROW;
-  const int cc = t % CH_ROW, rr0 = t / CH_ROW;
+  static_assert((BM * CH_ROW) % G_THREADS == 0, "whole store passes");
+  constexpr int PASSES = BM * CH_ROW / G_THREADS;
+  auto rr_of = [&](int pass) { return (t + pass * G_THREADS) / CH_ROW; };
+  auto cf_of = [&](int pass) { return (t + pass * G_THREADS) % CH_ROW * 16 / OSZ; };   // first column
   char* Cb = reinterpret_cast<char*>(g.C) + (b0 * g.sc0 + b1 * g.sc1) * OSZ;
   const int cols_valid = min(BN, g.N - n0);
-  const int cfirst = cc * 16 / OSZ;
-  static_assert(BM % ROWS_PER_PASS == 0, "whole store passes");
-  constexpr int PASSES = BM / ROWS_PER_PASS;
   // interior tile: every chunk is read from LDS (and the residual from memory) before the first store, so the
   // reads' latencies overlap instead of serialising pass by pass
   const bool full = m0 + BM <= g.M && cols_valid == BN && (OSZ == 1 && g.res ? g.vec_res != 0 : g.vec_store != 0) &&
@@ -648,14 +649,14 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
     v4i ch[PASSES];
 #pragma unroll
     for (int pass = 0; pass < PASSES; ++pass)
-      ch[pass] = *reinterpret_cast<const v4i*>(srow(rr0 + pass * ROWS_PER_PASS) + cc * 16);
+      ch[pass] = *reinterpret_cast<const v4i*>(srow(rr_of(pass)) + cf_of(pass) * OSZ);
     if (OSZ == 1 && g.res) {
-      const int8_t* Rb = g.R + b0 * g.sr0 + b1 * g.sr1 + (long long)(m0 + rr0) * g.ldr + n0 + cfirst;
-      int8_t* Db = g.D + b0 * g.sd0 + b1 * g.sd1 + (long long)(m0 + rr0) * g.ldd + n0 + cfirst;
+      const int8_t* Rb = g.R + b0 * g.sr0 + b1 * g.sr1 + (long long)m0 * g.ldr + n0;
+      int8_t* Db = g.D + b0 * g.sd0 + b1 * g.sd1 + (long long)m0 * g.ldd + n0;
       v4i rv[PASSES];
 #pragma unroll
       for (int pass = 0; pass < PASSES; ++pass)
-        rv[pass] = *reinterpret_cast<const v4i*>(Rb + (long long)pass * ROWS_PER_PASS * g.ldr);
+        rv[pass] = *reinterpret_cast<const v4i*>(Rb + (long long)rr_of(pass) * g.ldr + cf_of(pass));
       const int ma = g.ma, mb = g.mb, rnd2 = g.rnd2, sh2 = g.shift2;
 #pragma unroll
       for (int pass = 0; pass < PASSES; ++pass) {
@@ -673,22 +674,22 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
           const unsigned t23 = __builtin_amdgcn_perm((unsigned)o[3], (unsigned)o[2], 0x0c0c0400u);
           ov[q] = (int)__builtin_amdgcn_perm(t23, t01, 0x05040100u);
         }
-        *reinterpret_cast<v4i*>(Db + (long long)pass * ROWS_PER_PASS * g.ldd) = ov;
+        *reinterpret_cast<v4i*>(Db + (long long)rr_of(pass) * g.ldd + cf_of(pass)) = ov;
       }
       if (!g.store_y) return;
     }
-    char* Cr = Cb + ((long long)(m0 + rr0) * g.ldc + n0 + cfirst) * OSZ;
+    char* Cr = Cb + ((long long)m0 * g.ldc + n0) * OSZ;
 #pragma unroll
     for (int pass = 0; pass < PASSES; ++pass)
-      *reinterpret_cast<v4i*>(Cr + (long long)pass * ROWS_PER_PASS * g.ldc * OSZ) = ch[pass];
+      *reinterpret_cast<v4i*>(Cr + ((long long)rr_of(pass) * g.ldc + cf_of(pass)) * OSZ) = ch[pass];
     return;
   }
 #pragma unroll
   for (int pass = 0; pass < PASSES; ++pass) {
-    const int rr = rr0 + pass * ROWS_PER_PASS;
+    const int rr = rr_of(pass), cfirst = cf_of(pass);
     const int m = m0 + rr;
-    if (m >= g.M) break;
-    const int8_t* src = srow(rr) + cc * 16;
+    if (m >= g.M) break;                                 // rows grow with the pass
+    const int8_t* src = srow(rr) + cfirst * OSZ;
     if (OSZ == 1 && g.res) {
       // the fused add_requant: 16 results from the staged y chunk and the residual chunk at the same position
       const int8_t* rp = g.R + b0 * g.sr0 + b1 * g.sr1 + (long long)m * g.ldr + n0 + cfirst;
@@ -948,6 +949,9 @@ static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s,
     case 15: return launch_fast<256, 128, 2, 4, MUL24>(g, osz, batch, s);
     case 16: return launch_fast<256, 128, 2, 3, MUL24>(g, osz, batch, s);
     case 17: return launch_fast<128, 256, 2, 3, MUL24>(g, osz, batch, s);
+    case 18: return launch_fast<128, 192, 2, 3, MUL24>(g, osz, batch, s);
+    case 19: return launch_fast<256, 192, 2, 3, MUL24>(g, osz, batch, s);
+    case 20: return launch_fast<256, 192, 2, 4, MUL24>(g, osz, batch, s);
     default: break;
   }
   // measured on MI355X (block GEMM shapes, K 768 and 3072): wide products with at least six 256 x 256 tiles per CU
@@ -956,6 +960,12 @@ static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s,
   // keep the 128 x 128 tile (more workgroups)
   const long long tiles256 = (long long)((g.M + 255) / 256) * ((g.N + 255) / 256) * batch;
   if (persist_ok && g.N >= 2048 && tiles256 >= 6ll * num_cu) return persist();
+  // long K with N a multiple of 192 below 2048 (N 768, K 3072 measured): 256 x 192 tiles, one workgroup per CU with
+  // two or more whole tiles each, ahead of 256 x 128's one and a half rounds of two workgroups per CU -- but not with
+  // the fused residual add, whose heavier epilogue then runs with no second workgroup beside it (slower than 256 x 128)
+  const long long tiles192 = (long long)((g.M + 255) / 256) * (g.N / 192) * batch;
+  if (g.K >= 2048 && g.N % 192 == 0 && g.N < 2048 && !g.res && tiles192 >= 2ll * num_cu)
+    return launch_fast<256, 192, 2, 3, MUL24>(g, osz, batch, s);
   if ((long long)g.M * g.N * batch >= 256ll * 128 * 512 && g.M >= 256 && g.N >= 128)
     launch_fast<256, 128, 2, 3, MUL24>(g, osz, batch, s);
   else

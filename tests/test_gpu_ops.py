@@ -340,7 +340,23 @@ def test_gemm_with_fused_residual_add(dev, M, K, N, store_y):
 def test_gemm_wide_products_take_the_persistent_kernel(dev, M, N, K, dtype, lut, add):
     """Products with N >= 2048 and at least six 256 x 256 tiles per CU run on the persistent kernel (register epilogue,
     permuted B rows). Checked on sampled rows, the first and last 256 among them (edge rows and columns included)."""
-    rng = np.random.default_rng([41, M, N, K])
+    _check_sampled_gemm(dev, M, N, K, dtype, lut, add, 41)
+
+
+@pytest.mark.parametrize("M,N,K,dtype,lut,add", [(32768 + 37, 768, 3072, "i8", False, False),
+                                                 (32768, 1536, 2048, "i8", True, False),
+                                                 (33000, 768, 2048, "i16", False, False),
+                                                 (32768, 768, 3072, "i8", False, True)])
+def test_gemm_long_k_narrow_n_takes_256x192_tiles(dev, M, N, K, dtype, lut, add):
+    """K >= 2048 with N a multiple of 192 below 2048 and two or more 256 x 192 tiles per CU (the block's proj shape)
+    runs on 256 x 192 tiles unless the residual add is fused: 12 16-byte chunks a staged row, so a thread's chunks
+    change column between store passes. Ragged M exercises the partial-tile epilogue, and an i16 result and a LUT are
+    included; the fused-add case (256 x 128 tiles) checks the dispatch keeps it correct too."""
+    _check_sampled_gemm(dev, M, N, K, dtype, lut, add, 43)
+
+
+def _check_sampled_gemm(dev, M, N, K, dtype, lut, add, seed):
+    rng = np.random.default_rng([seed, M, N, K])
     a, w = rng.integers(-128, 128, (M, K), dtype=np.int8), rng.integers(-128, 128, (K, N), dtype=np.int8)
     rows = np.unique(np.concatenate([np.arange(256), np.arange(M - 256, M), rng.integers(0, M, 512)]))
     acc = sem.matmul_i8(a[rows].astype(np.int64), w.astype(np.int64), fast=True)   # float64 BLAS, exact here

@@ -1,11 +1,13 @@
 """Host checks of the integer identities the HIP kernels rely on, evaluated exactly on the CPU.
 
-The fused attention kernel (csrc/attention.hip) divides p = (e one + S // 2) // S as trunc(fma(e, A, B)) in float64
-with A = fl(one / S) and B = fl(fl((S // 2) / S) + 2^-40). Here fma is emulated exactly (the exact rational e A + B
-rounded once to the nearest double, which Python's float(Fraction) does) and compared with integer floor division on
-the cases where a floating-point quotient is most fragile: exact multiples n = k S and their neighbours, the largest
-divisors, and random draws.
+The fused attention kernel (csrc/attention.hip) divides p = (e one + S // 2) // S in float64 as
+y = fma(e, A, B - 1/2) with A = fl(one / S) and B = fl(fl((S // 2) / S) + 2^-40), then takes the low dword of
+fl(y + 1.5 2^52), i.e. y rounded to the nearest integer: floor(y + 1/2). Here fma is emulated exactly (the exact
+rational e A + B' rounded once to the nearest double, which Python's float(Fraction) does), the addition is an IEEE
+double addition, and the result is compared with integer floor division on the cases where a floating-point quotient
+is most fragile: exact multiples n = k S and their neighbours, the largest divisors, and random draws.
 """
+import struct
 from fractions import Fraction
 
 import numpy as np
@@ -16,11 +18,20 @@ def fdiv(a, b):
     return a / b                                  # IEEE double division, correctly rounded
 
 
-def kernel_quot(e, one, S):
+MAGIC = 1.5 * 2.0 ** 52
+
+
+def low_dword(x):
+    """The low 32 bits of a double's bit pattern, as a signed int."""
+    lo = struct.unpack("<Q", struct.pack("<d", x))[0] & 0xFFFFFFFF
+    return lo - (1 << 32) if lo >= 1 << 31 else lo
+
+
+def kernel_quot(e, one, S, eps=2.0 ** -40):
     A = fdiv(float(one), float(S))
-    B = fdiv(float(S >> 1), float(S)) + 2.0 ** -40
+    B = fdiv(float(S >> 1), float(S)) + eps - 0.5         # as the kernel: the - 0.5 is exact
     y = float(Fraction(e) * Fraction(A) + Fraction(B))   # fma: one rounding of the exact value
-    return int(y)                                         # truncation toward zero
+    return low_dword(y + MAGIC)                           # rounded to nearest, read from the mantissa
 
 
 def cases():
@@ -48,17 +59,31 @@ NEEDS_EPSILON = [(344077939, 2, 458770585), (334444885, 3, 668889770), (33552814
                  (18999029, 28, 151992232)]
 
 
+def in_domain(e, one, S):
+    """The kernel divides only quotients below 128: S sums the row's exp values, this key's own included, so
+    e <= S and n // S <= one <= 127 (the error bound assumes |y| < 128)."""
+    return (e * one + (S >> 1)) // S < 128
+
+
 def test_float64_division_is_exact_floor_division():
-    bad = [(e, one, S) for e, one, S in cases() + NEEDS_EPSILON
-           if kernel_quot(e, one, S) != (e * one + (S >> 1)) // S]
+    todo = [c for c in cases() + NEEDS_EPSILON if in_domain(*c)]
+    assert len(todo) > 500
+    bad = [(e, one, S) for e, one, S in todo if kernel_quot(e, one, S) != (e * one + (S >> 1)) // S]
     assert not bad, bad[:5]
 
 
 def test_the_epsilon_term_is_needed():
-    """Dropping the 2^-40 term truncates an exact quotient k to k - 1: the cases above pin it."""
+    """Dropping the 2^-40 term rounds an exact quotient k to k - 1: the cases above pin it."""
     for e, one, S in NEEDS_EPSILON:
-        A, B = float(one) / float(S), float(S >> 1) / float(S)
-        assert int(float(Fraction(e) * Fraction(A) + Fraction(B))) == (e * one + (S >> 1)) // S - 1
+        assert kernel_quot(e, one, S, eps=0.0) == (e * one + (S >> 1)) // S - 1
+
+
+def test_the_rounding_constant_reads_back_small_integers():
+    """fl(y + 1.5 2^52) holds round(y) in its low dword for y in (-1/2, 128), the kernel's range (never a tie)."""
+    for k in range(128):
+        for y in (k - 0.499, k - 0.25, float(k), k + 0.25, k + 0.499):
+            if y > -0.5:
+                assert low_dword(y + MAGIC) == round(y), y
 
 
 @pytest.mark.parametrize("S", [1, 2, 5, 1 << 16, (1 << 31) - 1])
@@ -67,4 +92,5 @@ def test_every_quotient_of_a_small_range(S):
     h = S >> 1
     top = min(((1 << 31) - 1 - h) // one, 4000)
     for e in range(top + 1):
-        assert kernel_quot(e, one, S) == (e * one + h) // S, (e, S)
+        if in_domain(e, one, S):
+            assert kernel_quot(e, one, S) == (e * one + h) // S, (e, S)
