@@ -942,6 +942,10 @@ static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s,
   auto persist = [&] { launch_persist<256, 256, 64, 4, MUL24, 8, 2>(g, osz, batch, num_cu, s); };
   switch (cfg) {
     case 39: if (persist_ok) return persist(); break;
+    case 40:
+      if (g.causal == 0 && ((g.K + 127) / 128) % 3 == 0)
+        return launch_persist<256, 128, 128, 3, MUL24, 8, 2>(g, osz, batch, num_cu, s);
+      break;
     case 11: return launch_fast<256, 256, 2, 3, MUL24>(g, osz, batch, s);
     case 12: return launch_fast<256, 256, 2, 4, MUL24>(g, osz, batch, s);
     case 13: return launch_fast<128, 128, 2, 3, MUL24>(g, osz, batch, s);
@@ -960,9 +964,15 @@ static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s,
   // keep the 128 x 128 tile (more workgroups)
   const long long tiles256 = (long long)((g.M + 255) / 256) * ((g.N + 255) / 256) * batch;
   if (persist_ok && g.N >= 2048 && tiles256 >= 6ll * num_cu) return persist();
-  // long K with N a multiple of 192 below 2048 (N 768, K 3072 measured): 256 x 192 tiles, one workgroup per CU with
-  // two or more whole tiles each, ahead of 256 x 128's one and a half rounds of two workgroups per CU -- but not with
-  // the fused residual add, whose heavier epilogue then runs with no second workgroup beside it (slower than 256 x 128)
+  // Long K, N below 2048 (the block's proj, K 3072, N 768): the persistent kernel on 256 x 128 tiles with 128-byte
+  // K blocks. Its loads fetch 128 contiguous bytes of each row (the 64-byte rows of a K block of 64 reach about half
+  // the L2 bandwidth), and the tiles (768 at proj) divide evenly over one workgroup per CU. Measured: proj 87.5 ->
+  // 82.5 us alone, about 5 us a step with its fused residual add. Short K (q, y) gains nothing and fc loses on it.
+  // Otherwise, N a multiple of 192 without a fused add: 256 x 192 tiles, one workgroup per CU with whole tiles
+  // (with the fused add its heavier epilogue has no second workgroup beside it and loses to 256 x 128).
+  const long long tiles128 = (long long)((g.M + 255) / 256) * ((g.N + 127) / 128) * batch;
+  if (g.K >= 2048 && g.N < 2048 && g.causal == 0 && ((g.K + 127) / 128) % 3 == 0 && tiles128 >= 2ll * num_cu)
+    return launch_persist<256, 128, 128, 3, MUL24, 8, 2>(g, osz, batch, num_cu, s);
   const long long tiles192 = (long long)((g.M + 255) / 256) * (g.N / 192) * batch;
   if (g.K >= 2048 && g.N % 192 == 0 && g.N < 2048 && !g.res && tiles192 >= 2ll * num_cu)
     return launch_fast<256, 192, 2, 3, MUL24>(g, osz, batch, s);

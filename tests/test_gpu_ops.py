@@ -347,11 +347,12 @@ def test_gemm_wide_products_take_the_persistent_kernel(dev, M, N, K, dtype, lut,
                                                  (32768, 1536, 2048, "i8", True, False),
                                                  (33000, 768, 2048, "i16", False, False),
                                                  (32768, 768, 3072, "i8", False, True)])
-def test_gemm_long_k_narrow_n_takes_256x192_tiles(dev, M, N, K, dtype, lut, add):
-    """K >= 2048 with N a multiple of 192 below 2048 and two or more 256 x 192 tiles per CU (the block's proj shape)
-    runs on 256 x 192 tiles unless the residual add is fused: 12 16-byte chunks a staged row, so a thread's chunks
-    change column between store passes. Ragged M exercises the partial-tile epilogue, and an i16 result and a LUT are
-    included; the fused-add case (256 x 128 tiles) checks the dispatch keeps it correct too."""
+def test_gemm_long_k_narrow_n(dev, M, N, K, dtype, lut, add):
+    """K >= 2048 with N below 2048 (the block's proj shape). K a multiple of 384 (24 K blocks of 128) runs on the
+    persistent kernel with 256 x 128 tiles and 128-byte K blocks, the fused residual add included; K 2048 (16 blocks)
+    with N a multiple of 192 runs on 256 x 192 tiles, whose staged epilogue has 12 16-byte chunks a row (a thread's
+    chunks change column between store passes). Ragged M exercises the partial-tile epilogues; an i16 result and a
+    LUT are included."""
     _check_sampled_gemm(dev, M, N, K, dtype, lut, add, 43)
 
 
