@@ -150,6 +150,7 @@ class CompiledModel:
         self._const_views = {}
         self._const_bt = {}
         self._plans = {}
+        self.group_gemms = True           # independent consecutive GEMMs as one anvil_gemm_i8_group call
 
     # --------------------------------------------------------------------------------------- layout choice
     def _choose_layouts(self) -> dict:
@@ -339,6 +340,8 @@ class CompiledModel:
                                                       int(op.s), out.size, out])
             else:
                 raise NotImplementedError(op.name)
+        if self.group_gemms:
+            _group_gemms(P)
         return P
 
     def _softmax_lut_ok(self, op) -> bool:
@@ -882,6 +885,46 @@ def _work(fn, args):
 def _call_gemm(dev, a: View, bt: View, c: View, b0, b1, M, N, K, strides, op, lut, out_dtype, flags=0):
     dev.gemm_i8(a.ptr, bt.ptr, c.ptr, b0, b1, M, N, K, strides, int(op.M), int(op.s),
                 None if lut is None else lut.ptr, out_dtype, flags)
+
+
+def _call_gemm_group(dev, calls):
+    dev.gemm_i8_group([(a.ptr, bt.ptr, c.ptr, b0, b1, M, N, K, strides, int(op.M), int(op.s),
+                        None if lut is None else lut.ptr, out_dtype, flags)
+                       for _, a, bt, c, b0, b1, M, N, K, strides, op, lut, out_dtype, flags in calls])
+
+
+def _gemm_bufs(args):
+    """(buffers read, buffers written) of a _call_gemm step."""
+    _, a, bt, c, *_rest = args
+    lut = args[11]
+    return {id(a.buf), id(bt.buf)} | ({id(lut.buf)} if lut is not None else set()), {id(c.buf)}
+
+
+def _group_gemms(P):
+    """Merge runs of consecutive _call_gemm steps of which none writes a buffer another one reads or writes (q, k and
+    v of one input) into _call_gemm_group steps of at most GEMM_GROUP_MAX products: the library runs such a group as
+    one launch when its members share a kernel."""
+    steps, works = [], []
+    i, n = 0, len(P.steps)
+    while i < n:
+        j = i + 1
+        if P.steps[i][1] is _call_gemm:
+            reads, writes = _gemm_bufs(P.steps[i][2])
+            while j < n and j - i < rt.GEMM_GROUP_MAX and P.steps[j][1] is _call_gemm:
+                r, w = _gemm_bufs(P.steps[j][2])
+                if w & (reads | writes) or r & writes:
+                    break
+                reads, writes = reads | r, writes | w
+                j += 1
+        if j - i == 1:
+            steps.append(P.steps[i])
+            works.append(P.works[i])
+        else:
+            run = P.steps[i:j]
+            steps.append(("+".join(lb for lb, _, _ in run), _call_gemm_group, (run[0][2][0], [a for _, _, a in run])))
+            works.append(("gemm", sum(w[1] for w in P.works[i:j]), sum(w[2] for w in P.works[i:j])))
+        i = j
+    P.steps, P.works = steps, works
 
 
 def _call_attention(dev, q: View, k: View, v: View, o: View, b0, b1, T, D, strides, s_op, sm, o_op, lut: View,

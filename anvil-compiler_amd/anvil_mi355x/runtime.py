@@ -49,6 +49,7 @@ SIGNATURES = {
     "anvil_event_elapsed": [_p, _i, _i, C.POINTER(C.c_float)],
     "anvil_gemm_i8": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i],
     "anvil_gemm_i8_ex": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _i],
+    "anvil_gemm_i8_group": [_p, _p, _i],
     "anvil_gemm_i8_add": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _p, _i32, _i32, _i, _p, _p, _i],
     "anvil_rmsnorm_int": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p],
     "anvil_rmsnorm_int_ex": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p, _i],
@@ -63,6 +64,16 @@ SIGNATURES = {
     "anvil_embed_quantize": [_p, _p, _i64, _i, _i, _p, _i, _p, _f64, _p, _i],
 }
 
+
+
+class GemmDesc(C.Structure):
+    """anvil_gemm_desc: the arguments of one anvil_gemm_i8_ex call."""
+    _fields_ = [("A", _p), ("Bt", _p), ("C", _p), ("lut", _p), ("strides", _i64 * 9), ("batch0", _i32),
+                ("batch1", _i32), ("M", _i32), ("N", _i32), ("K", _i32), ("mult", _i32), ("shift", _i32),
+                ("out_dtype", _i32), ("flags", _i32)]
+
+
+GEMM_GROUP_MAX = 4
 _lib = None
 _lock = threading.Lock()
 
@@ -184,6 +195,17 @@ class Device:
         self.lib.call("anvil_gemm_i8_ex", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)), C.c_void_p(_ptr(Cp)),
                       batch0, batch1, M, N, K, st, int(mult), shift, C.c_void_p(_ptr(lut) if lut is not None else 0),
                       DTYPE_CODE[out_dtype], int(flags))
+
+    def gemm_i8_group(self, calls):
+        """Independent gemm_i8 calls (tuples of its arguments) in one anvil_gemm_i8_group call."""
+        descs = (GemmDesc * len(calls))()
+        for d, (A, Bt, Cp, b0, b1, M, N, K, strides, mult, shift, lut, out_dtype, flags) in zip(descs, calls):
+            d.A, d.Bt, d.C = _ptr(A), _ptr(Bt), _ptr(Cp)
+            d.lut = _ptr(lut) if lut is not None else None
+            d.strides[:] = [int(s) for s in strides]
+            d.batch0, d.batch1, d.M, d.N, d.K = b0, b1, M, N, K
+            d.mult, d.shift, d.out_dtype, d.flags = int(mult), shift, DTYPE_CODE[out_dtype], int(flags)
+        self.lib.call("anvil_gemm_i8_group", self.ctx, descs, len(calls))
 
     def gemm_i8_add(self, A, Bt, Cp, batch0, batch1, M, N, K, strides, mult, shift, lut, R, ma, mb, shift2, D,
                     rstrides, flags):

@@ -428,8 +428,10 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
   }
 }
 
+// One output tile of the fast kernel: logical tile pid of batch entry bz (the XCD remap below assumes pid and the
+// workgroup id agree modulo 8).
 template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24>
-__global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8_fast(GemmArgs g) {
+__device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int bz) {
   constexpr int BK = 64, CPR = BK / 16;
   constexpr int WGN = 4 / WGM;
   constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
@@ -455,7 +457,6 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
   const int wm = wave / WGN, wn = wave % WGN;
 
   const int ntiles = g.tiles_m * g.tiles_n;
-  int pid = blockIdx.x;
   if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
   const int in_group = GROUP_M * g.tiles_n;
   const int first_m = (pid / in_group) * GROUP_M;
@@ -465,7 +466,7 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
   const int m0 = tile_m * BM, n0 = tile_n * BN;
   if (g.causal == 1 && n0 > m0 + BM - 1) return;
 
-  const int b0 = blockIdx.y / g.batch1, b1 = blockIdx.y % g.batch1;
+  const int b0 = bz / g.batch1, b1 = bz % g.batch1;
   const int8_t* Ab = g.A + b0 * g.sa0 + b1 * g.sa1 + (long long)m0 * g.lda;
   const int8_t* Bb = g.B + b0 * g.sb0 + b1 * g.sb1 + (long long)n0 * g.ldb;
   const int rows_a = min(g.M - m0, BM), rows_b = min(g.N - n0, BN);
@@ -732,6 +733,35 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
   }
 }
 
+template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24>
+__global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8_fast(GemmArgs g) {
+  fast_tile<BM, BN, WGM, NS, OSZ, MUL24>(g, blockIdx.x, blockIdx.y);
+}
+
+// Up to GEMM_GROUP_MAX independent products in one launch (q, k and v of one input, say): member i owns the
+// workgroups [first[i], first[i + 1]) (first[i] a multiple of 8, so each member's tiles keep their XCD placement),
+// batch entry by batch entry like the single kernel's grid. One grid leaves one tail where separate launches leave
+// one per product, and the launch gaps between them go.
+constexpr int GEMM_GROUP_MAX = 4;
+struct GemmGroupArgs {
+  GemmArgs g[GEMM_GROUP_MAX];
+  int first[GEMM_GROUP_MAX + 1];
+  int n;
+};
+
+template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24>
+__global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8_fast_group(GemmGroupArgs a) {
+  const int w = blockIdx.x;
+  int i = 0;
+#pragma unroll
+  for (int j = 1; j < GEMM_GROUP_MAX; ++j) i += (j < a.n && w >= a.first[j]) ? 1 : 0;
+  const GemmArgs& g = a.g[i];
+  const int ntiles = g.tiles_m * g.tiles_n, local = w - a.first[i];
+  const int bz = local / ntiles;
+  if (bz >= g.nbatch) return;                            // padding up to the next member's multiple of 8
+  fast_tile<BM, BN, WGM, NS, OSZ, MUL24>(g, local - bz * ntiles, bz);
+}
+
 // Persistent kernel with a register epilogue. Bt rows are loaded into LDS permuted within each 32-row group (LDS row c
 // holds Bt row bperm(c)), so accumulator r of lane l is output column 16 (l / 32) + r of its 32 x 32 tile: each lane
 // owns 16 consecutive columns of one row and writes them with one 16-byte store (two for i16), with no LDS staging.
@@ -935,35 +965,42 @@ static void launch_fast(GemmArgs& g, int osz, int batch, hipStream_t s) {
     hipLaunchKernelGGL((gemm_i8_fast<BM, BN, WGM, NS, 2, MUL24>), grid, dim3(G_THREADS), 0, s, g);
 }
 
-template <bool MUL24>
-static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s, int cfg, int num_cu) {
+template <int BM, int BN, int WGM, int NS, bool MUL24>
+static bool launch_fast_group(GemmArgs* gs, const int* batch, int n, int osz, hipStream_t s) {
+  GemmGroupArgs a{};
+  long long w = 0;
+  for (int i = 0; i < n; ++i) {
+    gs[i].tiles_m = (gs[i].M + BM - 1) / BM;
+    gs[i].tiles_n = (gs[i].N + BN - 1) / BN;
+    gs[i].nbatch = batch[i];
+    a.g[i] = gs[i];
+    a.first[i] = (int)w;
+    w += ((long long)gs[i].tiles_m * gs[i].tiles_n * batch[i] + 7) / 8 * 8;
+    if (w > (1ll << 31) - 1) return false;
+  }
+  a.first[n] = (int)w;
+  a.n = n;
+  if (osz == 1)
+    hipLaunchKernelGGL((gemm_i8_fast_group<BM, BN, WGM, NS, 1, MUL24>), dim3((unsigned)w), dim3(G_THREADS), 0, s, a);
+  else
+    hipLaunchKernelGGL((gemm_i8_fast_group<BM, BN, WGM, NS, 2, MUL24>), dim3((unsigned)w), dim3(G_THREADS), 0, s, a);
+  return true;
+}
+
+// The fast-path configuration of a product, named by the context's benchmarking override values: 39 and 40 the
+// persistent 256 x 256 (K blocks of 64) and 256 x 128 (K blocks of 128) kernels, 11 - 20 the one-tile-per-workgroup
+// shapes of the switch in launch_fast_choice. An override the product cannot take falls through to the rules.
+static int fast_choice(const GemmArgs& g, int batch, int cfg, int num_cu) {
   // the persistent 256 x 256 kernel: one workgroup of 8 waves per CU, four 32 KiB LDS stages, wave tiles 64 x 128
   const bool persist_ok = g.causal == 0 && ((g.K + 63) / 64) % 4 == 0;
-  auto persist = [&] { launch_persist<256, 256, 64, 4, MUL24, 8, 2>(g, osz, batch, num_cu, s); };
-  switch (cfg) {
-    case 39: if (persist_ok) return persist(); break;
-    case 40:
-      if (g.causal == 0 && ((g.K + 127) / 128) % 3 == 0)
-        return launch_persist<256, 128, 128, 3, MUL24, 8, 2>(g, osz, batch, num_cu, s);
-      break;
-    case 11: return launch_fast<256, 256, 2, 3, MUL24>(g, osz, batch, s);
-    case 12: return launch_fast<256, 256, 2, 4, MUL24>(g, osz, batch, s);
-    case 13: return launch_fast<128, 128, 2, 3, MUL24>(g, osz, batch, s);
-    case 14: return launch_fast<128, 128, 2, 4, MUL24>(g, osz, batch, s);
-    case 15: return launch_fast<256, 128, 2, 4, MUL24>(g, osz, batch, s);
-    case 16: return launch_fast<256, 128, 2, 3, MUL24>(g, osz, batch, s);
-    case 17: return launch_fast<128, 256, 2, 3, MUL24>(g, osz, batch, s);
-    case 18: return launch_fast<128, 192, 2, 3, MUL24>(g, osz, batch, s);
-    case 19: return launch_fast<256, 192, 2, 3, MUL24>(g, osz, batch, s);
-    case 20: return launch_fast<256, 192, 2, 4, MUL24>(g, osz, batch, s);
-    default: break;
-  }
+  const bool persist128_ok = g.causal == 0 && ((g.K + 127) / 128) % 3 == 0;
+  if ((cfg == 39 && persist_ok) || (cfg == 40 && persist128_ok) || (cfg >= 11 && cfg <= 20)) return cfg;
   // measured on MI355X (block GEMM shapes, K 768 and 3072): wide products with at least six 256 x 256 tiles per CU
   // take the persistent kernel (it halves the L2 traffic per MFMA of the 256 x 128 tile); 256 x 128 tiles with three
   // LDS stages (72 KiB) run two workgroups per CU, which hide each other's pipeline fill and epilogue; small problems
   // keep the 128 x 128 tile (more workgroups)
   const long long tiles256 = (long long)((g.M + 255) / 256) * ((g.N + 255) / 256) * batch;
-  if (persist_ok && g.N >= 2048 && tiles256 >= 6ll * num_cu) return persist();
+  if (persist_ok && g.N >= 2048 && tiles256 >= 6ll * num_cu) return 39;
   // Long K, N below 2048 (the block's proj, K 3072, N 768): the persistent kernel on 256 x 128 tiles with 128-byte
   // K blocks. Its loads fetch 128 contiguous bytes of each row (the 64-byte rows of a K block of 64 reach about half
   // the L2 bandwidth), and the tiles (768 at proj) divide evenly over one workgroup per CU. Measured: proj 87.5 ->
@@ -971,15 +1008,29 @@ static void launch_fast_by_shape(GemmArgs& g, int osz, int batch, hipStream_t s,
   // Otherwise, N a multiple of 192 without a fused add: 256 x 192 tiles, one workgroup per CU with whole tiles
   // (with the fused add its heavier epilogue has no second workgroup beside it and loses to 256 x 128).
   const long long tiles128 = (long long)((g.M + 255) / 256) * ((g.N + 127) / 128) * batch;
-  if (g.K >= 2048 && g.N < 2048 && g.causal == 0 && ((g.K + 127) / 128) % 3 == 0 && tiles128 >= 2ll * num_cu)
-    return launch_persist<256, 128, 128, 3, MUL24, 8, 2>(g, osz, batch, num_cu, s);
+  if (g.K >= 2048 && g.N < 2048 && persist128_ok && tiles128 >= 2ll * num_cu) return 40;
   const long long tiles192 = (long long)((g.M + 255) / 256) * (g.N / 192) * batch;
-  if (g.K >= 2048 && g.N % 192 == 0 && g.N < 2048 && !g.res && tiles192 >= 2ll * num_cu)
-    return launch_fast<256, 192, 2, 3, MUL24>(g, osz, batch, s);
-  if ((long long)g.M * g.N * batch >= 256ll * 128 * 512 && g.M >= 256 && g.N >= 128)
-    launch_fast<256, 128, 2, 3, MUL24>(g, osz, batch, s);
-  else
-    launch_fast<128, 128, 2, 3, MUL24>(g, osz, batch, s);
+  if (g.K >= 2048 && g.N % 192 == 0 && g.N < 2048 && !g.res && tiles192 >= 2ll * num_cu) return 19;
+  if ((long long)g.M * g.N * batch >= 256ll * 128 * 512 && g.M >= 256 && g.N >= 128) return 16;
+  return 13;
+}
+
+template <bool MUL24>
+static void launch_fast_choice(GemmArgs& g, int osz, int batch, hipStream_t s, int choice, int num_cu) {
+  switch (choice) {
+    case 39: return launch_persist<256, 256, 64, 4, MUL24, 8, 2>(g, osz, batch, num_cu, s);
+    case 40: return launch_persist<256, 128, 128, 3, MUL24, 8, 2>(g, osz, batch, num_cu, s);
+    case 11: return launch_fast<256, 256, 2, 3, MUL24>(g, osz, batch, s);
+    case 12: return launch_fast<256, 256, 2, 4, MUL24>(g, osz, batch, s);
+    case 14: return launch_fast<128, 128, 2, 4, MUL24>(g, osz, batch, s);
+    case 15: return launch_fast<256, 128, 2, 4, MUL24>(g, osz, batch, s);
+    case 16: return launch_fast<256, 128, 2, 3, MUL24>(g, osz, batch, s);
+    case 17: return launch_fast<128, 256, 2, 3, MUL24>(g, osz, batch, s);
+    case 18: return launch_fast<128, 192, 2, 3, MUL24>(g, osz, batch, s);
+    case 19: return launch_fast<256, 192, 2, 3, MUL24>(g, osz, batch, s);
+    case 20: return launch_fast<256, 192, 2, 4, MUL24>(g, osz, batch, s);
+    default: return launch_fast<128, 128, 2, 3, MUL24>(g, osz, batch, s);
+  }
 }
 
 template <int BM, int BN, int BK, int WGM, int PF, bool CHECKED>
@@ -1033,9 +1084,17 @@ struct AddEpilogue {
   int ma, mb, shift2;
 };
 
-static int gemm_entry(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
-                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
-                      int flags, const AddEpilogue* add) {
+// A validated product and the kernel family it takes.
+struct Prepared {
+  GemmArgs g;
+  int osz, batch;
+  bool checked, vec, fast, mul24;
+};
+
+// Argument checks that need no context (a group checks every member before any launch).
+static int gemm_validate(const int8_t* A, const int8_t* Bt, const void* C, int batch0, int batch1, int M, int N, int K,
+                         const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype, int flags,
+                         const AddEpilogue* add) {
   if (!A || !Bt || (!C && !add) || !strides) return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: null pointer");
   if (batch0 < 1 || batch1 < 1 || M < 1 || N < 1 || K < 1)
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: non-positive size (batch %d x %d, M %d, N %d, K %d)", batch0,
@@ -1058,6 +1117,14 @@ static int gemm_entry(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C
     if (out_dtype != ANVIL_I8) return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_add: i8 results only");
     if (add->shift2 < 0 || add->shift2 > 31) return set_error(ANVIL_E_VALUE, "shift %d outside [0, 31]", add->shift2);
   }
+  return ANVIL_OK;
+}
+
+static int gemm_prepare(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
+                        int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut,
+                        int out_dtype, int flags, const AddEpilogue* add, Prepared& p) {
+  if (int r = gemm_validate(A, Bt, C, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags, add))
+    return r;
   if (int r = check_ctx(ctx)) return r;
   GemmArgs g{};
   g.A = A;
@@ -1107,14 +1174,64 @@ static int gemm_entry(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C
     g.vec_res = aligned16(g.R) && aligned16(g.D) && ok16(g.ldr) && ok16(g.ldd) &&
                 (batch0 == 1 || (ok16(g.sr0) && ok16(g.sd0))) && (batch1 == 1 || (ok16(g.sr1) && ok16(g.sd1)));
   }
-  if (fast) {
-    if (flags & ANVIL_GEMM_MUL24)
-      launch_fast_by_shape<true>(g, osz, batch0 * batch1, ctx->stream, ctx->gemm_cfg, ctx->num_cu);
-    else
-      launch_fast_by_shape<false>(g, osz, batch0 * batch1, ctx->stream, ctx->gemm_cfg, ctx->num_cu);
-  } else {
-    launch_gemm(g, checked, osz, vec, batch0 * batch1, ctx->stream, ctx->gemm_cfg);
+  p.g = g;
+  p.osz = osz;
+  p.batch = batch0 * batch1;
+  p.checked = checked;
+  p.vec = vec;
+  p.fast = fast;
+  p.mul24 = (flags & ANVIL_GEMM_MUL24) != 0;
+  return ANVIL_OK;
+}
+
+static void gemm_launch(anvil_ctx* ctx, Prepared& p) {
+  if (!p.fast) return launch_gemm(p.g, p.checked, p.osz, p.vec, p.batch, ctx->stream, ctx->gemm_cfg);
+  const int choice = fast_choice(p.g, p.batch, ctx->gemm_cfg, ctx->num_cu);
+  if (p.mul24)
+    launch_fast_choice<true>(p.g, p.osz, p.batch, ctx->stream, choice, ctx->num_cu);
+  else
+    launch_fast_choice<false>(p.g, p.osz, p.batch, ctx->stream, choice, ctx->num_cu);
+}
+
+static int gemm_entry(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
+                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
+                      int flags, const AddEpilogue* add) {
+  Prepared p;
+  if (int r = gemm_prepare(ctx, A, Bt, C, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags, add, p))
+    return r;
+  gemm_launch(ctx, p);
+  ANVIL_LAUNCHED();
+  return ANVIL_OK;
+}
+
+// Independent products in one launch when every one of them takes the 256 x 128 one-tile-per-workgroup kernel with
+// the same result type and requant multiply, else one launch each (in order).
+extern "C" int anvil_gemm_i8_group(anvil_ctx* ctx, const anvil_gemm_desc* d, int count) {
+  if (!d) return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_group: null pointer");
+  if (count < 1 || count > GEMM_GROUP_MAX)
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_group: count %d outside [1, %d]", count, GEMM_GROUP_MAX);
+  for (int i = 0; i < count; ++i)
+    if (int r = gemm_validate(d[i].A, d[i].Bt, d[i].C, d[i].batch0, d[i].batch1, d[i].M, d[i].N, d[i].K, d[i].strides,
+                              d[i].mult, d[i].shift, d[i].lut, d[i].out_dtype, d[i].flags, nullptr))
+      return r;
+  Prepared p[GEMM_GROUP_MAX];
+  for (int i = 0; i < count; ++i)
+    if (int r = gemm_prepare(ctx, d[i].A, d[i].Bt, d[i].C, d[i].batch0, d[i].batch1, d[i].M, d[i].N, d[i].K,
+                             d[i].strides, d[i].mult, d[i].shift, d[i].lut, d[i].out_dtype, d[i].flags, nullptr, p[i]))
+      return r;
+  bool one = count > 1;
+  for (int i = 0; i < count && one; ++i)
+    one = p[i].fast && p[i].osz == p[0].osz && p[i].mul24 == p[0].mul24 &&
+          fast_choice(p[i].g, p[i].batch, ctx->gemm_cfg, ctx->num_cu) == 16;
+  if (one) {
+    GemmArgs gs[GEMM_GROUP_MAX];
+    int batch[GEMM_GROUP_MAX];
+    for (int i = 0; i < count; ++i) gs[i] = p[i].g, batch[i] = p[i].batch;
+    one = p[0].mul24 ? launch_fast_group<256, 128, 2, 3, true>(gs, batch, count, p[0].osz, ctx->stream)
+                     : launch_fast_group<256, 128, 2, 3, false>(gs, batch, count, p[0].osz, ctx->stream);
   }
+  if (!one)
+    for (int i = 0; i < count; ++i) gemm_launch(ctx, p[i]);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }

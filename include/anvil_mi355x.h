@@ -94,6 +94,24 @@ int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C,
                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
                      int flags);
 
+/* The arguments of one anvil_gemm_i8_ex call. */
+typedef struct anvil_gemm_desc {
+  const int8_t* A;
+  const int8_t* Bt;
+  void* C;
+  const int8_t* lut;
+  int64_t strides[9];
+  int32_t batch0, batch1, M, N, K;
+  int32_t mult, shift, out_dtype, flags;
+} anvil_gemm_desc;
+
+/* 1 to 4 independent qmatmul / qlinear ops, each computed exactly as anvil_gemm_i8_ex computes it (the reference
+ * evaluates them one op at a time, anvil/interp/graph.py:62-64 with anvil/semantics.py:95-103; q, k and v of one
+ * attention read one input and nothing of each other). Every member is validated before anything is launched.
+ * Members that all take the same kernel run as one launch (one tail instead of one per product), others one launch
+ * each. No member may write memory that another member reads or writes. */
+int anvil_gemm_i8_group(anvil_ctx* ctx, const anvil_gemm_desc* descs, int count);
+
 /* A qlinear / qmatmul whose int8 result y feeds an add_requant with an int8 residual R, fused in the GEMM's
  * epilogue (reference anvil/semantics.py:95-103, then add_requant :106-115):
  *   y = clamp_i8((acc * mult + 2^(shift-1)) >> shift) [-> lut];  D = clamp_i8((R * ma + y * mb + 2^(shift2-1)) >> shift2)

@@ -101,6 +101,32 @@ class FakeDevice:
         if out is not None:
             self.store(Cp, out_dtype, (b0, b1, M, N), (sc0, sc1, ldc, 1), out)
 
+    def gemm_i8_group(self, calls):
+        """Members run one after another; none may write bytes another member reads or writes."""
+        self.calls.append(("gemm_group", len(calls)))
+        assert 1 <= len(calls) <= 4
+
+        def span(ptr, dtype, dims, strides):
+            p = ptr.ptr if hasattr(ptr, "ptr") else int(ptr)
+            last = sum((d - 1) * s for d, s in zip(dims, strides))
+            return p, p + (last + 1) * SIZE[dtype]
+
+        reads, writes = [], []
+        for A, Bt, Cp, b0, b1, M, N, K, st, _, _, lut, dt, _ in calls:
+            r = [span(A, "i8", (b0, b1, M, K), (st[0], st[1], st[2], 1)),
+                 span(Bt, "i8", (b0, b1, N, K), (st[3], st[4], st[5], 1))]
+            if lut is not None:
+                r.append(span(lut, "i8", (256,), (1,)))
+            reads.append(r)
+            writes.append(span(Cp, dt, (b0, b1, M, N), (st[6], st[7], st[8], 1)))
+        hit = lambda x, y: x[0] < y[1] and y[0] < x[1]                       # noqa: E731
+        for i, w in enumerate(writes):
+            for j in range(len(calls)):
+                if j != i:
+                    assert not hit(w, writes[j]) and not any(hit(w, r) for r in reads[j]), (i, j)
+        for c in calls:
+            self.gemm_i8(*c)
+
     def gemm_i8_add(self, A, Bt, Cp, b0, b1, M, N, K, strides, mult, shift, lut, R, ma, mb, shift2, D, rstrides,
                     flags):
         """y = qmatmul epilogue, D = add_requant of the residual R (times ma) and y (times mb)."""

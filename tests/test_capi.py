@@ -113,3 +113,39 @@ def test_rmsnorm_flag_validation_precedes_the_device():
         rms(rt.RMS_S24)
     with pytest.raises(ValueError, match="null context"):
         rms(rt.OP_UNCHECKED | rt.RMS_S24)
+
+
+def test_gemm_desc_layout_matches_the_header(tmp_path):
+    """The ctypes mirror of anvil_gemm_desc has the C struct's size and field offsets (checked with gcc)."""
+    import subprocess
+    fields = [f for f, _ in rt.GemmDesc._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "anvil_mi355x.h"\nint main(void) {\n'
+                   '  printf("%zu", sizeof(anvil_gemm_desc));\n' +
+                   "".join(f'  printf(" %zu", offsetof(anvil_gemm_desc, {f}));\n' for f in fields) + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == [C.sizeof(rt.GemmDesc)] + [getattr(rt.GemmDesc, f).offset for f in fields]
+
+
+def test_gemm_group_validates_every_member_first():
+    lib = rt.library()
+    p = 4096
+    good = rt.GemmDesc(A=p, Bt=p, C=p, lut=None, batch0=1, batch1=1, M=16, N=16, K=16, mult=1, shift=3,
+                       out_dtype=rt.I8, flags=0)
+    good.strides[:] = [0, 0, 16, 0, 0, 16, 0, 0, 16]
+    bad = rt.GemmDesc.from_buffer_copy(good)
+    bad.shift = 32
+    grp = lambda *ds, n=None: lib.call("anvil_gemm_i8_group", None, (rt.GemmDesc * len(ds))(*ds),  # noqa: E731
+                                        len(ds) if n is None else n)
+    with pytest.raises(ValueError, match="null pointer"):
+        lib.call("anvil_gemm_i8_group", None, None, 1)
+    with pytest.raises(ValueError, match="count 0"):
+        grp(good, n=0)
+    with pytest.raises(ValueError, match="count 5"):
+        grp(good, good, good, good, good)
+    with pytest.raises(ValueError, match="shift 32"):                # the last member fails before any launch
+        grp(good, good, bad)
+    with pytest.raises(ValueError, match="null context"):
+        grp(good, good)

@@ -35,6 +35,7 @@ def test_planner_matches_oracle_on_config1(fake, cfg1):
             assert np.array_equal(res.ints[k], v), k
     kinds = [c[0] for c in fake.calls]
     assert kinds.count("copy") == 0                                  # no layout op is materialised
+    assert ("gemm_group", 3) in fake.calls                           # q, k and v: one group call
     # both residual adds run in the epilogues of the y and proj GEMMs; keep="all" still stores y and proj
     assert kinds.count("gemm") == 6 and kinds.count("gemm_add") == 2 and kinds.count("add") == 0
     assert all(c[8] for c in fake.calls if c[0] == "gemm_add")
@@ -72,6 +73,20 @@ def test_unproven_keep_outputs_plan_skips_masked_score_tiles(fake, cfg1):
     assert scores[7] & 2                                              # causal tile skip when scores are not kept
     b = cm.run(x, "mi355x", batch=True, keep="all").ints["out"]
     assert np.array_equal(a, b)
+
+
+def test_gemm_grouping_is_a_plan_choice(fake, cfg1):
+    """Grouped and separate launches give the same results; without grouping every product is its own call."""
+    x = models.eval_inputs(cfg1.spec, 2, 7)
+    cm = anvil_mi355x.compile(cfg1)
+    a = cm.run(x, "mi355x", batch=True, keep="all").ints
+    assert [lb for lb, _, _ in cm.plan(2, "all").steps][:2] == ["h1", "q+k+v"]
+    n = len(fake.calls)
+    cm2 = anvil_mi355x.compile(cfg1)
+    cm2.group_gemms = False
+    b = cm2.run(x, "mi355x", batch=True, keep="all").ints
+    assert not [c for c in fake.calls[n:] if c[0] == "gemm_group"]
+    assert a.keys() == b.keys() and all(np.array_equal(a[k], b[k]) for k in a)
 
 
 @pytest.mark.parametrize("seed", range(12))

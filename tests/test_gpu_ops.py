@@ -385,6 +385,55 @@ def _check_sampled_gemm(dev, M, N, K, dtype, lut, add, seed):
         assert np.array_equal(d.download((M, N), np.int8)[rows].astype(np.int64), want)
 
 
+# members (M, N, K, batch, A shared by the batch entries, LUT): q / k / v of the block (v computed transposed, per
+# sequence, with the weight as the shared left operand), ragged rows and columns, tile counts that are not multiples
+# of 8 (padding workgroups between members), and a group whose members take different kernels (one launch each)
+GROUP_CASES = {
+    "qkv": [(24576, 768, 768, 1, False, False), (24576, 768, 768, 1, False, True), (768, 1024, 768, 24, True, False)],
+    "ragged": [(24576 + 300, 768, 768, 1, False, False), (768, 1000, 768, 24, True, True),
+               (20000 + 37, 840 + 5, 512 + 16, 1, False, False), (4096, 640, 256, 7, False, False)],
+    "mixed": [(24576, 768, 768, 1, False, False), (300, 200, 64, 1, False, True), (16384, 3072, 768, 1, False, False)],
+}
+
+
+@pytest.mark.parametrize("dtype", ["i8", "i16"])
+@pytest.mark.parametrize("case", sorted(GROUP_CASES))
+def test_gemm_group_matches_separate_launches(dev, case, dtype):
+    """anvil_gemm_i8_group: every member's result equals anvil_gemm_i8_ex's for the same arguments (the whole
+    result, device against device), and the oracle's on sampled rows of each batch entry."""
+    members = GROUP_CASES[case]
+    if dtype == "i16":
+        members = [mb[:5] + (False,) for mb in members]
+    rng = np.random.default_rng([47, len(case), dtype == "i8"])
+    s, flags = 20, rt.GEMM_UNCHECKED | rt.GEMM_MUL24
+    calls, sep, checks = [], [], []
+    for M, N, K, nb, shared, lut in members:
+        a = rng.integers(-128, 128, (1 if shared else nb, M, K), dtype=np.int8)
+        bt = rng.integers(-128, 128, (nb, N, K), dtype=np.int8)
+        L = rng.integers(-128, 128, 256) if lut else None
+        rows = np.unique(np.concatenate([np.arange(min(M, 64)), np.arange(max(M - 64, 0), M), rng.integers(0, M, 64)]))
+        accs = [sem.matmul_i8(a[0 if shared else b][rows].astype(np.int64), bt[b].T.astype(np.int64), fast=True)
+                for b in range(nb)]
+        m = int(min(((1 << 31) - 1 - (1 << (s - 1))) // int(2 * max(np.abs(x).max() for x in accs)), (1 << 23) - 1))
+        st = [0, 0 if shared else M * K, K, 0, N * K, K, 0, M * N, N]
+        A, Bt = up(dev, a, "i8"), up(dev, bt, "i8")
+        Ld = None if L is None else up(dev, L, "i8")
+        c1, c2 = dev.alloc(nb * M * N * rt.ITEMSIZE[dtype]), dev.alloc(nb * M * N * rt.ITEMSIZE[dtype])
+        calls.append((A, Bt, c1, 1, nb, M, N, K, st, m, s, Ld, dtype, flags))
+        sep.append((A, Bt, c2, 1, nb, M, N, K, st, m, s, Ld, dtype, flags))
+        want = [sem.requant_dtype(x, m, s, dtype) for x in accs]
+        checks.append((c1, c2, (nb, M, N), rows, [w if L is None else sem.lut_i8(w, L) for w in want], (A, Bt, Ld)))
+    dev.gemm_i8_group(calls)
+    for c in sep:
+        dev.gemm_i8(*c)
+    dev.sync()
+    for i, (c1, c2, shape, rows, want, _) in enumerate(checks):
+        got = c1.download(shape, rt.NP_DTYPE[dtype])
+        assert np.array_equal(got, c2.download(shape, rt.NP_DTYPE[dtype])), (case, i)
+        for b, w in enumerate(want):
+            assert np.array_equal(got[b][rows].astype(np.int64), w), (case, i, b)
+
+
 @pytest.mark.parametrize("dtype", ["i8", "i16"])
 def test_embed_quantize(dev, dtype):
     """anvil_embed_quantize: clamp(rint((wte[id] + wpe[t]) / scale)) in float64, as the host computes it."""
