@@ -40,6 +40,32 @@ __device__ __forceinline__ int sbyte(const v4i& v, int b) {   // signed byte b (
   return (int)(int8_t)((unsigned)v[b >> 2] >> (8 * (b & 3)));
 }
 
+// signed byte B of x times w (|w| < 2^23) in one SDWA multiply, and a * b + c on 24-bit signed a, b: written out
+// because the compiler's own lowering of these adds a shift (and a full-width multiply) per element
+template <int B>
+__device__ __forceinline__ int mul_sbyte(unsigned x, int w) {
+  int d;
+  if constexpr (B == 0)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+        : "=v"(d) : "v"(x), "v"(w));
+  else if constexpr (B == 1)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:DWORD"
+        : "=v"(d) : "v"(x), "v"(w));
+  else if constexpr (B == 2)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:DWORD"
+        : "=v"(d) : "v"(x), "v"(w));
+  else
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:DWORD"
+        : "=v"(d) : "v"(x), "v"(w));
+  return d;
+}
+
+__device__ __forceinline__ int mad_i24(int a, int b, int c) {
+  int d;
+  asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(b), "v"(c));
+  return d;
+}
+
 // ------------------------------------------------------------------------------------- fast softmax_lut
 // For proven graphs (every intermediate fits int32, lut >= 0 and lut[255] >= 1, so S >= 1) with rows of a multiple
 // of 16 bytes: one wavefront per row, the row in registers as 16-byte chunks (lane l holds chunks l, l + 64, ...;
@@ -148,7 +174,8 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
   const bool active = lane < (cols >> 4);
   v4i wv = {0, 0, 0, 0};
   if (active) wv = *reinterpret_cast<const v4i*>(w + 16 * lane);
-  int wb[16];                                                   // this lane's 16 weights, sign-extended once
+  // this lane's 16 weights, sign-extended once
+  int wb[16];
 #pragma unroll
   for (int b = 0; b < 16; ++b) wb[b] = sbyte(wv, b);
   unsigned off[RMS_ROWS];                                       // row j, this lane's chunk; OOB for idle lanes
@@ -189,17 +216,23 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
     for (int j = 0; j < RMS_ROWS; ++j) {
       const int s = sh[j];
       const int rnd = s ? (1 << (s - 1)) : 0;
-      const int lo = s >= 24 ? INT32_MIN : -128 * (1 << s), hi = s >= 24 ? INT32_MAX : 128 * (1 << s) - 1;
+      int lo = s >= 24 ? INT32_MIN : -128 * (1 << s), hi = s >= 24 ? INT32_MAX : 128 * (1 << s) - 1;
+      asm("" : "+s"(lo), "+s"(hi));   // one med3 per element (a visible select becomes a v_cndmask per element)
       const int rm = S24 ? r[j] * mult : 0;
       v4i o;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         int y[4];
+        // proven: x w r and x w r M + rnd fit int32 (S24: |x w| and |r M| below 2^23)
+        if (S24) {
+          const unsigned xd = (unsigned)xv[j][q];
+          y[0] = med3i(mad_i24(mul_sbyte<0>(xd, wb[4 * q]), rm, rnd), lo, hi);
+          y[1] = med3i(mad_i24(mul_sbyte<1>(xd, wb[4 * q + 1]), rm, rnd), lo, hi);
+          y[2] = med3i(mad_i24(mul_sbyte<2>(xd, wb[4 * q + 2]), rm, rnd), lo, hi);
+          y[3] = med3i(mad_i24(mul_sbyte<3>(xd, wb[4 * q + 3]), rm, rnd), lo, hi);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int xw = sbyte(xv[j], 4 * q + e) * wb[4 * q + e];
-          // proven: x w r and x w r M + rnd fit int32
-          y[e] = med3i(S24 ? __mul24(xw, rm) + rnd : xw * r[j] * mult + rnd, lo, hi);
+          for (int e = 0; e < 4; ++e) y[e] = med3i(sbyte(xv[j], 4 * q + e) * wb[4 * q + e] * r[j] * mult + rnd, lo, hi);
         }
         o[q] = (int)sra_pack4(y[0], y[1], y[2], y[3], s);
       }

@@ -34,8 +34,8 @@ METRIC = "int8 block tokens/sec at 1 MI355X; GEMM int8 TOPS as % of MFMA peak"
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=5, choices=[1, 3, 4, 5])
     ap.add_argument("--keep", default="outputs", choices=["outputs", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -150,6 +150,7 @@ def main():
     if cpu is not None:
         got = cm.read(plan, cm.outputs)
         cpu["matches_gpu_output"] = all(np.array_equal(got[s][i:i + 1], o[s]) for i, o in cpu_out.items() for s in o)
+    e2e = end_to_end(cm, x, nb, spec.seq)
     stream = stream_copy(dev)
 
     line = {
@@ -168,6 +169,7 @@ def main():
                            "attention kernel's time, softmax included, counts as GEMM time"},
         "roofline": roof,
         "hbm_stream": stream,
+        "end_to_end": e2e,
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
@@ -250,6 +252,20 @@ def cpu_baseline(built, xq, outs):
                      f"affinity={affinity}",
            "one_core_tokens_s": round(one, 2), "seconds": round(wall, 2)}
     return rec, {i: o for i, _, o in res}
+
+
+def end_to_end(cm, x, nb, seq, calls=3):
+    """The PCIe-inclusive rate, never `value`: cm.run on the host float input (upload, quantize on the device, the
+    forward, download of the int8 output and its float64 dequantization on the host), one untimed call then `calls`
+    timed ones."""
+    cm.run(x, batch=True)
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        cm.run(x, batch=True)
+    dt = (time.perf_counter() - t0) / calls
+    return {"tokens_s": round(nb * seq / dt, 1), "ms_per_call": round(dt * 1e3, 2), "calls": calls,
+            "input_bytes": int(x.nbytes), "covers": "cm.run(x, batch=True): float input upload, device quantize, "
+                                                    "forward, output download and host dequantize"}
 
 
 def stream_copy(dev):
