@@ -256,6 +256,123 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
   }
 }
 
+// rmsnorm_int over rows of 256·CH bytes (the S24 form of rmsnorm_fast, every lane busy): a wave holds four rows,
+// 16 lanes a row, and lane sub of row rr reads and writes chunks c·16 + sub (16 bytes each, c < CH), so each load or
+// store instruction covers 256 contiguous bytes of every row. The row sums are reduced within each 16-lane DPP row,
+// read out as four scalars, and the per-row values (requant multiplier, shift, clamp bounds) return to the lanes by
+// selection on the lane's row.
+__device__ __forceinline__ int dpp_sum16(int v) {            // sum over the lane's 16-lane row, in every lane
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false);  // row_ror:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  return v;
+}
+
+__device__ __forceinline__ unsigned sra_pack4v(int x0, int x1, int x2, int x3, int sh) {   // shift per lane
+  unsigned d;
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+      : "=v"(d) : "v"(sh), "v"(x0));
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(d) : "v"(sh), "v"(x1));
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(d) : "v"(sh), "v"(x2));
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+      : "+v"(d) : "v"(sh), "v"(x3));
+  return d;
+}
+
+__device__ __forceinline__ int mad_i24v(int a, int b, int c) {
+  int d;
+  asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
+template <int CH>
+__global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
+                                                             const int* __restrict__ lut, int lut_len, int mult,
+                                                             int shift, long long rows, int8_t* __restrict__ out) {
+  constexpr int COLS = 256 * CH;
+  const int lane = threadIdx.x & 63, rr = lane >> 4, sub = lane & 15;
+  int wb[CH][16];                                               // this lane's weights, sign-extended once
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const v4i wv = *reinterpret_cast<const v4i*>(w + 16 * (16 * c + sub));
+#pragma unroll
+    for (int b = 0; b < 16; ++b) wb[c][b] = sbyte(wv, b);
+  }
+  unsigned off[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) off[c] = (unsigned)(rr * COLS + 16 * (16 * c + sub));
+  const long long step = (long long)gridDim.x * R_WAVES * 4;
+  auto group = [&](const int8_t* base, long long r0) {        // a raw buffer over rows r0 .. r0 + 3
+    const long long n = r0 < rows ? std::min<long long>(4, rows - r0) : 0;
+    return uniform_rsrc(base + (r0 < rows ? r0 : 0) * COLS, (int)(n * COLS));
+  };
+  auto load = [&](long long r0, v4i* xv) {
+    const __amdgpu_buffer_rsrc_t rs = group(x, r0);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) xv[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, off[c], 0, 0));
+  };
+  auto pick = [&](const int* v) {                               // v[rr] of four wave-uniform values
+    return rr == 0 ? v[0] : (rr == 1 ? v[1] : (rr == 2 ? v[2] : v[3]));
+  };
+  auto process = [&](const v4i* xv, long long r0) {
+    int ss = 0;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[c][q], xv[c][q], ss, false);
+    ss = dpp_sum16(ss);
+    int rm_s[4], sh_s[4], rnd_s[4], lo_s[4], hi_s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int t = __builtin_amdgcn_readlane(ss, 16 * j);
+      int k = 0;
+      while (t >= lut_len) {
+        t >>= 2;
+        ++k;
+      }
+      const int sh = shift + k;
+      rm_s[j] = lut[t] * mult;                                  // proven below 2^23 in magnitude
+      sh_s[j] = sh;
+      rnd_s[j] = sh ? 1 << (sh - 1) : 0;
+      lo_s[j] = sh >= 24 ? INT32_MIN : -128 * (1 << sh);
+      hi_s[j] = sh >= 24 ? INT32_MAX : 128 * (1 << sh) - 1;
+    }
+    const int rm = pick(rm_s), sh = pick(sh_s), rnd = pick(rnd_s), lo = pick(lo_s), hi = pick(hi_s);
+    const __amdgpu_buffer_rsrc_t ws = group(out, r0);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      v4i o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const unsigned xd = (unsigned)xv[c][q];
+        // proven: x w r and x w r M + rnd fit int32, |x w| and |r M| below 2^23
+        const int y0 = med3i(mad_i24v(mul_sbyte<0>(xd, wb[c][4 * q]), rm, rnd), lo, hi);
+        const int y1 = med3i(mad_i24v(mul_sbyte<1>(xd, wb[c][4 * q + 1]), rm, rnd), lo, hi);
+        const int y2 = med3i(mad_i24v(mul_sbyte<2>(xd, wb[c][4 * q + 2]), rm, rnd), lo, hi);
+        const int y3 = med3i(mad_i24v(mul_sbyte<3>(xd, wb[c][4 * q + 3]), rm, rnd), lo, hi);
+        o[q] = (int)sra_pack4v(y0, y1, y2, y3, sh);
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o), ws,
+                                             off[c], 0, 0);
+    }
+  };
+  long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * 4;
+  v4i xa[CH], xb[CH];
+  load(row0, xa);
+  while (row0 < rows) {
+    load(row0 + step, xb);
+    process(xa, row0);
+    row0 += step;
+    if (row0 >= rows) break;
+    load(row0 + step, xa);
+    process(xb, row0);
+    row0 += step;
+  }
+}
+
 static unsigned row_grid(long long rows, int device_cus) {
   long long blocks = (rows + R_WAVES - 1) / R_WAVES;
   const long long cap = (long long)device_cus * 16;            // enough resident waves to cover HBM latency
@@ -389,7 +506,17 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
     // the next group's loads in flight
     const long long groups = (rows + RMS_ROWS - 1) / RMS_ROWS;
     const dim3 grid((unsigned)std::min<long long>((groups + R_WAVES - 1) / R_WAVES, 8ll * ctx->num_cu));
-    if (flags & ANVIL_RMS_S24)
+    const int ch = cols / 256;
+    if ((flags & ANVIL_RMS_S24) && cols % 256 == 0 && ch <= 4) {      // rows of 256, 512, 768 or 1024 bytes
+      auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len, mult,
+                           shift, (long long)rows, out);
+      };
+      if (ch == 1) launch(rmsnorm_rows16<1>);
+      else if (ch == 2) launch(rmsnorm_rows16<2>);
+      else if (ch == 3) launch(rmsnorm_rows16<3>);
+      else launch(rmsnorm_rows16<4>);
+    } else if (flags & ANVIL_RMS_S24)
       hipLaunchKernelGGL(rmsnorm_fast<true>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
                          mult, shift, (long long)rows, cols, out);
     else
