@@ -308,16 +308,21 @@ def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
         assert np.array_equal(got, want), (seed, kind, np.argwhere(got != want)[:5])
 
 
+# add_requant multipliers: a negative one, config 5's two adds (Ma above 2^23, 128 (Ma + Mb) close to 2^31), and
+# Ma = Mb = 1 with no shift
+ADD_MULTS = [(300, -200, 9), (11157253, 4299753, 24), (7873258, 3110671, 23), (1, 1, 0)]
+
+
 @pytest.mark.parametrize("M,K,N", [(256, 768, 768), (300, 64, 200), (33, 48, 72), (1024, 256, 384)])
 @pytest.mark.parametrize("store_y", [True, False])
-def test_gemm_with_fused_residual_add(dev, M, K, N, store_y):
+@pytest.mark.parametrize("ma,mb,s2", ADD_MULTS)
+def test_gemm_with_fused_residual_add(dev, M, K, N, store_y, ma, mb, s2):
     """anvil_gemm_i8_add: y = qlinear(a, w) [LUT] and D = add_requant(r, y) in one launch, bit-exact with the two ops;
     N not a multiple of 16 takes the per-byte epilogue."""
     rng = np.random.default_rng([31, M, K, N, int(store_y)])
     a, w, r = rng.integers(-128, 128, (M, K)), rng.integers(-128, 128, (K, N)), rng.integers(-128, 128, (M, N))
     m, s = 3, 16
     lut = rng.integers(-128, 128, 256) if N == 200 else None
-    ma, mb, s2 = 300, -200, 9
     y = sem.qmatmul(a, w, m, s, lut)
     want = sem.add_requant(r, y, ma, mb, s2)
     c = dev.alloc(M * N) if store_y else None
@@ -356,7 +361,15 @@ def test_gemm_long_k_narrow_n(dev, M, N, K, dtype, lut, add):
     _check_sampled_gemm(dev, M, N, K, dtype, lut, add, 43)
 
 
-def _check_sampled_gemm(dev, M, N, K, dtype, lut, add, seed):
+@pytest.mark.parametrize("M,N,K", [(32768, 768, 768), (32768 + 37, 768, 3072), (32768, 3072, 768)])
+@pytest.mark.parametrize("ma,mb,s2", ADD_MULTS[1:3])
+def test_gemm_fused_add_block_multipliers(dev, M, N, K, ma, mb, s2):
+    """The block's add multipliers on the kernels that take the block's shapes: 256 x 128 tiles (y), the persistent
+    kernel with 128-byte K blocks (proj, ragged rows) and the 256 x 256 persistent kernel."""
+    _check_sampled_gemm(dev, M, N, K, "i8", False, True, 45, (ma, mb, s2))
+
+
+def _check_sampled_gemm(dev, M, N, K, dtype, lut, add, seed, mults=(300, -200, 9)):
     rng = np.random.default_rng([seed, M, N, K])
     a, w = rng.integers(-128, 128, (M, K), dtype=np.int8), rng.integers(-128, 128, (K, N), dtype=np.int8)
     rows = np.unique(np.concatenate([np.arange(256), np.arange(M - 256, M), rng.integers(0, M, 512)]))
@@ -372,8 +385,8 @@ def _check_sampled_gemm(dev, M, N, K, dtype, lut, add, seed):
     if add:
         r = rng.integers(-128, 128, (M, N), dtype=np.int8)
         d = dev.alloc(M * N)
-        dev.gemm_i8_add(up(dev, a, "i8"), up(dev, wt, "i8"), c, 1, 1, M, N, K, st, m, s, None, up(dev, r, "i8"), 300,
-                        -200, 9, d, [0, 0, N, 0, 0, N], flags)
+        dev.gemm_i8_add(up(dev, a, "i8"), up(dev, wt, "i8"), c, 1, 1, M, N, K, st, m, s, None, up(dev, r, "i8"),
+                        *mults, d, [0, 0, N, 0, 0, N], flags)
     else:
         dev.gemm_i8(up(dev, a, "i8"), up(dev, wt, "i8"), c, 1, 1, M, N, K, st, m, s,
                     None if L is None else up(dev, L, "i8"), dtype, flags)
@@ -381,7 +394,7 @@ def _check_sampled_gemm(dev, M, N, K, dtype, lut, add, seed):
     got = c.download((M, N), rt.NP_DTYPE[dtype])[rows].astype(np.int64)
     assert np.array_equal(got, y), np.argwhere(got != y)[:5]
     if add:
-        want = sem.add_requant(r[rows].astype(np.int64), y, 300, -200, 9)
+        want = sem.add_requant(r[rows].astype(np.int64), y, *mults)
         assert np.array_equal(d.download((M, N), np.int8)[rows].astype(np.int64), want)
 
 
