@@ -583,9 +583,37 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
     if (kt + 2 < nk) step(kt + 2, L2, L1, L3);
   }
 
+  // the staged tile leaves in 16-byte chunks, chunk idx = t + pass * G_THREADS of the tile: row idx / CH_ROW,
+  // column chunk idx % CH_ROW (a thread keeps one column chunk when CH_ROW divides the thread count)
+  constexpr int CH_ROW = BN * OSZ / 16;
+  static_assert((BM * CH_ROW) % G_THREADS == 0, "whole store passes");
+  constexpr int PASSES = BM * CH_ROW / G_THREADS;
+  auto rr_of = [&](int pass) { return (t + pass * G_THREADS) / CH_ROW; };
+  auto cf_of = [&](int pass) { return (t + pass * G_THREADS) % CH_ROW * 16 / OSZ; };   // first column
+  const int cols_valid = min(BN, g.N - n0);
+  const bool res = OSZ == 1 && g.res;
+  // interior tile: every chunk is read from LDS (and the residual from memory) before the first store, so the
+  // reads' latencies overlap instead of serialising pass by pass
+  const bool full = m0 + BM <= g.M && cols_valid == BN && (res ? g.vec_res != 0 : g.vec_store != 0) &&
+                    (!res || !g.store_y || g.vec_store) && (!res || (long long)BM * g.ldr < (1ll << 31));
+  // An interior tile's residual chunks are loaded now, so their latency overlaps the staging below. With an i8
+  // result the loads are issued whatever the tile (out of range, so loading nothing, without a residual): they are
+  // then the newest NR loads, and waiting for all but those retires the pipeline's last (zero-filling) stage loads
+  // before the staging overwrites their arrays. With no add possible (i16) there are none and the wait is for all.
+  constexpr int NR = OSZ == 1 ? PASSES : 0;
+  const bool res_full = res && full;
+  const int8_t* Rb = g.R + b0 * g.sr0 + b1 * g.sr1 + (long long)m0 * g.ldr + n0;
+  const __amdgpu_buffer_rsrc_t rres = uniform_rsrc(res_full ? Rb : g.A, res_full ? (int)(BM * g.ldr) : 0);
+  v4i rv[NR > 0 ? NR : 1];
+#pragma unroll
+  for (int pass = 0; pass < NR; ++pass)
+    rv[pass] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rres, res_full ? (unsigned)(rr_of(pass) * g.ldr + cf_of(pass)) : OOB, 0, 0));
+
   // epilogue: requant (+ LUT) into the staging tile spread over the stage arrays (RPA rows each), then 16-byte
   // stores
-  __syncthreads();
+  wait_vm_lgkm0<NR>();
+  stage_barrier();
   const int lo = OSZ == 1 ? -128 : -32768, hi = OSZ == 1 ? 127 : 32767;
   auto srow = [&](int r) -> int8_t* {
     if (r < RPA) return L0 + r * SROW;
@@ -631,33 +659,17 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
     stage(std::true_type{});
   else
     stage(std::false_type{});
-  __syncthreads();
+  wait_vm_lgkm0<63>();                                   // the staging writes, not the residual loads
+  stage_barrier();
 
-  // the staged tile leaves in 16-byte chunks, chunk idx = t + pass * G_THREADS of the tile: row idx / CH_ROW,
-  // column chunk idx % CH_ROW (a thread keeps one column chunk when CH_ROW divides the thread count)
-  constexpr int CH_ROW = BN * OSZ / 16;
-  static_assert((BM * CH_ROW) % G_THREADS == 0, "whole store passes");
-  constexpr int PASSES = BM * CH_ROW / G_THREADS;
-  auto rr_of = [&](int pass) { return (t + pass * G_THREADS) / CH_ROW; };
-  auto cf_of = [&](int pass) { return (t + pass * G_THREADS) % CH_ROW * 16 / OSZ; };   // first column
   char* Cb = reinterpret_cast<char*>(g.C) + (b0 * g.sc0 + b1 * g.sc1) * OSZ;
-  const int cols_valid = min(BN, g.N - n0);
-  // interior tile: every chunk is read from LDS (and the residual from memory) before the first store, so the
-  // reads' latencies overlap instead of serialising pass by pass
-  const bool full = m0 + BM <= g.M && cols_valid == BN && (OSZ == 1 && g.res ? g.vec_res != 0 : g.vec_store != 0) &&
-                    (!(OSZ == 1 && g.res) || !g.store_y || g.vec_store);
   if (full) {
     v4i ch[PASSES];
 #pragma unroll
     for (int pass = 0; pass < PASSES; ++pass)
       ch[pass] = *reinterpret_cast<const v4i*>(srow(rr_of(pass)) + cf_of(pass) * OSZ);
-    if (OSZ == 1 && g.res) {
-      const int8_t* Rb = g.R + b0 * g.sr0 + b1 * g.sr1 + (long long)m0 * g.ldr + n0;
+    if (res) {
       int8_t* Db = g.D + b0 * g.sd0 + b1 * g.sd1 + (long long)m0 * g.ldd + n0;
-      v4i rv[PASSES];
-#pragma unroll
-      for (int pass = 0; pass < PASSES; ++pass)
-        rv[pass] = *reinterpret_cast<const v4i*>(Rb + (long long)rr_of(pass) * g.ldr + cf_of(pass));
       const int ma = g.ma, mb = g.mb, rnd2 = g.rnd2, sh2 = g.shift2;
 #pragma unroll
       for (int pass = 0; pass < PASSES; ++pass) {
