@@ -142,6 +142,20 @@ def test_rmsnorm_fast_walks_many_row_groups(dev, flags, d):
     assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s, flags=flags), want)
 
 
+@pytest.mark.parametrize("d", [64, 768])
+def test_rmsnorm_shift_reaching_int32_bounds(dev, d):
+    """Requant shifts s + k from 20 up to 27: at 24 and above the pre-shift clamp bounds saturate to the int32 limits
+    (rows with a large sum of squares take k up to 7 with a 1024-entry LUT)."""
+    rng = np.random.default_rng([62, d])
+    w = rng.integers(-127, 128, d)
+    lut = rng.integers(1, 1 << 14, 1024)
+    x = np.concatenate([rng.integers(-128, 128, (61, d)), rng.integers(-3, 4, (60, d)), np.full((2, d), -128)])
+    want = sem.rmsnorm_int(x, w, lut, 1, 20)
+    got = _rms(dev, x, "i8", w, lut, 1, 20, flags=rt.OP_UNCHECKED | rt.RMS_S24)
+    assert np.array_equal(got, want)
+    assert np.abs(want).max() > 0
+
+
 def test_rmsnorm_i16_wide(dev):
     d = 32
     rng = np.random.default_rng(8)
