@@ -74,7 +74,9 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   static_assert(4 * 32 * OROW * 4 >= 32 * 256, "the per-row p tables fit in the partial-O space");
   __shared__ __attribute__((aligned(16))) int lut_s[256];
   __shared__ double lutd_s[256];                            // the LUT as doubles, for the p tables
-  __shared__ int red_m[4][32], red_s[4][32];
+  __shared__ __attribute__((aligned(16))) int red_m[4][32];   // after the max: the rows' (A, B) as doubles
+  __shared__ int red_s[4][32];
+  __shared__ int dlow_s[32];
   __shared__ __attribute__((aligned(256))) int opart[4][32 * OROW];   // 256: the p-table rows
 
   const int t = threadIdx.x;
@@ -211,26 +213,39 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   S += __shfl_xor(S, 32, 64);
   if (half == 0) red_s[w][l32] = S;
   const bool mono = __syncthreads_and(t == 255 || lut_s[t] <= lut_s[t + 1]) != 0;   // lut_s is visible here
-  S = red_s[0][l32] + red_s[1][l32] + red_s[2][l32] + red_s[3][l32];
 
   // ---- 3. probabilities, O_w = P V over this wave's tiles
   // p depends on the row and the score only, so each row gets a byte table of (lut[d] one + S // 2) // S over the
   // scores s, d = s - max + 255, built in the partial-O space (free until this phase ends). With a non-decreasing table the
   // quotient is 0 below the first d where lut[d] one + S // 2 >= S, and only the entries from there up are divided;
   // otherwise every entry is.
-  const double Sd = (double)S;                           // S >= lut[255] >= 1: the row maximum maps to d = 255
-  const double qa = (double)a.one / Sd;
-  const double qb = (double)(S >> 1) / Sd + 0x1p-40 - 0.5;   // the - 0.5 is exact (Sterbenz, or S = 1)
-  int d0 = 0;
-  if (mono) {
-    // lut[d] one + S // 2 >= S  <=>  lut[d] >= e0 = ceil((S - S // 2) / one); d0 = #{d : lut[d] < e0}, by binary
-    // search over the non-decreasing table (256 when even lut[255] is below e0)
-    const int e0 = (S - (S >> 1) + a.one - 1) / a.one;
-    int pos = 0;
+  // The per-row constants (two float64 divisions, an integer division, a binary search) are the same for the four
+  // waves of a row, so wave 0 alone forms them (lanes l and l + 32 both hold row l % 32) and passes them on in LDS:
+  // the other waves' instructions go to the other workgroups on the CU.
+  double* qab = reinterpret_cast<double*>(&red_m[0][0]);  // [0, 32): A, [32, 64): B; red_m is read before the last barrier
+  if (w == 0) {
+    S = red_s[0][l32] + red_s[1][l32] + red_s[2][l32] + red_s[3][l32];
+    const double Sd = (double)S;                         // S >= lut[255] >= 1: the row maximum maps to d = 255
+    const double qa0 = (double)a.one / Sd;
+    const double qb0 = (double)(S >> 1) / Sd + 0x1p-40 - 0.5;   // the - 0.5 is exact (Sterbenz, or S = 1)
+    int d0 = 0;
+    if (mono) {
+      // lut[d] one + S // 2 >= S  <=>  lut[d] >= e0 = ceil((S - S // 2) / one); d0 = #{d : lut[d] < e0}, by binary
+      // search over the non-decreasing table (256 when even lut[255] is below e0)
+      const int e0 = (S - (S >> 1) + a.one - 1) / a.one;
+      int pos = 0;
 #pragma unroll
-    for (int step = 128; step >= 1; step >>= 1) pos += lut_s[pos + step - 1] < e0 ? step : 0;
-    d0 = lut_s[255] < e0 ? 256 : pos;
+      for (int step = 128; step >= 1; step >>= 1) pos += lut_s[pos + step - 1] < e0 ? step : 0;
+      d0 = lut_s[255] < e0 ? 256 : pos;
+    }
+    if (half == 0) {
+      qab[l32] = qa0;
+      qab[32 + l32] = qb0;
+      dlow_s[l32] = max(d0, 127 - mx);                    // d below 127 - max needs s < -128
+    }
   }
+  __syncthreads();
+  const double qa = qab[l32], qb = qab[32 + l32];
   // The tables sit in the partial-O space, 256 bytes a row: the entry of score s in row r is at column
   // (s & 255) ^ 4 r, so a lookup address is the row base with its low byte replaced by the swizzled score byte
   // (one v_perm), and the 32 rows' entries for one s fall in 32 different banks.
@@ -244,7 +259,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   {
     const int part = 2 * w + half;                       // this lane's eighth of its row's table
     int8_t* trow = ptab + l32 * PT;
-    const int dlow = max(d0, 127 - mx);                  // d below 127 - max needs s < -128
+    const int dlow = dlow_s[l32];
     for (int d = 255 - part; d >= dlow; d -= 32) {      // four independent entries per pass, reads issued together
       int du[4];
       double lv[4];
