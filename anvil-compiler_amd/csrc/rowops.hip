@@ -60,6 +60,25 @@ __device__ __forceinline__ int mul_sbyte(unsigned x, int w) {
   return d;
 }
 
+// signed byte B of x times signed byte B of w, both selected and sign-extended by the SDWA operands
+template <int B>
+__device__ __forceinline__ int mul_sbytes(unsigned x, unsigned w) {
+  int d;
+  if constexpr (B == 0)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:BYTE_0"
+        : "=v"(d) : "v"(x), "v"(w));
+  else if constexpr (B == 1)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:BYTE_1"
+        : "=v"(d) : "v"(x), "v"(w));
+  else if constexpr (B == 2)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:BYTE_2"
+        : "=v"(d) : "v"(x), "v"(w));
+  else
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:BYTE_3"
+        : "=v"(d) : "v"(x), "v"(w));
+  return d;
+}
+
 __device__ __forceinline__ int mad_i24(int a, int b, int c) {
   int d;
   asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(b), "v"(c));
@@ -294,13 +313,9 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
                                                              int shift, long long rows, int8_t* __restrict__ out) {
   constexpr int COLS = 256 * CH;
   const int lane = threadIdx.x & 63, rr = lane >> 4, sub = lane & 15;
-  int wb[CH][16];                                               // this lane's weights, sign-extended once
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const v4i wv = *reinterpret_cast<const v4i*>(w + 16 * (16 * c + sub));
-#pragma unroll
-    for (int b = 0; b < 16; ++b) wb[c][b] = sbyte(wv, b);
-  }
+  v4i wv[CH];                                                   // this lane's weights, packed (each multiply
+#pragma unroll                                                  // selects and sign-extends its byte)
+  for (int c = 0; c < CH; ++c) wv[c] = *reinterpret_cast<const v4i*>(w + 16 * (16 * c + sub));
   unsigned off[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) off[c] = (unsigned)(rr * COLS + 16 * (16 * c + sub));
@@ -347,12 +362,12 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
       v4i o;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const unsigned xd = (unsigned)xv[c][q];
+        const unsigned xd = (unsigned)xv[c][q], wd = (unsigned)wv[c][q];
         // proven: x w r and x w r M + rnd fit int32, |x w| and |r M| below 2^23
-        const int y0 = med3i(mad_i24v(mul_sbyte<0>(xd, wb[c][4 * q]), rm, rnd), lo, hi);
-        const int y1 = med3i(mad_i24v(mul_sbyte<1>(xd, wb[c][4 * q + 1]), rm, rnd), lo, hi);
-        const int y2 = med3i(mad_i24v(mul_sbyte<2>(xd, wb[c][4 * q + 2]), rm, rnd), lo, hi);
-        const int y3 = med3i(mad_i24v(mul_sbyte<3>(xd, wb[c][4 * q + 3]), rm, rnd), lo, hi);
+        const int y0 = med3i(mad_i24v(mul_sbytes<0>(xd, wd), rm, rnd), lo, hi);
+        const int y1 = med3i(mad_i24v(mul_sbytes<1>(xd, wd), rm, rnd), lo, hi);
+        const int y2 = med3i(mad_i24v(mul_sbytes<2>(xd, wd), rm, rnd), lo, hi);
+        const int y3 = med3i(mad_i24v(mul_sbytes<3>(xd, wd), rm, rnd), lo, hi);
         o[q] = (int)sra_pack4v(y0, y1, y2, y3, sh);
       }
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o), ws,
