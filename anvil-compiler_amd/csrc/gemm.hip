@@ -627,6 +627,9 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
 #pragma unroll
   for (int j = 0; j < TM; ++j) rowp[j] = srow(wm * WM + j * 32 + l32);
   const int mult = g.mult, rnd = g.rnd, shift = g.shift;
+  // i8 without a LUT: the clamp runs before the shift (bounds [-128, 127] << shift, saturated to int32) and one SDWA
+  // shift writes each byte of the packed dword
+  const int clo = (int)max(-128ll << shift, (long long)INT32_MIN), chi = (int)min((128ll << shift) - 1, (long long)INT32_MAX);
   auto stage = [&](auto lut_c) {
     constexpr bool LUT = decltype(lut_c)::value;
 #pragma unroll
@@ -636,6 +639,16 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int n_l = wn * WN + i * 32 + 8 * q + 4 * half;
+          if constexpr (OSZ == 1 && !LUT) {
+            int x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int a = acc[i][j][4 * q + e];
+              x[e] = med3i(MUL24 ? (__mul24(a, mult) + rnd) : (a * mult + rnd), clo, chi);
+            }
+            *reinterpret_cast<unsigned*>(rowp[j] + n_l) = sra_pack4(x[0], x[1], x[2], x[3], shift);
+            continue;
+          }
           int v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
