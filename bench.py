@@ -1,16 +1,17 @@
 #!/usr/bin/env python3
 """Benchmark: int8 block tokens/s on 1 MI355X, and GEMM int8 TOPS as a fraction of the MFMA peak.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config 5] [--keep outputs] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 300] [--warmup 10] [--config 5] [--keep outputs] [--no-cpu-baseline]
 
 Workload (default): config 5, the GPT-2-small-shaped int8 block (n_embd 768, 12 heads, T 1024, batch 32, causal),
 random-init N(0, 0.02) weights, N(0, 1) synthetic activations, per-tensor int8 calibrated on 8 seeded batches.
 A step is one forward of the block over the batch (every graph op on the GPU, graph outputs left in HBM); the
 quantized input is resident in HBM before the timed region. K steps are timed between two device synchronisations
-(host wall clock); the dominant kernel is bracketed by HIP events on the library's stream inside the timed region.
+(host wall clock); the dominant kernel is bracketed by HIP events on the library's stream on every 10th timed step.
 
 Printed: one JSON line with the metric, the dominant kernel's roofline, a per-kernel breakdown from an untimed
-profiled pass, a stream-copy figure for the achievable HBM bandwidth, and the CPU baseline: this repo's literal numpy
+profiled pass, a stream-copy figure for the achievable HBM bandwidth, the PCIe-inclusive rate of `cm.run` on the host
+float input (never `value`), and the CPU baseline: this repo's literal numpy
 restatement of the reference interpreter (oracle/, int64 `@`, single-threaded per process) on P sequences of the
 same batch in P processes on this host's cores (exact, as batched evaluation equals per-sample evaluation), scaled
 to tokens/s. It runs before the GPU is first touched, so the worker processes are forked from a process with no
