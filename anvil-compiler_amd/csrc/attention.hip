@@ -23,7 +23,7 @@
 //      by score. O_w = P V over the wave's tiles on MFMA, P packed in registers: lane l's 16 probabilities of a tile
 //      are keys 16 (l / 32) .. + 15 (the key rows entered the score MFMA in bperm order), so its V^T fragment is one
 //      contiguous 16-byte load.
-//   4. The four partial O tiles (int32) are summed through LDS; o = clamp((O M_o + rnd(s_o)) >> s_o), 4-byte
+//   4. The four partial O tiles (int32) are summed through two LDS slots; o = clamp((O M_o + rnd(s_o)) >> s_o), 4-byte
 //      stores.
 // Every product is proven to fit int32 (prove_no_overflow), so the requants run in 32 bits; with S24 the score
 // requant multiply is one 24-bit multiply-add (|acc|, |M_s| < 2^23).
@@ -67,17 +67,17 @@ __device__ __forceinline__ v4i chunk16(const int8_t* row, int chunk) {
 }
 
 template <int NTW, int D, bool S24>
-__global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
+__global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(AttnArgs a) {
   constexpr int KS = (D + 31) / 32;         // 32-wide MFMA k-steps over the head dim
   constexpr int CT = (D + 31) / 32;         // 32-wide output column tiles
   constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
-  static_assert(4 * 32 * OROW * 4 >= 32 * 256, "the per-row p tables fit in the partial-O space");
+  static_assert(2 * 32 * OROW * 4 >= 32 * 256, "the per-row p tables fit in the partial-O space");
   __shared__ __attribute__((aligned(16))) int lut_s[256];
   __shared__ double lutd_s[256];                            // the LUT as doubles, for the p tables
   __shared__ __attribute__((aligned(16))) int red_m[4][32];   // after the max: the rows' (A, B) as doubles
   __shared__ int red_s[4][32];
   __shared__ int dlow_s[32];
-  __shared__ __attribute__((aligned(256))) int opart[4][32 * OROW];   // 256: the p-table rows
+  __shared__ __attribute__((aligned(256))) int opart[2][32 * OROW];   // 256: the p-table rows
 
   const int t = threadIdx.x;
   const int lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -176,7 +176,6 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   };
   v4i vf[CT], vn[CT];
   vload(w, vf);
-  if (NTW > 1) vload(w + 4, vn);
   mx = max(mx, __shfl_xor(mx, 32, 64));
   if (half == 0) red_m[w][l32] = mx;
   lut_s[t] = lutv;
@@ -282,8 +281,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   auto pass3 = [&](auto self, auto ic) __attribute__((always_inline)) -> void {   // nested passes, as for K
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
-    v4i vn2[CT];
-    if (i + 2 < NTW) vload(nt + 8, vn2);
+    if (i + 1 < NTW) vload(nt + 4, vn);                 // one tile ahead (two cost 8 registers)
     int p[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -304,10 +302,7 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) oacc[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf[ct], pf, oacc[ct], 0, 0, 0);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      vf[ct] = vn[ct];
-      vn[ct] = vn2[ct];
-    }
+    for (int ct = 0; ct < CT; ++ct) vf[ct] = vn[ct];
     if constexpr (i + 1 < NTW) {
       if (nt + 4 < ntiles) self(self, std::integral_constant<int, i + 1>{});
     }
@@ -315,22 +310,39 @@ __global__ __launch_bounds__(A_THREADS) void attention_i8(AttnArgs a) {
   if (w < ntiles) pass3(pass3, std::integral_constant<int, 0>{});
 
   // ---- 4. sum the four partial O tiles, requant, store. Lane l holds O_w[row l % 32][32 ct + 8 g + 4 (l / 32) + e].
+  // Two LDS slots (half the partial-O space of one slot a wave, which lets five workgroups share a CU): waves 2 and 3
+  // store theirs, waves 0 and 1 add them in and store the pair sums, and every thread adds the two slots. A lane
+  // reads and then rewrites only its own chunks of a slot.
   __syncthreads();                                       // every wave is done with the p tables
-  int* op = opart[w] + l32 * OROW;
+  int* op = opart[w & 1] + l32 * OROW;
+  auto put = [&]() {
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct)
+    for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<v4i*>(op + 32 * ct + 8 * g + 4 * half) =
-          v4i{oacc[ct][4 * g], oacc[ct][4 * g + 1], oacc[ct][4 * g + 2], oacc[ct][4 * g + 3]};
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<v4i*>(op + 32 * ct + 8 * g + 4 * half) =
+            v4i{oacc[ct][4 * g], oacc[ct][4 * g + 1], oacc[ct][4 * g + 2], oacc[ct][4 * g + 3]};
+  };
+  if (w >= 2) put();
+  __syncthreads();
+  if (w < 2) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const v4i x = *reinterpret_cast<const v4i*>(op + 32 * ct + 8 * g + 4 * half);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) oacc[ct][4 * g + e] += x[e];
+      }
+    put();
+  }
   __syncthreads();
   constexpr int C4 = D / 4;                              // 4-column groups per row
   int8_t* Ob = a.O + b0 * a.so0 + b1 * a.so1 + (long long)q0 * a.ldo;
   for (int idx = t; idx < 32 * C4; idx += A_THREADS) {
     const int row = idx / C4, c = 4 * (idx % C4);
     v4i sum = *reinterpret_cast<const v4i*>(opart[0] + row * OROW + c);
-#pragma unroll
-    for (int ww = 1; ww < 4; ++ww) sum += *reinterpret_cast<const v4i*>(opart[ww] + row * OROW + c);
+    sum += *reinterpret_cast<const v4i*>(opart[1] + row * OROW + c);
     int o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = min(max((sum[e] * a.mo + a.rndo) >> a.so, -128), 127);
