@@ -23,8 +23,8 @@
 //      by score. O_w = P V over the wave's tiles on MFMA, P packed in registers: lane l's 16 probabilities of a tile
 //      are keys 16 (l / 32) .. + 15 (the key rows entered the score MFMA in bperm order), so its V^T fragment is one
 //      contiguous 16-byte load.
-//   4. The four partial O tiles (int32) are summed through two LDS slots; o = clamp((O M_o + rnd(s_o)) >> s_o), 4-byte
-//      stores.
+//   4. The four partial O tiles (int32) are summed through two LDS slots; o = clamp((O M_o + rnd(s_o)) >> s_o),
+//      4-byte stores.
 // Every product is proven to fit int32 (prove_no_overflow), so the requants run in 32 bits; with S24 the score
 // requant multiply is one 24-bit multiply-add (|acc|, |M_s| < 2^23).
 #include <algorithm>
