@@ -371,6 +371,9 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
         if (FULL) {
           if (res) {
             const int ma = g.ma, mb = g.mb, rnd2 = g.rnd2, sh2 = g.shift2;
+            // clamp before the shift, then one SDWA shift into each byte lane
+            const int clo2 = (int)max(-128ll << sh2, (long long)INT32_MIN);
+            const int chi2 = (int)min((128ll << sh2) - 1, (long long)INT32_MAX);
             v4i ov;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -378,9 +381,9 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int r = (int)(int8_t)((unsigned)rv[j][i][q] >> (8 * e));
-                o[e] = min(max((r * ma + v[4 * q + e] * mb + rnd2) >> sh2, -128), 127);   // proven inside int32
+                o[e] = med3i(r * ma + v[4 * q + e] * mb + rnd2, clo2, chi2);   // proven inside int32
               }
-              ov[q] = (int)pack4(o[0], o[1], o[2], o[3]);
+              ov[q] = (int)sra_pack4(o[0], o[1], o[2], o[3], sh2);
             }
             *reinterpret_cast<v4i*>(Db + (long long)m * g.ldd + n) = ov;
             if (!g.store_y) continue;
@@ -684,6 +687,9 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
     if (res) {
       int8_t* Db = g.D + b0 * g.sd0 + b1 * g.sd1 + (long long)m0 * g.ldd + n0;
       const int ma = g.ma, mb = g.mb, rnd2 = g.rnd2, sh2 = g.shift2;
+      // clamp before the shift, then one SDWA shift into each byte lane
+      const int clo2 = (int)max(-128ll << sh2, (long long)INT32_MIN);
+      const int chi2 = (int)min((128ll << sh2) - 1, (long long)INT32_MAX);
 #pragma unroll
       for (int pass = 0; pass < PASSES; ++pass) {
         v4i ov;
@@ -694,11 +700,9 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
           for (int e = 0; e < 4; ++e) {
             const int y = (int)(int8_t)((unsigned)ch[pass][q] >> (8 * e));
             const int r = (int)(int8_t)((unsigned)rv[pass][q] >> (8 * e));
-            o[e] = min(max((r * ma + y * mb + rnd2) >> sh2, -128), 127);      // proven inside int32
+            o[e] = med3i(r * ma + y * mb + rnd2, clo2, chi2);                // proven inside int32
           }
-          const unsigned t01 = __builtin_amdgcn_perm((unsigned)o[1], (unsigned)o[0], 0x0c0c0400u);
-          const unsigned t23 = __builtin_amdgcn_perm((unsigned)o[3], (unsigned)o[2], 0x0c0c0400u);
-          ov[q] = (int)__builtin_amdgcn_perm(t23, t01, 0x05040100u);
+          ov[q] = (int)sra_pack4(o[0], o[1], o[2], o[3], sh2);
         }
         *reinterpret_cast<v4i*>(Db + (long long)rr_of(pass) * g.ldd + cf_of(pass)) = ov;
       }
