@@ -89,6 +89,28 @@ def test_gemm_grouping_is_a_plan_choice(fake, cfg1):
     assert a.keys() == b.keys() and all(np.array_equal(a[k], b[k]) for k in a)
 
 
+def test_dependent_gemms_are_not_grouped(fake):
+    """Five qlinears of one input form a group of four and a single; a qlinear that reads another's output starts
+    a new run: the members of a group never read or write each other's buffers."""
+    g = GraphBuilder("grp")
+    x = g.input("x", [8, 16], scale=0.1)
+    ys = [g.qlinear(f"y{i}", x, g.const(f"w{i}", [16, 16]), 3, 9, scale=0.1) for i in range(5)]
+    z = g.qlinear("z", ys[4], g.const("wz", [16, 16]), 3, 9, scale=0.1)
+    u = g.qlinear("u", x, g.const("wu", [16, 16]), 3, 9, scale=0.1)
+    g.output(*ys, z, u)
+    rng = np.random.default_rng(5)
+    consts = {f"w{i}": rng.integers(-20, 20, (16, 16)) for i in range(5)}
+    consts.update(wz=rng.integers(-20, 20, (16, 16)), wu=rng.integers(-20, 20, (16, 16)))
+    cm = anvil_mi355x.compile((g.module(), consts))
+    xq = rng.integers(-128, 128, (8, 16))
+    res = cm.run(xq, quantized=True, keep="all")
+    assert [lb for lb, _, _ in cm.plan(1, "all").steps] == ["y0+y1+y2+y3", "y4", "z+u"]
+    assert [c[1] for c in fake.calls if c[0] == "gemm_group"] == [4, 2]
+    want = interp.run(g.module(), {"x": xq}, consts)
+    for k in ("y0", "y3", "y4", "z", "u"):
+        assert np.array_equal(res.ints[k], want.values[k]), k
+
+
 @pytest.mark.parametrize("seed", range(12))
 def test_planner_matches_oracle_on_random_graphs(fake, seed):
     m, c, x, want = helpers.random_case(seed)
