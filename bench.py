@@ -174,6 +174,8 @@ def main():
         "hbm_stream": stream,
         "end_to_end": e2e,
         "kernels": kernels,
+        "kernels_note": "per launch, HIP events around each kernel in an untimed pass of 3 steps (each figure includes "
+                        "the dispatch gap before its kernel); the timed figures are value and roofline.avg_us",
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
