@@ -119,7 +119,10 @@ class CompiledModel:
 
     def __init__(self, module, consts, *, device: int = 0, proven: bool = False):
         self.module, self.consts = module, dict(consts)
-        self.proven = bool(proven)        # prove_no_overflow held: kernels may skip their int32 checks
+        # proven: the sound int32 analysis (|multipliers|) holds, so kernels may skip their int32 checks. A graph
+        # that passes only the reference's looser check (a negative multiplier) runs on the checked kernels.
+        bounds = Q.int32_bounds(module, self.consts) if proven else None
+        self.proven = bool(proven) and bounds.ok
         self.func = g.func_of(module)
         self.ops = [op for op in self.func.ops if not isinstance(op, g.OutputOp)]
         outs = [op for op in self.func.ops if isinstance(op, g.OutputOp)]
@@ -140,9 +143,7 @@ class CompiledModel:
             if isinstance(op, g.ConstOp) or (isinstance(op, (g.TransposeOp, g.ReshapeOp)) and op.x in self.is_const):
                 self.is_const.add(op.result)
         self.phys = self._choose_layouts()
-        self.acc_bounds = {}                     # matmul result -> proven bound on |accumulator|
-        if self.proven:
-            Q.prove_no_overflow(module, self.consts, acc_bounds=self.acc_bounds)
+        self.acc_bounds = bounds.acc if self.proven else {}    # matmul result -> proven bound on |accumulator|
         self.device_index = device
         self.dev = None
         self.embedding = None             # (wte, wpe) float32 host tables of a token model

@@ -19,9 +19,9 @@ max-abs / 127 per tensor; requant (M, s) from fixed_point against the worst case
 from __future__ import annotations
 
 import hashlib
+import inspect
 import json
 import math
-import os
 from dataclasses import asdict, dataclass, field
 from pathlib import Path
 
@@ -89,6 +89,12 @@ def embed(spec: BlockSpec, params, ids):
     return params["wte"].astype(np.float64)[ids] + params["wpe"].astype(np.float64)[None, : ids.shape[-1]]
 
 
+def gelu(x):
+    """GELU, erf form (torch.nn.GELU's default), in float64."""
+    from scipy.special import erf
+    return 0.5 * x * (1 + erf(np.asarray(x, dtype=np.float64) / math.sqrt(2)))
+
+
 def _rms(x, w):
     return x / np.sqrt((x * x).mean(-1, keepdims=True) + np.float32(EPS)) * w
 
@@ -134,7 +140,7 @@ def float_forward_amax(spec: BlockSpec, params, x, amax: dict):
         rec(L + "h2", h2)
         fc = h2 @ params[L + "fc"].T
         rec(L + "fc", fc)
-        ge = Q.gelu(fc).astype(np.float32)
+        ge = gelu(fc).astype(np.float32)
         rec(L + "gelu", ge)
         proj = ge @ params[L + "proj"].T
         rec(L + "proj", proj)
@@ -175,12 +181,12 @@ def build_graph(spec: BlockSpec, params, x_scale: float, amax: dict) -> Built:
 
     def weight(w_io):
         sw = Q.maxabs_scale(w_io)
-        return Q.quantize_array(w_io, sw), sw
+        return Q.to_int8(w_io, sw), sw
 
     def rmsnorm(sym, xv, sx, w_f):
         so = act(sym)
         wq, sw = weight(w_f)
-        lut, s = Q.rmsnorm_lut(sx, sw, so, int(np.abs(wq).max()), C, EPS)
+        lut, s = Q.rsqrt_table(sx, sw, so, int(np.abs(wq).max()), C, EPS)
         v = b.rmsnorm_int(sym, xv, const(f"{sym}.w", wq, "i8", sw), const(f"{sym}.rsqrt_lut", lut, "i32"), 1, s, so)
         scales[sym], mag[sym] = so, 128
         return v, so
@@ -189,7 +195,7 @@ def build_graph(spec: BlockSpec, params, x_scale: float, amax: dict) -> Built:
         so = act(sym)
         wq, sw = weight(w_oi.T.astype(np.float64))
         bound = xmag * int(np.abs(wq).sum(axis=0).max())
-        (m,), s = Q.fixed_point([sx * sw / so], [bound])
+        (m,), s = Q.choose_shift([sx * sw / so], [bound])
         scale = so if lut is None else out_scale
         v = b.qlinear(sym, xv, const(f"{sym}.w", wq, "i8", sw), m, s, scale, lut=lut)
         scales[sym], mag[sym] = scale, 128
@@ -197,7 +203,7 @@ def build_graph(spec: BlockSpec, params, x_scale: float, amax: dict) -> Built:
 
     def add(sym, av, sa, bv, sb, ma_, mb_):
         so = act(sym)
-        (ma, mb), s = Q.fixed_point([sa / so, sb / so], [ma_, mb_])
+        (ma, mb), s = Q.choose_shift([sa / so, sb / so], [ma_, mb_])
         v = b.add_requant(sym, av, bv, ma, mb, s, so)
         scales[sym], mag[sym] = so, 128
         return v, so
@@ -214,20 +220,20 @@ def build_graph(spec: BlockSpec, params, x_scale: float, amax: dict) -> Built:
             heads[n] = b.transpose(f"{L}{n}h", r, [1, 0, 2])
         kT = b.transpose(f"{L}kT", heads["k"], [0, 2, 1])
         s_sc = act(L + "scores")
-        (m,), s = Q.fixed_point([sh["q"] * sh["k"] / math.sqrt(d) / s_sc], [d * 128 * 128])
+        (m,), s = Q.choose_shift([sh["q"] * sh["k"] / math.sqrt(d) / s_sc], [d * 128 * 128])
         sc = b.qmatmul(L + "scores", heads["q"], kT, m, s, s_sc)
-        elut = Q.exp_lut(s_sc, T, Q.SOFTMAX_ONE)
+        elut = Q.exp_table(s_sc, T, Q.SOFTMAX_ONE)
         p = b.softmax_lut(L + "p", sc, const(f"{L}p.exp_lut", elut, "i32"), Q.SOFTMAX_ONE, spec.causal,
                           1 / Q.SOFTMAX_ONE)
         s_o = act(L + "o")
-        (m,), s = Q.fixed_point([sh["v"] / Q.SOFTMAX_ONE / s_o], [T * Q.SOFTMAX_ONE * 128])
+        (m,), s = Q.choose_shift([sh["v"] / Q.SOFTMAX_ONE / s_o], [T * Q.SOFTMAX_ONE * 128])
         o = b.qmatmul(L + "o", p, heads["v"], m, s, s_o)
         om = b.reshape(f"{L}om", b.transpose(f"{L}om.t", o, [1, 0, 2]), [T, C])
         y, s_y = linear(L + "y", om, s_o, 128, params[L + "y"])
         r1, s_r1 = add(L + "r1", x, sx, y, s_y, 128, 128)
         h2, s_h2 = rmsnorm(L + "h2", r1, s_r1, params[L + "ln2"])
         s_fc, s_ge = act(L + "fc"), act(L + "gelu")
-        glut = Q.act_lut(Q.gelu, s_fc, s_ge)
+        glut = Q.activation_table(gelu, s_fc, s_ge)
         if spec.gelu == "fused":
             ge, _ = linear(L + "fc", h2, s_h2, 128, params[L + "fc"], lut=const(f"{L}fc.gelu_lut", glut, "i8", s_ge),
                            out_scale=s_ge)
@@ -284,30 +290,50 @@ def calibrate(spec: BlockSpec, params, tag: int):
     return sin, amax
 
 
-CACHE = Path(__file__).resolve().parents[1] / "_cache"
-_VERSION = 1
+CALIB_DIR = Path(__file__).resolve().parent / "calib"
+_CALIB_CODE = ("init_params", "embed", "_rms", "gelu", "float_forward_amax", "calib_inputs", "to_float_input",
+               "calibrate")
 
 
-def build(spec: BlockSpec, tag: int, cache: bool = True) -> Built:
-    """Calibrate and build the quantized graph of `spec` (weights seed spec.wseed, calibration seed tag). The
-    calibration result (input scale and max-abs values) is cached on disk by a digest of the spec; the graph is
-    always rebuilt from it."""
+def calib_code_digest() -> str:
+    """sha256 of the source of every function the calibration result depends on: a change to any of them gives a
+    new calibration key, so a stored result can never outlive the code that produced it."""
+    h = hashlib.sha256()
+    for name in _CALIB_CODE:
+        h.update(inspect.getsource(globals()[name]).encode())
+    return h.hexdigest()
+
+
+def calib_key(spec: BlockSpec, tag: int) -> str:
+    return hashlib.sha256(json.dumps([tag, asdict(spec), calib_code_digest()], sort_keys=True).encode()).hexdigest()[:16]
+
+
+def calib_path(spec: BlockSpec, tag: int) -> Path:
+    return CALIB_DIR / f"calib-{calib_key(spec, tag)}.json"
+
+
+def write_calibration(spec: BlockSpec, tag: int) -> Path:
+    """Run the float calibration of (spec, tag) and store it under calib/ (a tracked file: the committed
+    calibration, not the host's float arithmetic, then fixes every scale and constant of the built graph)."""
+    sin, amax = calibrate(spec, init_params(spec), tag)
+    path = calib_path(spec, tag)
+    CALIB_DIR.mkdir(parents=True, exist_ok=True)
+    body = {"key": calib_key(spec, tag), "tag": tag, "spec": asdict(spec), "sin": sin, "amax": amax}
+    path.write_text(json.dumps(body, indent=1, sort_keys=True) + "\n")
+    return path
+
+
+def build(spec: BlockSpec, tag: int, stored: bool = True) -> Built:
+    """The quantized graph of `spec` (weights seed spec.wseed, calibration seed tag). With stored=True (the default)
+    the calibration (input scale and max-abs values) comes from the tracked calib/ file of this spec, tag and
+    calibration code when there is one, so every machine builds the same constants; otherwise it is computed here."""
     params = init_params(spec)
-    key = hashlib.sha256(json.dumps([_VERSION, tag, asdict(spec)], sort_keys=True).encode()).hexdigest()[:16]
-    path = CACHE / f"calib-{key}.json"
-    if cache and path.exists():
+    path = calib_path(spec, tag)
+    if stored and path.exists():
         body = json.loads(path.read_text())
         sin, amax = body["sin"], body["amax"]
     else:
         sin, amax = calibrate(spec, params, tag)
-        if cache:
-            try:
-                CACHE.mkdir(parents=True, exist_ok=True)
-                tmp = path.with_suffix(f".tmp{os.getpid()}")
-                tmp.write_text(json.dumps({"sin": sin, "amax": amax}))
-                tmp.replace(path)
-            except OSError:
-                pass
     return build_graph(spec, params, sin, amax)
 
 
@@ -320,10 +346,10 @@ CONFIGS = {
 }
 
 
-def config(n: int, cache: bool = True):
+def config(n: int, stored: bool = True):
     """(Built, eval batch) for block config n in {1, 3, 4, 5}."""
     spec, tag, batch = CONFIGS[n]
-    return build(spec, tag, cache), batch
+    return build(spec, tag, stored), batch
 
 
 def config_tag(n: int) -> int:

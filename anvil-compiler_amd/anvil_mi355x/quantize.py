@@ -1,249 +1,340 @@
-"""Quantization recipe (host setup, run once per model): fixed-point multipliers, LUT builders, overflow proof.
+"""Integer constants of a quantized graph, and the int32 proof that guards them.
 
-Restates the reference's anvil/frontend/quantize.py:32-253 (contract 8, symmetric per-tensor int8):
+Everything here runs once on the host while a model is built. It decides three kinds of constants:
 
-    fixed_point(ms, bounds, k)    largest shift s with sum(bound_i * round(m_i 2^s)) + 2^(s+k-1) <= INT32_MAX
-    rmsnorm_lut / rmsnorm_lut_wide  rsqrt LUTs for rmsnorm_int (i8 rows; i16 rows with ss_shift / ss_init)
-    exp_bits / exp_lut            softmax_lut's exp table, exp_lut[d + 255] = round(exp(d s) 2^E)
-    act_lut(f, s_in, s_out)       any int8 -> int8 activation (SiLU, GELU) as a 256-entry LUT
-    prove_no_overflow(module)     propagate magnitude bounds and bound every int32 intermediate of every op
+* requant multipliers and shifts (choose_shift): the widest shift whose worst-case numerator still fits int32;
+* lookup tables: the rsqrt table of rmsnorm_int (rsqrt_table, wide_rsqrt_table), softmax_lut's exp table
+  (exp_table) and int8 -> int8 activation tables (activation_table);
+* the int32 proof over a finished graph (prove_no_overflow, int32_bounds).
 
-The MI355X kernels compute every requant numerator in 64 bits and flag, rather than wrap, a value outside int32;
-prove_no_overflow is what makes such a flag impossible for the graphs compile() accepts.
+The numbers these produce must equal the reference quantizer's (anvil/frontend/quantize.py:40-253, symmetric
+per-tensor int8, xf's contract 8), because bit-exact outputs need bit-equal constants: every float expression that
+feeds a rint() or a round() keeps the reference's operation order, and every bound the proof checks is the
+reference's. The code is organised differently: a shift search over all candidate shifts, a WideRow model of the
+reachable (index, step) states of a wide rmsnorm row, and a BoundWalker with one handler per op kind that serves
+two policies (the reference's decision, and the sound bound the GPU kernels rely on).
 """
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass, field
 
 import numpy as np
 
 from . import ir as g
 
 INT32_MAX = (1 << 31) - 1
-RSQRT_LEN = 1024
-SOFTMAX_ONE = 127
-HEADROOM = 1.5
-QMAX = {"i8": 127, "i16": (1 << 15) - 1}
+RSQRT_LEN = 1024            # entries of an rmsnorm rsqrt table
+SOFTMAX_ONE = 127           # softmax_lut's `one`: probabilities land in [0, 127]
+HEADROOM = 1.5              # activation scale = HEADROOM * max|activation| / 127
+DTYPE_MAG = {"i8": 128, "i16": 1 << 15, "i32": 1 << 31}    # largest |value| of each dtype
 
 
-def _rnd(s):
-    return (1 << (s - 1)) if s else 0
+def half(s: int) -> int:
+    """The rounding term of an arithmetic right shift by s: 2^(s-1), or 0 for s = 0."""
+    return 1 << (s - 1) if s > 0 else 0
 
 
-def rsqrt_index(ss: int, n: int):
-    """(idx, k) for one row sum: shift right by 2 until below n, counting steps (reference codegen/lower.py:107-113)."""
-    ss, k = int(ss), 0
-    while ss >= n:
-        ss >>= 2
-        k += 1
-    return ss, k
+# ------------------------------------------------------------------------------------------------ requant
 
+def choose_shift(ratios, bounds, extra: int = 0, top: int = 31):
+    """(multipliers, s) for real ratios m_i applied to integers of magnitude <= bound_i: the largest s in
+    [0, top - extra] at which M_i = round(m_i 2^s) keeps sum_i bound_i M_i + 2^(s+extra-1) within int32 (`extra` is
+    a shift the op adds at run time, as rmsnorm's normalisation steps do). Reference: anvil/frontend/quantize.py:40-56
+    (its fixed_point). ValueError when a multiplier rounds to 0 at that shift, OverflowError when no shift fits."""
+    ratios, bounds = list(ratios), list(bounds)
+    if not ratios or len(ratios) != len(bounds):
+        raise ValueError(f"choose_shift: {len(ratios)} ratios against {len(bounds)} bounds")
+    if min(ratios) <= 0 or min(bounds) < 0:
+        raise ValueError(f"choose_shift: ratios must be > 0 and bounds >= 0 (got {ratios}, {bounds})")
 
-def fixed_point(ms, bounds, k=0, *, max_shift=31):
-    """(M_i, s): the largest s in [0, max_shift - k] with M_i = round(m_i 2^s) and
-    sum(bound_i M_i) + 2^(s+k-1) <= INT32_MAX (reference quantize.py:40-56). ValueError if a multiplier vanishes
-    at the chosen shift, OverflowError if no shift fits."""
-    if len(ms) != len(bounds) or not ms:
-        raise ValueError("fixed_point needs one bound per multiplier")
-    if any(m <= 0 for m in ms) or any(b < 0 for b in bounds):
-        raise ValueError(f"multipliers must be positive and bounds non-negative: {ms}, {bounds}")
-    for s in range(max_shift - k, -1, -1):
-        mi = [round(m * (1 << s)) for m in ms]
-        if sum(int(b) * m for b, m in zip(bounds, mi)) + ((1 << (s + k - 1)) if s + k else 0) <= INT32_MAX:
-            if min(mi) < 1:
-                raise ValueError(f"multipliers {ms} vanish at shift {s}")
-            return mi, s
-    raise OverflowError(f"bounds {bounds} leave no room for multipliers {ms}")
+    def numerator(s):
+        mults = [round(m * (1 << s)) for m in ratios]
+        return mults, sum(int(b) * mm for b, mm in zip(bounds, mults)) + half(s + extra)
+
+    fitting = [s for s in range(top - extra + 1) if numerator(s)[1] <= INT32_MAX]
+    if not fitting:
+        raise OverflowError(f"choose_shift: bounds {bounds} overflow int32 for ratios {ratios} at every shift")
+    s = max(fitting)
+    mults = numerator(s)[0]
+    if min(mults) < 1:
+        raise ValueError(f"choose_shift: ratios {ratios} round to a zero multiplier at shift {s}")
+    return mults, s
 
 
 def maxabs_scale(x) -> float:
+    """Symmetric int8 scale of x: max|x| / 127."""
     return float(np.abs(np.asarray(x)).max()) / 127
 
 
-def quantize_array(x, scale):
+def to_int8(x, scale):
+    """Round half to even at `scale`, saturating at int8, as int64."""
     return np.clip(np.rint(np.asarray(x) / scale), -128, 127).astype(np.int64)
 
 
-def rsqrt_kmax(d, n=RSQRT_LEN, mag=128):
-    """Normalisation steps rmsnorm_int takes on the loudest row of d entries of magnitude mag."""
-    return rsqrt_index(d * mag * mag, n)[1]
+# ------------------------------------------------------------------------------------------------ rmsnorm
+
+def rsqrt_steps(ss: int, n: int):
+    """(index, k): the row sum ss divided by 4 (two bits shifted out) k times, until it indexes an n-entry table
+    (reference anvil/codegen/lower.py:107-113)."""
+    ss, k = int(ss), 0
+    while ss >= n:
+        ss, k = ss >> 2, k + 1
+    return ss, k
 
 
-def rmsnorm_lut(sx, sw, sh, wmax, d, eps, n=RSQRT_LEN):
-    """(rsqrt_lut, s) for an i8 row (reference quantize.py:72-80): lut[i] = round(rsqrt(sx^2 i / d + eps) sx sw / sh
-    2^s), lut[0] = 0."""
-    ss = np.arange(1, n)
-    r = np.r_[0, 1 / np.sqrt(sx ** 2 * ss / d + eps) * sx * sw / sh]
-    (rmax,), s = fixed_point([r.max()], [128 * wmax], rsqrt_kmax(d, n))
-    lut = np.rint(r * (1 << s)).astype(np.int64)
-    assert lut.max() == rmax
-    return lut, s
+def loudest_row_steps(d: int, n: int = RSQRT_LEN, mag: int = 128) -> int:
+    """The k of a row of d entries all of magnitude mag: the largest k any such row reaches."""
+    return rsqrt_steps(d * mag * mag, n)[1]
 
 
-def ss_shift_for(d, mag):
-    """Least c with d ((mag^2 + 2^(c-1)) >> c) <= INT32_MAX (reference quantize.py:85-91)."""
-    for c in range(31):
-        if d * ((mag * mag + _rnd(c)) >> c) <= INT32_MAX:
-            return c
-    raise OverflowError(f"no square shift fits {d} entries of magnitude {mag}")
+def rsqrt_table(sx, sw, sh, wmax, d, eps, n=RSQRT_LEN):
+    """(table, s) of an int8 rmsnorm from input scale sx through weight scale sw (max |w| = wmax) to output scale sh:
+    table[i] = rint(sx sw / sh / sqrt(sx^2 i / d + eps) 2^s) for i >= 1, table[0] = 0, with s the widest shift at
+    which x * w * table[i] (+ rounding, after up to loudest_row_steps(d) extra shifts) fits int32 for |x| <= 128
+    (reference anvil/frontend/quantize.py:72-80)."""
+    idx = np.arange(1, n)
+    real = np.r_[0, 1 / np.sqrt(sx ** 2 * idx / d + eps) * sx * sw / sh]
+    (top,), s = choose_shift([real.max()], [128 * wmax], loudest_row_steps(d, n))
+    table = np.rint(real * (1 << s)).astype(np.int64)
+    if table.max() != top:
+        raise AssertionError("rsqrt_table: the table's largest entry differs from its chosen multiplier")
+    return table, s
 
 
-def _xmax(ss_max, c, mag):
-    return min(mag, math.isqrt(max(0, (ss_max + 1) * (1 << c) - _rnd(c) - 1)))
+def square_shift(d: int, mag: int) -> int:
+    """Least c for which d squares of magnitude mag, each rounded and shifted right by c, sum within int32 (the
+    wide rmsnorm's ss_shift; 0 for int8 rows). Reference anvil/frontend/quantize.py:85-91."""
+    c = next((c for c in range(31) if d * ((mag * mag + half(c)) >> c) <= INT32_MAX), None)
+    if c is None:
+        raise OverflowError(f"square_shift: {d} squares of {mag} overflow int32 at every shift")
+    return c
 
 
-def rms_xmax_table(d, n, c, mag, e=0):
-    """{k: largest |x| a row with rsqrt_index(ss) = (i, k) can hold, per LUT index i} (reference
-    quantize.py:99-113)."""
-    ss_top = d * ((mag * mag + _rnd(c)) >> c) + e
-    kmax = rsqrt_index(ss_top, n)[1]
-    out = {}
-    for k in range(kmax + 1):
-        hi = np.minimum((np.arange(n, dtype=object) + 1) * (4 ** k) - 1, ss_top)
-        xm = np.array([_xmax(int(v) - e, c, mag) if v >= e else 0 for v in hi], dtype=np.int64)
-        if k:
-            xm[: n // 4] = 0
-        out[k] = xm
-    return out
+@dataclass
+class WideRow:
+    """The reachable states of an rmsnorm row of d entries (|x| <= mag) with square shift c and sum offset e:
+    ss = e + sum((x^2 + 2^(c-1)) >> c) lands on table index i after k steps of rsqrt_steps. For each k it holds
+    xmax[k][i], the largest |x| one entry of such a row can have; x * table[i] is largest at large k, not at the
+    table's largest entry (reference anvil/frontend/quantize.py:99-119)."""
+    d: int
+    n: int
+    c: int
+    mag: int
+    e: int = 0
+    xmax: dict = field(init=False)
+
+    def __post_init__(self):
+        top = self.d * ((self.mag * self.mag + half(self.c)) >> self.c) + self.e     # the loudest row's ss
+        self.xmax = {}
+        for k in range(rsqrt_steps(top, self.n)[1] + 1):
+            # the largest ss that still lands on index i after k steps, capped by the loudest row
+            ss_hi = [min((i + 1) * 4 ** k - 1, top) for i in range(self.n)]
+            col = np.array([self._largest_entry(v - self.e) if v >= self.e else 0 for v in ss_hi], dtype=np.int64)
+            if k > 0:
+                col[: self.n // 4] = 0         # a shifted sum is >= n/4: lower indices need k = 0
+            self.xmax[k] = col
+
+    def _largest_entry(self, budget: int) -> int:
+        """Largest |x| <= mag whose shifted square (x^2 + 2^(c-1)) >> c is at most budget."""
+        return min(self.mag, math.isqrt(max(0, ((budget + 1) << self.c) - half(self.c) - 1)))
+
+    @property
+    def kmax(self) -> int:
+        return max(self.xmax)
+
+    def numerators(self, table, wmax: int, mult: int, s: int) -> dict:
+        """{k: worst x * w * table[i] * mult + 2^(s+k-1)} over the reachable (i, k)."""
+        table = np.asarray(table, dtype=np.int64)
+        return {k: int((col * wmax * table).max()) * mult + half(s + k) for k, col in self.xmax.items()}
+
+    def worst_product(self, table, wmax: int) -> int:
+        table = np.asarray(table, dtype=np.int64)
+        return max(int((col * wmax * table).max()) for col in self.xmax.values())
 
 
-def rms_wide_bounds(lut, wmax, M, s, xm_table):
-    lut = np.asarray(lut, dtype=np.int64)
-    return {k: int((xm * wmax * lut).max()) * M + _rnd(s + k) for k, xm in xm_table.items()}
-
-
-def rmsnorm_lut_wide(sx, sw, sh, wmax, d, eps, mag, n=RSQRT_LEN):
-    """(rsqrt_lut, s, c, e) for an i16 row with eps folded into the sum (reference quantize.py:122-144)."""
-    c = ss_shift_for(d, mag)
+def wide_rsqrt_table(sx, sw, sh, wmax, d, eps, mag, n=RSQRT_LEN):
+    """(table, s, c, e) of an rmsnorm over wide (int16) rows. Squares are rounded and shifted by c = square_shift(d,
+    mag); eps enters as the integer offset e = max(1, round(eps / unit)) of the sum, unit = sx^2 2^c / d being the
+    mean square one count of ss stands for, so the table holds the eps-free rsqrt(unit i) sx sw / sh. s is the widest
+    shift at which every reachable x * w * table[i] (+ rounding) fits int32 under WideRow's bound (reference
+    anvil/frontend/quantize.py:122-144)."""
+    c = square_shift(d, mag)
     unit = sx ** 2 * (1 << c) / d
     e = max(1, int(round(eps / unit)))
-    if d * ((mag * mag + _rnd(c)) >> c) + e > INT32_MAX:
-        raise OverflowError(f"eps folds to {e}: the rmsnorm sum of squares cannot stay in int32 at scale {sx}")
-    ss = np.arange(1, n)
-    r = np.r_[0, 1 / np.sqrt(unit * ss) * sx * sw / sh]
-    xm = rms_xmax_table(d, n, c, mag, e)
-    kmax = max(xm)
-    for s in range(31 - kmax, -1, -1):
-        lut = np.rint(r * (1 << s)).astype(np.int64)
-        if max(rms_wide_bounds(lut, wmax, 1, s, xm).values()) <= INT32_MAX:
-            if lut[n // 4:].min() < 64:
-                raise ValueError(f"rsqrt LUT too coarse at shift {s} (min entry {lut[n // 4:].min()})")
-            return lut, s, c, e
-    raise OverflowError("no rsqrt LUT shift fits a wide rmsnorm")
+    if d * ((mag * mag + half(c)) >> c) + e > INT32_MAX:
+        raise OverflowError(f"wide_rsqrt_table: the eps offset {e} pushes the row sum past int32 at scale {sx}")
+    idx = np.arange(1, n)
+    real = np.r_[0, 1 / np.sqrt(unit * idx) * sx * sw / sh]
+    row = WideRow(d, n, c, mag, e)
+    for s in range(31 - row.kmax, -1, -1):
+        table = np.rint(real * (1 << s)).astype(np.int64)
+        if max(row.numerators(table, wmax, 1, s).values()) > INT32_MAX:
+            continue
+        coarsest = int(table[n // 4:].min())
+        if coarsest < 64:
+            raise ValueError(f"wide_rsqrt_table: at shift {s} the table's smallest reachable entry is {coarsest} < 64")
+        return table, s, c, e
+    raise OverflowError("wide_rsqrt_table: no table shift keeps the wide rmsnorm within int32")
 
 
-def exp_bits(t, one=SOFTMAX_ONE):
-    """Largest E with every softmax_lut intermediate in int32 for rows of t entries <= 2^E (reference
-    quantize.py:155-157)."""
-    return max(e for e in range(31) if (one + t // 2) << e <= INT32_MAX and t << e <= INT32_MAX)
+# ------------------------------------------------------------------------------------------------ softmax
+
+def exp_shift(t: int, one: int = SOFTMAX_ONE) -> int:
+    """Largest E for which a softmax row of t entries, each <= 2^E, keeps its sum (t 2^E) and its numerators
+    ((one + t // 2) 2^E) within int32 (reference anvil/frontend/quantize.py:155-157)."""
+    return max(e for e in range(31) if max(one + t // 2, t) << e <= INT32_MAX)
 
 
-def exp_lut(score_scale, t, one=SOFTMAX_ONE):
-    """exp_lut[d + 255] = round(exp(d score_scale) 2^E), d in [-255, 0] (reference quantize.py:160-162)."""
-    return np.rint(np.exp(np.arange(-255, 1) * score_scale) * (1 << exp_bits(t, one))).astype(np.int64)
+def exp_table(score_scale, t: int, one: int = SOFTMAX_ONE):
+    """softmax_lut's 256-entry table: entry j holds rint(exp((j - 255) score_scale) 2^E), E = exp_shift(t, one)
+    (reference anvil/frontend/quantize.py:160-162)."""
+    return np.rint(np.exp(np.arange(-255, 1) * score_scale) * (1 << exp_shift(t, one))).astype(np.int64)
 
+
+# ------------------------------------------------------------------------------------------------ activations
 
 def silu(x):
     return x / (1 + np.exp(-x))
 
 
-def gelu(x):
-    """GELU, erf form (torch.nn.GELU's default)."""
-    from scipy.special import erf
-    return 0.5 * x * (1 + erf(np.asarray(x, dtype=np.float64) / math.sqrt(2)))
+def activation_table(f, s_in, s_out):
+    """int8 -> int8 table of an elementwise activation: entry j holds to_int8(f((j - 128) s_in), s_out), as the
+    reference tabulates its SiLU node (anvil/frontend/quantize.py:446-452)."""
+    return to_int8(f(np.arange(-128, 128) * s_in), s_out)
 
 
-def act_lut(f, s_in, s_out):
-    """int8 activation LUT: quantize_array(f(i s_in), s_out) for i in [-128, 127], the reference's recipe for an
-    unfused SiLU node (quantize.py:446-452), applied here to any elementwise activation."""
-    return quantize_array(f(np.arange(-128, 128) * s_in), s_out)
+# ------------------------------------------------------------------------------------------------ int32 proof
+
+@dataclass
+class Bounds:
+    """What the int32 analysis of one graph found."""
+    worst: dict            # op sym -> largest |intermediate| of the op
+    failures: list         # one message per intermediate that can leave int32
+    acc: dict              # matmul result Value -> bound on |accumulator|
+
+    @property
+    def ok(self) -> bool:
+        return not self.failures
 
 
-def silu_lut(s_in):
-    """(lut, scale): SiLU at its own max-abs scale (reference quantize.py:147-152)."""
-    y = silu(np.arange(-128, 128) * s_in)
-    s = maxabs_scale(y)
-    return quantize_array(y, s), s
+class BoundWalker:
+    """Magnitude propagation over a graph: each value gets a bound on its |elements| (inputs by dtype, consts by
+    their values, op results by their dtype or LUT), and each op's int32 intermediates are bounded from its
+    operands' magnitudes, as the reference's prove_no_overflow does (anvil/frontend/quantize.py:175-253).
 
+    reference=True reproduces that function's decision exactly, including its two loose spots: multipliers enter
+    with their sign (a negative M bounds nothing), and a const right operand with batch dims sums its first axis.
+    reference=False is the sound policy the GPU kernels' unchecked paths rely on: |M|, and the column sums of each
+    batch entry of a const right operand."""
 
-# ----------------------------------------------------------------------------------------- overflow proof
+    def __init__(self, consts=None, reference: bool = True):
+        self.consts = consts or {}
+        self.reference = reference
+        self.mag, self.values, self.worst, self.failures, self.acc = {}, {}, {}, [], {}
+        self.handlers = {
+            g.InputOp: self._input, g.ConstOp: self._const, g.QMatmulOp: self._matmul, g.QLinearOp: self._matmul,
+            g.LutOp: self._lut, g.LutMulOp: self._lut_mul, g.RmsNormIntOp: self._rmsnorm,
+            g.SoftmaxLutOp: self._softmax, g.AddRequantOp: self._add, g.TransposeOp: self._view,
+            g.ReshapeOp: self._view,
+        }
 
-def prove_no_overflow(module, consts=None, acc_bounds: dict | None = None) -> dict:
-    """Magnitude propagation over the graph (reference quantize.py:175-253): int8 inputs 128, i16 2^15, softmax
-    outputs `one`, LUT outputs max|table|. Returns {op sym: worst |intermediate|}; raises OverflowError naming
-    every op whose bound exceeds INT32_MAX. acc_bounds, when given, receives {matmul result value: bound on its
-    |accumulator|} (what lets a kernel use a 24-bit requant multiply)."""
-    consts = consts or {}
-    mag, cval, worst, bad = {}, {}, {}, []
-    for op in g.func_of(module).ops:
-        if isinstance(op, g.OutputOp):
-            continue
-        r = op.results[0]
-        name = op.sym_str or op.name
-        checks = {}
-        if isinstance(op, g.InputOp):
-            m = {"i8": 128, "i16": 1 << 15}.get(g.qt(r).dtype, 1 << 31)
-        elif isinstance(op, g.ConstOp):
-            v = (np.asarray(op.value, dtype=np.int64).reshape(g.qt(r).dims) if op.value is not None
-                 else np.asarray(consts[op.sym_str], dtype=np.int64))
-            cval[r] = v
-            m = int(np.abs(v).max()) if v.size else 0
-        elif isinstance(op, (g.QMatmulOp, g.QLinearOp)):
-            M, s = abs(int(op.M)), int(op.s)          # magnitudes: a negative multiplier flips no bound
-            if op.b in cval:
-                acc = mag[op.a] * int(np.abs(cval[op.b]).sum(axis=0).max())
-            else:
-                acc = g.qt(op.a).dims[-1] * mag[op.a] * mag[op.b]
-            checks = {"acc": acc, "acc*M + round": acc * M + _rnd(s)}
-            if acc_bounds is not None:
-                acc_bounds[r] = acc
-            m = mag[op.lut] if op.lut is not None else (128 if g.qt(r).dtype == "i8" else 1 << 15)
-        elif isinstance(op, g.LutOp):
-            m = mag[op.table]
-        elif isinstance(op, g.LutMulOp):
-            M, s = abs(int(op.M)), int(op.s)          # magnitudes: a negative multiplier flips no bound
-            prod = mag[op.table] * mag[op.y]
-            checks = {"lut*y": prod, "lut*y*M + round": prod * M + _rnd(s)}
-            m = 128
-        elif isinstance(op, g.RmsNormIntOp):
-            M, s = abs(int(op.M)), int(op.s)          # magnitudes: a negative multiplier flips no bound
-            d, n = g.qt(op.x).dims[-1], g.qt(op.lut).dims[0]
-            c, e = op.ss_shift_int, op.ss_init_int
-            if g.qt(op.x).dtype == "i8" and c == 0 and e == 0:
-                kmax = rsqrt_kmax(d, n, mag[op.x])
-                xwr = mag[op.x] * mag[op.w] * mag[op.lut]
-                checks = {"sum x^2": d * mag[op.x] ** 2, "x*w*r": xwr, "x*w*r*M + round": xwr * M + _rnd(s + kmax)}
-            else:
-                if op.lut not in cval:
-                    raise ValueError(f"{name}: the wide rmsnorm bound needs the rsqrt LUT's values")
-                xm = rms_xmax_table(d, n, c, mag[op.x], e)
-                kmax = max(xm)
-                lut = cval[op.lut]
-                xwr = max(int((v * mag[op.w] * lut).max()) for v in xm.values())
-                checks = {"x^2 + round": mag[op.x] ** 2 + _rnd(c),
-                          "sum x^2": d * ((mag[op.x] ** 2 + _rnd(c)) >> c) + e, "x*w": mag[op.x] * mag[op.w],
-                          "x*w*r": xwr, "x*w*r*M + round": max(rms_wide_bounds(lut, mag[op.w], M, s, xm).values())}
-            if s + kmax > 31:
-                bad.append(f"{name}: shift s + kmax = {s + kmax} > 31")
-            m = 128
-        elif isinstance(op, g.SoftmaxLutOp):
-            one, emax, t = int(op.one), mag[op.lut], g.qt(op.x).dims[-1]
-            checks = {"exp sum": t * emax, "e*one + S/2": emax * one + t * emax // 2}
-            m = one
-        elif isinstance(op, g.AddRequantOp):
-            Ma, Mb, s = abs(int(op.Ma)), abs(int(op.Mb)), int(op.s)
-            checks = {"a*Ma + b*Mb + round": mag[op.a] * Ma + mag[op.b] * Mb + _rnd(s)}
-            m = 128 if g.qt(r).dtype == "i8" else 1 << 15
-        elif isinstance(op, (g.TransposeOp, g.ReshapeOp)):
-            m = mag[op.x]
-            if op.x in cval:
-                cval[r] = cval[op.x]
+    def _m(self, attr) -> int:
+        v = int(attr)
+        return v if self.reference else abs(v)
+
+    def walk(self, module) -> Bounds:
+        for op in g.func_of(module).ops:
+            if isinstance(op, g.OutputOp):
+                continue
+            handler = self.handlers.get(type(op))
+            if handler is None:
+                raise NotImplementedError(f"int32 proof: no bound for {op.name}")
+            mag, terms = handler(op)
+            self.mag[op.results[0]] = mag
+            if terms:
+                label = op.sym_str or op.name
+                self.worst[label] = max(v for _, v in terms)
+                self.failures += [f"{label}: {what} can reach {v} > {INT32_MAX}" for what, v in terms if v > INT32_MAX]
+        return Bounds(self.worst, self.failures, self.acc)
+
+    # ---- one handler per op kind: (magnitude of the result, [(intermediate, bound)])
+    def _input(self, op):
+        return DTYPE_MAG.get(g.qt(op.result).dtype, 1 << 31), []
+
+    def _const(self, op):
+        t = g.qt(op.result)
+        src = op.value if op.value is not None else self.consts[op.sym_str]
+        v = np.asarray(src, dtype=np.int64).reshape(t.dims)
+        self.values[op.result] = v
+        return (int(np.abs(v).max()) if v.size else 0), []
+
+    def _matmul(self, op):
+        mult, s = self._m(op.M), int(op.s)
+        if op.b in self.values:
+            w = np.abs(self.values[op.b])
+            colsum = w.sum(axis=0) if self.reference else w.sum(axis=-2)
+            acc = self.mag[op.a] * int(colsum.max())
         else:
-            raise NotImplementedError(f"prove_no_overflow: {op.name}")
-        mag[r] = m
-        if checks:
-            worst[name] = max(checks.values())
-            bad += [f"{name}: {k} reaches {v} > {INT32_MAX}" for k, v in checks.items() if v > INT32_MAX]
-    if bad:
-        raise OverflowError("int32 overflow possible: " + "; ".join(bad))
-    return worst
+            acc = g.qt(op.a).dims[-1] * self.mag[op.a] * self.mag[op.b]
+        self.acc[op.result] = acc
+        out = self.mag[op.lut] if op.lut is not None else DTYPE_MAG[g.qt(op.result).dtype]
+        return out, [("accumulator", acc), ("requant numerator", acc * mult + half(s))]
+
+    def _lut(self, op):
+        return self.mag[op.table], []
+
+    def _lut_mul(self, op):
+        prod = self.mag[op.table] * self.mag[op.y]
+        return 128, [("table * y", prod), ("requant numerator", prod * self._m(op.M) + half(int(op.s)))]
+
+    def _rmsnorm(self, op):
+        mult, s = self._m(op.M), int(op.s)
+        d, n = g.qt(op.x).dims[-1], g.qt(op.lut).dims[0]
+        c, e = op.ss_shift_int, op.ss_init_int
+        mx, mw = self.mag[op.x], self.mag[op.w]
+        if g.qt(op.x).dtype == "i8" and c == 0 and e == 0:
+            # int8 rows: every entry at its dtype bound and the table at its largest entry
+            kmax = loudest_row_steps(d, n, mx)
+            xwr = mx * mw * self.mag[op.lut]
+            terms = [("sum of squares", d * mx * mx), ("x * w * table", xwr),
+                     ("requant numerator", xwr * mult + half(s + kmax))]
+        else:
+            if op.lut not in self.values:
+                raise ValueError(f"{op.sym_str or op.name}: a wide rmsnorm is bounded through its rsqrt table, "
+                                 "which must be a const")
+            row = WideRow(d, n, c, mx, e)
+            kmax, table = row.kmax, self.values[op.lut]
+            terms = [("rounded square", mx * mx + half(c)), ("sum of squares", d * ((mx * mx + half(c)) >> c) + e),
+                     ("x * w", mx * mw), ("x * w * table", row.worst_product(table, mw)),
+                     ("requant numerator", max(row.numerators(table, mw, mult, s).values()))]
+        if s + kmax > 31:
+            self.failures.append(f"{op.sym_str or op.name}: requant shift s + kmax = {s + kmax} exceeds 31")
+        return 128, terms
+
+    def _softmax(self, op):
+        one, top, t = int(op.one), self.mag[op.lut], g.qt(op.x).dims[-1]
+        return one, [("row sum", t * top), ("numerator", top * one + t * top // 2)]
+
+    def _add(self, op):
+        num = self.mag[op.a] * self._m(op.Ma) + self.mag[op.b] * self._m(op.Mb) + half(int(op.s))
+        return DTYPE_MAG[g.qt(op.result).dtype], [("requant numerator", num)]
+
+    def _view(self, op):
+        if op.x in self.values:
+            self.values[op.result] = self.values[op.x]
+        return self.mag[op.x], []
+
+
+def int32_bounds(module, consts=None, *, reference: bool = False) -> Bounds:
+    """The int32 analysis of a graph under one policy (BoundWalker); never raises for a bound."""
+    return BoundWalker(consts, reference).walk(module)
+
+
+def prove_no_overflow(module, consts=None) -> dict:
+    """The reference's compile-time check (anvil/frontend/quantize.py:175-253, called by anvil/driver.py:119-132):
+    {op sym: worst |intermediate|} when every bound holds under its rules, else OverflowError naming each op."""
+    b = int32_bounds(module, consts, reference=True)
+    if not b.ok:
+        raise OverflowError("int32 overflow possible: " + "; ".join(b.failures))
+    return b.worst

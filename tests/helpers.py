@@ -1,9 +1,12 @@
 """Test helpers: seeded random transformer-style graphs, the scalar C oracle binding and a graph walker over it.
 
-random_case(seed) restates the coverage of the reference's random graph generator (tests/vortexv/vv_graphs.py:49-123):
-multi-head batched matmuls with a transposed or plain right operand, transposes of any perm, reshapes, odd row
-lengths, LUT epilogues, i16 results feeding an i16 rmsnorm with ss_shift / ss_init, causal and non-causal softmax
-with T1 != T2 and an i32 softmax output. A draw the oracle rejects (int32 overflow, zero softmax sum) is redrawn.
+random_case(seed) draws a graph with the op mix the reference's random graph tests cover (tests/vortexv/
+vv_graphs.py): head-batched matmuls whose right operand is a transposed view reached by one or two transposes, a
+cross-attention key length, causal and non-causal softmax (one output in i32), reshapes, LUT epilogues, lut_mul and
+lut, negative multipliers, and a wide variant whose i16 residual stream feeds an rmsnorm with ss_shift / ss_init.
+The generator evaluates each op on the sampled inputs as it adds it, and fits every requant multiplier to the spread
+of the accumulator it scales, so values spread across their dtype instead of saturating. A draw the oracle rejects
+(int32 overflow, zero softmax sum) is redrawn.
 """
 from __future__ import annotations
 
@@ -17,104 +20,150 @@ import numpy as np
 
 from anvil_mi355x.ir import GraphBuilder
 from oracle import interp
+from oracle import semantics as sem
 
 ROOT = Path(__file__).resolve().parents[1]
 
 
-def _rsqrt_lut(n):
-    return np.round((1 << 15) / np.sqrt(np.arange(n) + 1)).astype(np.int64)
+class _Fuzz:
+    """A GraphBuilder paired with the values of its ops on one sampled input."""
 
+    def __init__(self, rng):
+        self.rng = rng
+        self.b = GraphBuilder("rand")
+        self.consts, self.val = {}, {}
 
-def _exp_lut(tau=24.0):
-    return np.round((1 << 14) * np.exp((np.arange(256) - 255) / tau)).astype(np.int64)
+    def pick(self, *opts):
+        return opts[int(self.rng.integers(len(opts)))]
 
+    def input(self, name, shape, dtype="i8"):
+        v = self.b.input(name, list(shape), dtype)
+        self.val[v] = self.rng.integers(-128, 128, shape)
+        return v
 
-SD = 60.0
+    def const(self, name, data, dtype="i8"):
+        data = np.asarray(data, dtype=np.int64)
+        self.consts[name] = data
+        v = self.b.const(name, list(data.shape), dtype)
+        self.val[v] = data
+        return v
 
+    def weight(self, name, shape):
+        return self.const(name, self.rng.integers(-128, 128, shape))
 
-def _scaled(rng, prod_sd, target_sd, lo=10, hi=20):
-    s = int(rng.integers(lo, hi + 1))
-    m = max(1, int(round(target_sd / prod_sd * (1 << s) * rng.uniform(0.5, 2.0))))
-    return min(m, (1 << 31) - 1), s
+    def fit(self, acc, spread, shifts, negative=False):
+        """(M, s): s drawn from `shifts`, M scaling the accumulator's root mean square to about `spread`."""
+        s = int(self.rng.integers(shifts[0], shifts[1] + 1))
+        sd = max(float(np.sqrt(np.mean(np.square(acc, dtype=np.float64)))), 1.0)
+        m = int(np.clip(round(spread / sd * (1 << s) * self.rng.uniform(0.6, 1.7)), 1, (1 << 31) - 1))
+        return -m if negative else m, s
 
+    def matmul(self, kind, name, a, b, spread=45.0, lut=None, dtype="i8", negative=False):
+        acc = self.val[a] @ self.val[b]
+        m, s = self.fit(acc, spread, (9, 19), negative)
+        r = getattr(self.b, kind)(name, a, b, m, s, lut=lut, dtype=dtype)
+        self.val[r] = sem.qmatmul(self.val[a], self.val[b], m, s, None if lut is None else self.val[lut], dtype)
+        return r
 
-def _mm(rng, k, target_sd=40.0):
-    return _scaled(rng, SD * SD * np.sqrt(k), target_sd)
+    def view(self, kind, name, x, arg):
+        r = getattr(self.b, kind)(name, x, list(arg))
+        self.val[r] = np.transpose(self.val[x], arg) if kind == "transpose" else self.val[x].reshape(arg)
+        return r
+
+    def rmsnorm(self, name, x, table, wide=False):
+        d = self.val[x].shape[-1]
+        w = self.weight(name + ".w", [d])
+        xv = self.val[x]
+        c, e = (int(self.rng.integers(3, 9)), int(self.rng.integers(0, 80))) if wide else (0, 0)
+        ss = ((xv * xv + (1 << c >> 1)) >> c).sum(-1) + e
+        idx, k = sem.rsqrt_index(ss, len(self.val[table]))
+        acc = xv * self.val[w] * self.val[table][idx][..., None] / (2.0 ** k)[..., None]
+        if wide:           # the wide rows keep M = 1, as the quantizer builds them: the spread is set by s alone
+            rms = max(float(np.sqrt(np.mean(np.square(acc)))), 1.0)
+            m, s = 1, int(np.clip(round(np.log2(rms / 45.0) + self.rng.uniform(-0.7, 0.7)), 0, 31 - int(k.max())))
+        else:
+            m, s = self.fit(acc, 45.0, (12, 22))
+        r = self.b.rmsnorm_int(name, x, w, table, m, s, ss_shift=c, ss_init=e)
+        self.val[r] = sem.rmsnorm_wide(xv, self.val[w], self.val[table], m, s, c, e, "i16" if wide else "i8")
+        return r
+
+    def add(self, name, a, b_, dtype, spread):
+        ma, s = self.fit(self.val[a], spread / 2, (8, 16))
+        mb, _ = self.fit(self.val[b_], spread / 2, (s, s))
+        r = self.b.add_requant(name, a, b_, ma, mb, s, dtype=dtype)
+        self.val[r] = sem.add_requant(self.val[a], self.val[b_], ma, mb, s, dtype)
+        return r
+
+    def softmax(self, name, x, table, one, causal, dtype="i8"):
+        r = self.b.softmax_lut(name, x, table, one, causal, dtype=dtype)
+        self.val[r] = sem.softmax_lut(self.val[x], self.val[table], one, causal)
+        return r
+
+    def lut(self, name, x, table):
+        r = self.b.lut(name, x, table)
+        self.val[r] = sem.lut_i8(self.val[x], self.val[table])
+        return r
+
+    def lut_mul(self, name, x, y, table):
+        prod = self.val[table][self.val[x] + 128] * self.val[y]
+        m, s = self.fit(prod, 45.0, (9, 19))
+        r = self.b.lut_mul(name, x, y, table, m, s)
+        self.val[r] = sem.swiglu_lut(self.val[x], self.val[y], self.val[table], m, s)
+        return r
 
 
 def _draw(rng):
-    T = int(rng.integers(2, 9))
-    T2 = T if rng.random() < 0.6 else int(rng.integers(2, 9))
-    H = int(rng.integers(1, 4))
-    dh = int(rng.integers(2, 11))
-    d = int(rng.integers(3, 22))
-    ff = int(rng.integers(3, 26))
-    wide = rng.random() < 0.5
-    neg_m = rng.random() < 0.3
-    g = GraphBuilder("rand")
-    consts = {}
-
-    def const(name, shape, dtype="i8", value=None):
-        v = rng.integers(-128, 128, shape) if value is None else np.asarray(value)
-        consts[name] = np.asarray(v, dtype=np.int64)
-        return g.const(name, list(consts[name].shape), dtype)
-
-    x = g.input("x", [T, d])
-    xk = g.input("xk", [T2, d])
-    nl = int(rng.choice([64, 256, 1024]))
-    rs = const("rsqrt", [nl], "i32", _rsqrt_lut(nl))
-    rms = lambda: _scaled(rng, SD * (1 << 15) / (SD * np.sqrt(d)), 40.0, 4, 14)   # noqa: E731
-    h = g.rmsnorm_int("h", x, const("nw", [d]), rs, *rms())
-    hk = g.rmsnorm_int("hk", xk, const("nwk", [d]), rs, *rms())
-    q = g.qlinear("q", h, const("wq", [d, H * dh]), *_mm(rng, d))
-    k = g.qlinear("k", hk, const("wk", [d, H * dh]), *_mm(rng, d))
-    v = g.qlinear("v", hk, const("wv", [d, H * dh]), *_mm(rng, d))
-    qh = g.transpose("qh", g.reshape("q3", q, [T, H, dh]), [1, 0, 2])
-    k3 = g.reshape("k3", k, [T2, H, dh])
+    """One random graph: rmsnorm -> multi-head (possibly cross) attention -> residual -> rmsnorm -> gated MLP ->
+    residual, plus a second softmax of the scores as an i32 output."""
+    f = _Fuzz(rng)
+    tq = int(rng.integers(2, 10))
+    tk = tq if rng.random() < 0.55 else int(rng.integers(2, 10))
+    heads, hd = int(rng.integers(1, 4)), int(rng.integers(2, 12))
+    d, ff = int(rng.integers(3, 23)), int(rng.integers(3, 27))
+    wide = bool(rng.random() < 0.5)
+    n_rs = int(f.pick(64, 256, 1024))
+    rsqrt = f.const("rsqrt", np.round(32768.0 / np.sqrt(np.arange(n_rs) + 1.0)), "i32")
+    x, xk = f.input("x", (tq, d)), f.input("xk", (tk, d))
+    h, hk = f.rmsnorm("h", x, rsqrt), f.rmsnorm("hk", xk, rsqrt)
+    q = f.matmul("qlinear", "q", h, f.weight("wq", [d, heads * hd]))
+    k = f.matmul("qlinear", "k", hk, f.weight("wk", [d, heads * hd]))
+    v = f.matmul("qlinear", "v", hk, f.weight("wv", [d, heads * hd]))
+    qh = f.view("transpose", "qh", f.view("reshape", "q3", q, (tq, heads, hd)), (1, 0, 2))
+    k3 = f.view("reshape", "k3", k, (tk, heads, hd))
     if rng.random() < 0.5:
-        kT = g.transpose("kT", k3, [1, 2, 0])
+        kt = f.view("transpose", "kT", k3, (1, 2, 0))
     else:
-        kT = g.transpose("kT", g.transpose("kh", k3, [1, 0, 2]), [0, 2, 1])
-    sc = g.qmatmul("scores", qh, kT, *_mm(rng, dh))
+        kt = f.view("transpose", "kT", f.view("transpose", "kh", k3, (1, 0, 2)), (0, 2, 1))
+    scores = f.matmul("qmatmul", "scores", qh, kt)
+    temp = float(rng.uniform(8.0, 40.0))
+    exp = f.const("exp", np.round(16384.0 * np.exp((np.arange(256) - 255.0) / temp)), "i32")
     causal = bool(rng.random() < 0.6)
-    ex = const("exp", [256], "i32", _exp_lut(float(rng.uniform(8, 40))))
-    p = g.softmax_lut("p", sc, ex, int(rng.integers(32, 128)), causal)
-    vh = g.transpose("vh", g.reshape("v3", v, [T2, H, dh]), [1, 0, 2])
-    om, os_ = _mm(rng, T2)
-    o = g.qmatmul("o", p, vh, -om if neg_m else om, os_)
-    o2 = g.reshape("o2", g.transpose("ot", o, [1, 0, 2]), [T, H * dh])
-    y = g.qlinear("y", o2, const("wo", [H * dh, d]), *_mm(rng, H * dh))
-    rdt = "i16" if wide else "i8"
-    rt_ = 2000.0 if wide else 40.0
-    ma, s1 = _scaled(rng, SD, rt_ / 2, 8, 16)
-    r1 = g.add_requant("r1", x, y, ma, _scaled(rng, SD, rt_ / 2, s1, s1)[0], s1, dtype=rdt)
-    if wide:
-        h2 = g.rmsnorm_int("h2", r1, const("nw2", [d]), rs, 1, int(rng.integers(12, 20)),
-                           ss_shift=int(rng.integers(4, 9)), ss_init=int(rng.integers(0, 64)))
-    else:
-        h2 = g.rmsnorm_int("h2", r1, const("nw2", [d]), rs, *rms())
-    silu = const("silu", [256])
-    gate = g.qlinear("gate", h2, const("wg", [d, ff]), *_mm(rng, d),
-                     lut=const("glut", [256]) if rng.random() < 0.5 else None)
-    up = g.qlinear("up", h2, const("wu", [d, ff]), *_mm(rng, d))
-    act = g.lut_mul("act", gate, up, silu, *_scaled(rng, SD * SD, 40.0))
-    act = g.lut("act2", act, const("lut2", [256]))
-    dn = g.qlinear("down", act, const("wd", [ff, d]), *_mm(rng, ff, 2000.0 if wide else 40.0), dtype=rdt)
-    rsd = 2000.0 if wide else SD
-    ma, s2 = _scaled(rng, rsd, 20.0, 8, 18)
-    out = g.add_requant("out", r1, dn, ma, _scaled(rng, rsd, 20.0, s2, s2)[0], s2)
-    p32 = g.softmax_lut("p32", sc, ex, int(rng.integers(1, 1 << 12)), not causal, dtype="i32")
-    g.output(out, p32)
-    inputs = {"x": rng.integers(-128, 128, (T, d)), "xk": rng.integers(-128, 128, (T2, d))}
-    return g.module(), consts, inputs
+    p = f.softmax("p", scores, exp, int(rng.integers(32, 128)), causal)
+    vh = f.view("transpose", "vh", f.view("reshape", "v3", v, (tk, heads, hd)), (1, 0, 2))
+    o = f.matmul("qmatmul", "o", p, vh, negative=bool(rng.random() < 0.3))
+    om = f.view("reshape", "o2", f.view("transpose", "ot", o, (1, 0, 2)), (tq, heads * hd))
+    y = f.matmul("qlinear", "y", om, f.weight("wo", [heads * hd, d]))
+    res_dt, res_spread = ("i16", 2000.0) if wide else ("i8", 45.0)
+    r1 = f.add("r1", x, y, res_dt, res_spread)
+    h2 = f.rmsnorm("h2", r1, rsqrt, wide=wide)
+    glut = f.weight("glut", [256]) if rng.random() < 0.5 else None
+    gate = f.matmul("qlinear", "gate", h2, f.weight("wg", [d, ff]), lut=glut)
+    up = f.matmul("qlinear", "up", h2, f.weight("wu", [d, ff]))
+    act = f.lut("act2", f.lut_mul("act", gate, up, f.weight("silu", [256])), f.weight("lut2", [256]))
+    down = f.matmul("qlinear", "down", act, f.weight("wd", [ff, d]), spread=res_spread, dtype=res_dt)
+    out = f.add("out", r1, down, "i8", 20.0)
+    p32 = f.softmax("p32", scores, exp, int(rng.integers(1, 1 << 12)), not causal, dtype="i32")
+    f.b.output(out, p32)
+    inputs = {"x": f.val[x], "xk": f.val[xk]}
+    return f.b.module(), f.consts, inputs
 
 
 def random_case(seed, tries=50):
     """(module, consts, inputs, oracle GraphResult) for seed, redrawn until the oracle accepts the draw."""
-    rng = np.random.default_rng([7, seed])
+    rng = np.random.default_rng([11, seed])
     for _ in range(tries):
-        m, c, x = _draw(rng)
         try:
+            m, c, x = _draw(rng)
             return m, c, x, interp.run(m, x, c)
         except (OverflowError, ValueError, ZeroDivisionError):
             continue

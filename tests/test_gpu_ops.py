@@ -44,7 +44,7 @@ def test_gemm_config2_sweep(dev, M, K):
     a = rng.integers(-127, 128, (M, K))
     w = rng.integers(-127, 128, (K, K))
     acc = sem.matmul_i8(a, w, fast=True)
-    (m,), s = Q.fixed_point([127 / (1.5 * int(np.abs(acc).max()))], [128 * int(np.abs(w).sum(axis=0).max())])
+    (m,), s = Q.choose_shift([127 / (1.5 * int(np.abs(acc).max()))], [128 * int(np.abs(w).sum(axis=0).max())])
     want = sem.requant(acc, m, s)
     got = run_gemm(dev, a, w, m, s)
     assert np.array_equal(got, want), (M, K, int((got != want).sum()))
@@ -119,7 +119,7 @@ def test_rmsnorm_i8(dev, d, flags):
     16 lanes a row when d is 256, 512, 768 or 1024; results are the same bits either way."""
     rng = np.random.default_rng([6, d])
     w = rng.integers(-127, 128, d)
-    lut, s = Q.rmsnorm_lut(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
+    lut, s = Q.rsqrt_table(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
     x = np.concatenate([rng.integers(-128, 128, (200, d)), np.full((1, d), -128), np.zeros((1, d), int),
                         np.full((1, d), 127), np.rint(rng.standard_normal((50, d)) * 3).astype(int)])
     want = sem.rmsnorm_int(x, w, lut, 1, s)
@@ -136,7 +136,7 @@ def test_rmsnorm_fast_walks_many_row_groups(dev, flags, d):
     rows = 8 * 4 * 256 * 4 * 3 + 3
     rng = np.random.default_rng([61, rows])
     w = rng.integers(-127, 128, d)
-    lut, s = Q.rmsnorm_lut(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
+    lut, s = Q.rsqrt_table(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
     x = rng.integers(-128, 128, (rows, d))
     want = sem.rmsnorm_int(x, w, lut, 1, s)
     assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s, flags=flags), want)
@@ -160,7 +160,7 @@ def test_rmsnorm_i16_wide(dev):
     d = 32
     rng = np.random.default_rng(8)
     w = rng.integers(-127, 128, d)
-    lut, s, c, e = Q.rmsnorm_lut_wide(4e-4, 0.01, 0.02, 127, d, 1e-6, 1 << 15)
+    lut, s, c, e = Q.wide_rsqrt_table(4e-4, 0.01, 0.02, 127, d, 1e-6, 1 << 15)
     x = np.concatenate([rng.integers(-(1 << 15), 1 << 15, (100, d)), np.full((1, d), -(1 << 15)),
                         np.full((1, d), (1 << 15) - 1), np.zeros((1, d), int)])
     want = sem.rmsnorm_wide(x, w, lut, 1, s, c, e, "i16")
@@ -190,7 +190,7 @@ def test_softmax(dev, causal, shape, flags):
     x = rng.integers(-128, 128, shape)
     x[..., 0, :] = -128                          # a row of the minimum value
     x[..., -1, :] = 127                          # and one of the maximum
-    lut = Q.exp_lut(0.05, shape[-1])
+    lut = Q.exp_table(0.05, shape[-1])
     want = sem.softmax_lut(x, lut, 127, causal)
     assert np.array_equal(_softmax(dev, x, lut, 127, causal, flags=flags), want)
 
@@ -290,7 +290,7 @@ def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127
     if lut_kind == "random":
         lut = rng.integers(1, 1 << 20, 256)
     else:
-        lut = Q.exp_lut(0.5 if lut_kind == "steep" else 0.05, T, one)
+        lut = Q.exp_table(0.5 if lut_kind == "steep" else 0.05, T, one)
     split = lambda a: a.reshape(B, T, H, D).transpose(0, 2, 1, 3)       # noqa: E731
     scores = sem.qmatmul(split(q), np.swapaxes(split(k), -1, -2), ms, ss, fast=True)
     p = sem.softmax_lut(scores, lut, one, causal)

@@ -49,7 +49,7 @@ def test_wide_semantics_reduce_to_int8_forms():
     T, D = 4, 32
     x = RNG.integers(-128, 128, (5, T, D))
     w = RNG.integers(-128, 128, D)
-    lut, s = Q.rmsnorm_lut(0.03, 0.01, 0.02, int(np.abs(w).max()), D, 1e-6)
+    lut, s = Q.rsqrt_table(0.03, 0.01, 0.02, int(np.abs(w).max()), D, 1e-6)
     assert np.array_equal(sem.rmsnorm_wide(x, w, lut, 1, s), sem.rmsnorm_int(x, w, lut, 1, s))
     assert np.array_equal(sem.rmsnorm_wide(x, w, lut, 1, s, 0, 0, "i16"), sem.rmsnorm_int(x, w, lut, 1, s))
     a, b = RNG.integers(-128, 128, (2, 50))
@@ -73,7 +73,7 @@ def test_crafted_overflow_known_answer():
     x = np.full((4, 8), -128)
     assert Q.prove_no_overflow(_linear_graph(m_ok, 10))["y"] == acc * m_ok + (1 << 9)
     interp.run(_linear_graph(m_ok, 10), {"x": x})
-    with pytest.raises(OverflowError, match=r"y: acc\*M \+ round reaches"):
+    with pytest.raises(OverflowError, match=r"y: requant numerator can reach"):
         Q.prove_no_overflow(_linear_graph(m_ok + 1, 10))
     with pytest.raises(OverflowError):
         interp.run(_linear_graph(m_ok + 1, 10), {"x": x})
@@ -107,17 +107,17 @@ def test_overflow_proof_wide_chain():
     Q.prove_no_overflow(b.module(), {})
 
 
-def test_fixed_point_known_answers():
+def test_choose_shift_known_answers():
     """tests/frontend/test_quantize.py:36-42."""
     with pytest.raises(OverflowError):
-        Q.fixed_point([1.0], [1 << 31])
+        Q.choose_shift([1.0], [1 << 31])
     with pytest.raises(ValueError):
-        Q.fixed_point([1e-12, 1.0], [1 << 24, 1 << 24])
-    (m,), s = Q.fixed_point([0.37], [1 << 20], max_shift=12)
+        Q.choose_shift([1e-12, 1.0], [1 << 24, 1 << 24])
+    (m,), s = Q.choose_shift([0.37], [1 << 20], top=12)
     assert s == 12 and m == round(0.37 * 4096)
 
 
-def test_fixed_point_is_the_largest_admissible_shift():
+def test_choose_shift_is_the_largest_admissible_shift():
     """The defining property (quantize.py:40-56): the chosen s admits its multipliers, s + 1 does not."""
     rng = np.random.default_rng(3)
     for _ in range(300):
@@ -125,7 +125,7 @@ def test_fixed_point_is_the_largest_admissible_shift():
         bounds = [int(b) for b in rng.integers(0, 1 << 24, len(ms))]
         k = int(rng.integers(0, 5))
         try:
-            mi, s = Q.fixed_point(ms, bounds, k)
+            mi, s = Q.choose_shift(ms, bounds, k)
         except (ValueError, OverflowError):
             continue
 
@@ -137,12 +137,12 @@ def test_fixed_point_is_the_largest_admissible_shift():
         assert s == 31 - k or not fits(s + 1)
 
 
-def test_rsqrt_kmax_and_exp_bits():
-    """rsqrt_kmax(8) for 8 entries of magnitude 128: 8 * 2^14 = 2^17 needs 4 shifts by 2 to drop below 1024;
-    exp_bits is the largest E keeping (one + t//2) << E and t << E in int32 (quantize.py:155-157)."""
-    assert Q.rsqrt_kmax(8) == 4
+def test_loudest_row_steps_and_exp_shift():
+    """loudest_row_steps(8) for 8 entries of magnitude 128: 8 * 2^14 = 2^17 needs 4 shifts by 2 to drop below 1024;
+    exp_shift is the largest E keeping (one + t//2) << E and t << E in int32 (quantize.py:155-157)."""
+    assert Q.loudest_row_steps(8) == 4
     for t in range(1, 2049, 7):
-        e = Q.exp_bits(t)
+        e = Q.exp_shift(t)
         ok = lambda e_: ((127 + t // 2) << e_) <= (1 << 31) - 1 and (t << e_) <= (1 << 31) - 1   # noqa: E731
         assert ok(e) and not ok(e + 1)
 

@@ -51,7 +51,7 @@ def test_matmul_brute_force_and_fast_path():
 
 
 def test_softmax_is_round_half_up_of_the_exact_share():
-    lut = Q.exp_lut(0.07, 40)
+    lut = Q.exp_table(0.07, 40)
     for causal in (False, True):
         x = RNG.integers(-128, 128, (3, 40, 40))
         p = sem.softmax_lut(x, lut, 127, causal)
@@ -68,14 +68,14 @@ def test_softmax_is_round_half_up_of_the_exact_share():
 
 
 def test_softmax_closed_forms_and_mask():
-    lut = Q.exp_lut(0.05, 16)
+    lut = Q.exp_table(0.05, 16)
     E = int(lut[255])
     for n in range(1, 17):                       # a constant row of n kept entries: round half up of one / n
         p = sem.softmax_lut(np.full((1, n), 7), lut, 127, False)
         assert (p == int(np.floor(Fraction(127, n) + Fraction(1, 2)))).all()
     onehot = np.full((1, 16), -128)
     onehot[0, 5] = 127
-    sharp = Q.exp_lut(0.2, 16)                   # exp(-51) 2^23 rounds to 0: only the maximum survives
+    sharp = Q.exp_table(0.2, 16)                   # exp(-51) 2^23 rounds to 0: only the maximum survives
     assert sharp[0] == 0
     p = sem.softmax_lut(onehot, sharp, 127, False)
     assert p[0, 5] == 127 and p.sum() == 127
@@ -100,7 +100,7 @@ def test_rsqrt_index_characterisation():
 def test_rmsnorm_rational_form():
     d = 48
     w = RNG.integers(-127, 128, d)
-    lut, s = Q.rmsnorm_lut(0.02, 0.01, 0.03, int(np.abs(w).max()), d, 1e-5)
+    lut, s = Q.rsqrt_table(0.02, 0.01, 0.03, int(np.abs(w).max()), d, 1e-5)
     x = np.concatenate([RNG.integers(-128, 128, (20, d)), np.zeros((1, d), int), np.full((1, d), -128)])
     out = sem.rmsnorm_int(x, w, lut, 1, s)
     assert not out[20].any()                     # a zero row sums to 0 and maps to lut[0] = 0
