@@ -354,3 +354,35 @@ def config(n: int, stored: bool = True):
 
 def config_tag(n: int) -> int:
     return CONFIGS[n][1]
+
+
+# ------------------------------------------------------------------------------------- config 2: linear sweep
+
+LINEAR_SHAPES = [(m, k) for m in (256, 4096, 16384) for k in (768, 3072)]     # (M, K), N = K
+
+
+@dataclass
+class Linear:
+    """One int8 qlinear with a per-tensor requant: x (M, K) @ w (K, N), the standalone GEMM sweep."""
+    module: object
+    consts: dict
+    x: np.ndarray               # (M, K) int64 values in [-127, 127]
+    mult: int
+    shift: int
+
+
+def linear_config(M: int, K: int, N: int | None = None, tag: int = 2) -> Linear:
+    """Config 2 at one shape: x and w uniform integers in [-127, 127] (seeded by (tag, M, K, N)), and the requant
+    (mult, shift) = choose_shift([127 / (1.5 max|acc|)], [128 max_n sum_k |w[k, n]|]): the accumulator's largest
+    magnitude on these inputs maps to 127 / 1.5 (the quantizer's headroom), and the multiplier is safe for any int8
+    input, as the quantizer sizes a linear's (anvil/frontend/quantize.py:401-409)."""
+    N = K if N is None else N
+    rng = np.random.default_rng([tag, M, K, N])
+    x = rng.integers(-127, 128, (M, K))
+    w = rng.integers(-127, 128, (K, N))
+    acc_max = int(np.abs(x.astype(np.float64) @ w.astype(np.float64)).max())   # exact: |acc| < 2^53
+    (mult,), shift = Q.choose_shift([127 / (Q.HEADROOM * acc_max)], [128 * int(np.abs(w).sum(axis=0).max())])
+    b = g.GraphBuilder("linear")
+    y = b.qlinear("y", b.input("x", [M, K], "i8", 1.0), b.const("w", [K, N], "i8", 1.0), mult, shift, 1.0)
+    b.output(y)
+    return Linear(b.module(), {"w": w}, x, mult, shift)

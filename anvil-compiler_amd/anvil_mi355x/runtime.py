@@ -47,6 +47,7 @@ SIGNATURES = {
     "anvil_zero": [_p, _p, _sz],
     "anvil_event_record": [_p, _i],
     "anvil_event_elapsed": [_p, _i, _i, C.POINTER(C.c_float)],
+    "anvil_time_kernels": [_p, _i, _i],
     "anvil_gemm_i8": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i],
     "anvil_gemm_i8_ex": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _i],
     "anvil_gemm_i8_group": [_p, _p, _i],
@@ -183,6 +184,22 @@ class Device:
         ms = C.c_float()
         self.lib.call("anvil_event_elapsed", self.ctx, slot0, slot1, C.byref(ms))
         return float(ms.value)
+
+    def time_kernels(self, slot0: int, slot1: int):
+        """Arm the kernel-bound timer (anvil_time_kernels): the kernels launched until disarm() carry the events
+        of slot0 (first kernel's start) and slot1 (last kernel's end)."""
+        self.lib.call("anvil_time_kernels", self.ctx, slot0, slot1)
+
+    def disarm(self):
+        self.lib.call("anvil_time_kernels", self.ctx, -1, -1)
+
+    def timed(self, slot0: int, slot1: int, fn, *args):
+        """fn(*args) with its kernels bound to the events of slot0 and slot1."""
+        self.time_kernels(slot0, slot1)
+        try:
+            fn(*args)
+        finally:
+            self.disarm()
 
     def close(self):
         if self.ctx:

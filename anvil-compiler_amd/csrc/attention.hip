@@ -353,10 +353,10 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
 template <int NTW, bool S24>
 static void launch_attention(const AttnArgs& a, int D, unsigned grid, hipStream_t s) {
   switch (D) {
-    case 16: hipLaunchKernelGGL((attention_i8<NTW, 16, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
-    case 32: hipLaunchKernelGGL((attention_i8<NTW, 32, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((attention_i8<NTW, 64, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
-    default: hipLaunchKernelGGL((attention_i8<NTW, 128, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    case 16: ANVIL_LAUNCH((attention_i8<NTW, 16, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    case 32: ANVIL_LAUNCH((attention_i8<NTW, 32, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    case 64: ANVIL_LAUNCH((attention_i8<NTW, 64, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    default: ANVIL_LAUNCH((attention_i8<NTW, 128, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
   }
 }
 

@@ -1,6 +1,7 @@
 // Shared host and device helpers of the anvil_mi355x library (gfx950 only).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -41,6 +42,27 @@ int check_ctx(anvil_ctx* ctx);
   do {                                                         \
     hipError_t e_ = (call);                                    \
     if (e_ != hipSuccess) return ::anvil::hip_fail(e_, #call); \
+  } while (0)
+
+// Kernel timer (anvil_time_kernels): while armed for a stream, every launch on that stream carries the timer's
+// events, bound to the kernel itself (hipExtLaunchKernel): the start event to the first launch's start, the stop
+// event to each launch's end, so the pair spans the kernels and no dispatch gap or event packet.
+struct KernelTimer {
+  hipStream_t stream;
+  hipEvent_t start;   // cleared once the first timed launch has taken it
+  hipEvent_t stop;
+};
+extern __thread KernelTimer g_timer;   // zero-initialised per thread (a trivial type: no TLS init function)
+
+#define ANVIL_LAUNCH(kernel, grid, block, lds, strm_, ...)                                                  \
+  do {                                                                                                      \
+    if (::anvil::g_timer.stop && ::anvil::g_timer.stream == (strm_)) {                                      \
+      hipEvent_t start_ = ::anvil::g_timer.start;                                                           \
+      ::anvil::g_timer.start = nullptr;                                                                     \
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, strm_, start_, ::anvil::g_timer.stop, 0, __VA_ARGS__); \
+    } else {                                                                                                \
+      hipLaunchKernelGGL(kernel, grid, block, lds, strm_, __VA_ARGS__);                                     \
+    }                                                                                                       \
   } while (0)
 
 #define ANVIL_LAUNCHED()                                                      \

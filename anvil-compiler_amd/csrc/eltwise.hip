@@ -81,6 +81,22 @@ __global__ __launch_bounds__(E_THREADS) void copy_strided_kernel(CopyArgs c) {
   }
 }
 
+// A dense view (strides of a row-major array) with 16-byte-aligned ends is a plain byte copy: 16 bytes a lane,
+// four independent loads in flight per lane per pass.
+__global__ __launch_bounds__(E_THREADS) void copy_dense16_kernel(const uint4* __restrict__ s, uint4* __restrict__ d,
+                                                                 long long n16) {
+  const long long stride = (long long)gridDim.x * E_THREADS;
+  long long i = (long long)blockIdx.x * E_THREADS + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const uint4 v0 = s[i], v1 = s[i + stride], v2 = s[i + 2 * stride], v3 = s[i + 3 * stride];
+    d[i] = v0;
+    d[i + stride] = v1;
+    d[i + 2 * stride] = v2;
+    d[i + 3 * stride] = v3;
+  }
+  for (; i < n16; i += stride) d[i] = s[i];
+}
+
 // --------------------------------------------------------------------------------------------- quantize
 template <typename TI, typename TO>
 __global__ __launch_bounds__(E_THREADS) void quantize_kernel(const TI* __restrict__ x, double scale, long long n,
@@ -122,10 +138,10 @@ static void launch_add(anvil_ctx* ctx, const void* a, const void* b, int ma, int
                        int out_dtype) {
   const long long rnd = s ? (1ll << (s - 1)) : 0;
   if (out_dtype == ANVIL_I8)
-    hipLaunchKernelGGL((add_requant_kernel<TA, TB, int8_t>), dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream,
+    ANVIL_LAUNCH((add_requant_kernel<TA, TB, int8_t>), dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream,
                        (const TA*)a, (const TB*)b, ma, mb, s, rnd, n, (int8_t*)out, -128, 127, ctx->flags);
   else
-    hipLaunchKernelGGL((add_requant_kernel<TA, TB, int16_t>), dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream,
+    ANVIL_LAUNCH((add_requant_kernel<TA, TB, int16_t>), dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream,
                        (const TA*)a, (const TB*)b, ma, mb, s, rnd, n, (int16_t*)out, -32768, 32767, ctx->flags);
 }
 
@@ -162,7 +178,7 @@ int anvil_lut_i8(anvil_ctx* ctx, const int8_t* x, const int8_t* table, int64_t n
   if (!x || !table || !out) return set_error(ANVIL_E_VALUE, "anvil_lut_i8: null pointer");
   if (n < 0) return set_error(ANVIL_E_VALUE, "anvil_lut_i8: negative size");
   if (n == 0) return ANVIL_OK;
-  hipLaunchKernelGGL(lut_kernel, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, x, table, (long long)n, out);
+  ANVIL_LAUNCH(lut_kernel, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, x, table, (long long)n, out);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }
@@ -175,7 +191,7 @@ int anvil_lut_mul(anvil_ctx* ctx, const int8_t* x, const int8_t* y, const int8_t
   if (n < 0) return set_error(ANVIL_E_VALUE, "anvil_lut_mul: negative size");
   if (n == 0) return ANVIL_OK;
   const long long rnd = shift ? (1ll << (shift - 1)) : 0;
-  hipLaunchKernelGGL(lut_mul_kernel, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, x, y, table, mult, shift,
+  ANVIL_LAUNCH(lut_mul_kernel, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, x, y, table, mult, shift,
                      rnd, (long long)n, out, ctx->flags);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
@@ -197,15 +213,27 @@ int anvil_copy_strided(anvil_ctx* ctx, const void* src, void* dst, int elem_size
     c.strides[i] = src_strides[i];
     c.n *= dims[i];
   }
+  if (elem_size != 1 && elem_size != 2 && elem_size != 4)
+    return set_error(ANVIL_E_VALUE, "anvil_copy_strided: element size %d", elem_size);
+  bool dense = true;
+  for (long long i = rank - 1, want = 1; i >= 0; want *= c.dims[i], --i) dense &= c.dims[i] == 1 || c.strides[i] == want;
+  const long long bytes = c.n * elem_size;
+  if (dense && bytes % 16 == 0 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0) {
+    const long long n16 = bytes / 16;
+    ANVIL_LAUNCH(copy_dense16_kernel, dim3(grid_for(n16, 4)), dim3(E_THREADS), 0, ctx->stream,
+                 (const uint4*)src, (uint4*)dst, n16);
+    ANVIL_LAUNCHED();
+    return ANVIL_OK;
+  }
   switch (elem_size) {
     case 1:
-      hipLaunchKernelGGL(copy_strided_kernel<int8_t>, dim3(grid_for(c.n)), dim3(E_THREADS), 0, ctx->stream, c);
+      ANVIL_LAUNCH(copy_strided_kernel<int8_t>, dim3(grid_for(c.n)), dim3(E_THREADS), 0, ctx->stream, c);
       break;
     case 2:
-      hipLaunchKernelGGL(copy_strided_kernel<int16_t>, dim3(grid_for(c.n)), dim3(E_THREADS), 0, ctx->stream, c);
+      ANVIL_LAUNCH(copy_strided_kernel<int16_t>, dim3(grid_for(c.n)), dim3(E_THREADS), 0, ctx->stream, c);
       break;
     case 4:
-      hipLaunchKernelGGL(copy_strided_kernel<int32_t>, dim3(grid_for(c.n)), dim3(E_THREADS), 0, ctx->stream, c);
+      ANVIL_LAUNCH(copy_strided_kernel<int32_t>, dim3(grid_for(c.n)), dim3(E_THREADS), 0, ctx->stream, c);
       break;
     default:
       return set_error(ANVIL_E_VALUE, "anvil_copy_strided: element size %d", elem_size);
@@ -223,16 +251,16 @@ int anvil_quantize(anvil_ctx* ctx, const void* x, int x_is_f64, double scale, in
   const int lo = dtype_lo(out_dtype), hi = dtype_hi(out_dtype);
   dim3 gr(grid_for(n)), bl(E_THREADS);
   if (x_is_f64 && out_dtype == ANVIL_I8)
-    hipLaunchKernelGGL((quantize_kernel<double, int8_t>), gr, bl, 0, ctx->stream, (const double*)x, scale, (long long)n,
+    ANVIL_LAUNCH((quantize_kernel<double, int8_t>), gr, bl, 0, ctx->stream, (const double*)x, scale, (long long)n,
                        (int8_t*)out, lo, hi);
   else if (x_is_f64)
-    hipLaunchKernelGGL((quantize_kernel<double, int16_t>), gr, bl, 0, ctx->stream, (const double*)x, scale,
+    ANVIL_LAUNCH((quantize_kernel<double, int16_t>), gr, bl, 0, ctx->stream, (const double*)x, scale,
                        (long long)n, (int16_t*)out, lo, hi);
   else if (out_dtype == ANVIL_I8)
-    hipLaunchKernelGGL((quantize_kernel<float, int8_t>), gr, bl, 0, ctx->stream, (const float*)x, scale, (long long)n,
+    ANVIL_LAUNCH((quantize_kernel<float, int8_t>), gr, bl, 0, ctx->stream, (const float*)x, scale, (long long)n,
                        (int8_t*)out, lo, hi);
   else
-    hipLaunchKernelGGL((quantize_kernel<float, int16_t>), gr, bl, 0, ctx->stream, (const float*)x, scale,
+    ANVIL_LAUNCH((quantize_kernel<float, int16_t>), gr, bl, 0, ctx->stream, (const float*)x, scale,
                        (long long)n, (int16_t*)out, lo, hi);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
@@ -253,10 +281,10 @@ int anvil_embed_quantize(anvil_ctx* ctx, const int64_t* ids, int64_t rows, int T
   const long long n = rows * C;
   const int lo = dtype_lo(out_dtype), hi = dtype_hi(out_dtype);
   if (out_dtype == ANVIL_I8)
-    hipLaunchKernelGGL(embed_quantize_kernel<int8_t>, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, ids, wte, wpe,
+    ANVIL_LAUNCH(embed_quantize_kernel<int8_t>, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, ids, wte, wpe,
                        (long long)rows, T, C, vocab, scale, (int8_t*)out, lo, hi, ctx->flags);
   else
-    hipLaunchKernelGGL(embed_quantize_kernel<int16_t>, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, ids, wte,
+    ANVIL_LAUNCH(embed_quantize_kernel<int16_t>, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, ids, wte,
                        wpe, (long long)rows, T, C, vocab, scale, (int16_t*)out, lo, hi, ctx->flags);
   ANVIL_LAUNCHED();
   return ANVIL_OK;

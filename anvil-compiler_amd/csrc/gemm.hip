@@ -978,9 +978,9 @@ static void launch_persist(GemmArgs& g, int osz, int batch, int num_cu, hipStrea
   const int slots = 8 * ((num_cu * persist_occupancy<BM, BN, BK, NS>()) / 8);
   const int nwg = (int)std::min<long long>(slots, 8 * ((total + 7) / 8));
   if (osz == 1)
-    hipLaunchKernelGGL((gemm_i8_persist<BM, BN, BK, NS, NW, WGN, 1, MUL24>), dim3(nwg), dim3(NW * 64), 0, s, g);
+    ANVIL_LAUNCH((gemm_i8_persist<BM, BN, BK, NS, NW, WGN, 1, MUL24>), dim3(nwg), dim3(NW * 64), 0, s, g);
   else
-    hipLaunchKernelGGL((gemm_i8_persist<BM, BN, BK, NS, NW, WGN, 2, MUL24>), dim3(nwg), dim3(NW * 64), 0, s, g);
+    ANVIL_LAUNCH((gemm_i8_persist<BM, BN, BK, NS, NW, WGN, 2, MUL24>), dim3(nwg), dim3(NW * 64), 0, s, g);
 }
 
 template <int BM, int BN, int WGM, int NS, bool MUL24>
@@ -989,9 +989,9 @@ static void launch_fast(GemmArgs& g, int osz, int batch, hipStream_t s) {
   g.tiles_n = (g.N + BN - 1) / BN;
   dim3 grid(g.tiles_m * g.tiles_n, batch);
   if (osz == 1)
-    hipLaunchKernelGGL((gemm_i8_fast<BM, BN, WGM, NS, 1, MUL24>), grid, dim3(G_THREADS), 0, s, g);
+    ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 1, MUL24>), grid, dim3(G_THREADS), 0, s, g);
   else
-    hipLaunchKernelGGL((gemm_i8_fast<BM, BN, WGM, NS, 2, MUL24>), grid, dim3(G_THREADS), 0, s, g);
+    ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 2, MUL24>), grid, dim3(G_THREADS), 0, s, g);
 }
 
 template <int BM, int BN, int WGM, int NS, bool MUL24>
@@ -1010,9 +1010,9 @@ static bool launch_fast_group(GemmArgs* gs, const int* batch, int n, int osz, hi
   a.first[n] = (int)w;
   a.n = n;
   if (osz == 1)
-    hipLaunchKernelGGL((gemm_i8_fast_group<BM, BN, WGM, NS, 1, MUL24>), dim3((unsigned)w), dim3(G_THREADS), 0, s, a);
+    ANVIL_LAUNCH((gemm_i8_fast_group<BM, BN, WGM, NS, 1, MUL24>), dim3((unsigned)w), dim3(G_THREADS), 0, s, a);
   else
-    hipLaunchKernelGGL((gemm_i8_fast_group<BM, BN, WGM, NS, 2, MUL24>), dim3((unsigned)w), dim3(G_THREADS), 0, s, a);
+    ANVIL_LAUNCH((gemm_i8_fast_group<BM, BN, WGM, NS, 2, MUL24>), dim3((unsigned)w), dim3(G_THREADS), 0, s, a);
   return true;
 }
 
@@ -1069,14 +1069,14 @@ static void launch_cfg(GemmArgs& g, int osz, bool vec, int batch, hipStream_t s)
   dim3 grid(g.tiles_m * g.tiles_n, batch);
   if (osz == 1) {
     if (vec)
-      hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, WGM, PF, 1, CHECKED, true>), grid, dim3(G_THREADS), 0, s, g);
+      ANVIL_LAUNCH((gemm_i8_kernel<BM, BN, BK, WGM, PF, 1, CHECKED, true>), grid, dim3(G_THREADS), 0, s, g);
     else
-      hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, WGM, PF, 1, CHECKED, false>), grid, dim3(G_THREADS), 0, s, g);
+      ANVIL_LAUNCH((gemm_i8_kernel<BM, BN, BK, WGM, PF, 1, CHECKED, false>), grid, dim3(G_THREADS), 0, s, g);
   } else {
     if (vec)
-      hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, WGM, PF, 2, CHECKED, true>), grid, dim3(G_THREADS), 0, s, g);
+      ANVIL_LAUNCH((gemm_i8_kernel<BM, BN, BK, WGM, PF, 2, CHECKED, true>), grid, dim3(G_THREADS), 0, s, g);
     else
-      hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, WGM, PF, 2, CHECKED, false>), grid, dim3(G_THREADS), 0, s, g);
+      ANVIL_LAUNCH((gemm_i8_kernel<BM, BN, BK, WGM, PF, 2, CHECKED, false>), grid, dim3(G_THREADS), 0, s, g);
   }
 }
 

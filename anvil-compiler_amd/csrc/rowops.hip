@@ -524,7 +524,7 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
     const int ch = cols / 256;
     if ((flags & ANVIL_RMS_S24) && cols % 256 == 0 && ch <= 4) {      // rows of 256, 512, 768 or 1024 bytes
       auto launch = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len, mult,
+        ANVIL_LAUNCH(kernel, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len, mult,
                            shift, (long long)rows, out);
       };
       if (ch == 1) launch(rmsnorm_rows16<1>);
@@ -532,17 +532,17 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
       else if (ch == 3) launch(rmsnorm_rows16<3>);
       else launch(rmsnorm_rows16<4>);
     } else if (flags & ANVIL_RMS_S24)
-      hipLaunchKernelGGL(rmsnorm_fast<true>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
+      ANVIL_LAUNCH(rmsnorm_fast<true>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
                          mult, shift, (long long)rows, cols, out);
     else
-      hipLaunchKernelGGL(rmsnorm_fast<false>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
+      ANVIL_LAUNCH(rmsnorm_fast<false>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
                          mult, shift, (long long)rows, cols, out);
   } else if (x_dtype == ANVIL_I8) {
-    hipLaunchKernelGGL(rmsnorm_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
+    ANVIL_LAUNCH(rmsnorm_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
                        (const int8_t*)x, w, lut, lut_len, mult, shift, ss_shift, ss_init, (long long)rows, cols, out,
                        ctx->flags);
   } else {
-    hipLaunchKernelGGL(rmsnorm_kernel<int16_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
+    ANVIL_LAUNCH(rmsnorm_kernel<int16_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
                        (const int16_t*)x, w, lut, lut_len, mult, shift, ss_shift, ss_init, (long long)rows, cols,
                        out, ctx->flags);
   }
@@ -561,13 +561,13 @@ static void launch_softmax_fast(anvil_ctx* ctx, const int8_t* x, const int32_t* 
                                 long long rows, int t1, int t2, TO* out) {
   const unsigned grid = row_grid(rows, ctx->num_cu);
   if (t2 <= 1024)
-    hipLaunchKernelGGL((softmax_fast<1, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
+    ANVIL_LAUNCH((softmax_fast<1, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
                        t1, t2, out);
   else if (t2 <= 2048)
-    hipLaunchKernelGGL((softmax_fast<2, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
+    ANVIL_LAUNCH((softmax_fast<2, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
                        t1, t2, out);
   else
-    hipLaunchKernelGGL((softmax_fast<4, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
+    ANVIL_LAUNCH((softmax_fast<4, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
                        t1, t2, out);
 }
 
@@ -591,10 +591,10 @@ extern "C" int anvil_softmax_lut_ex(anvil_ctx* ctx, const int8_t* x, const int32
     else
       launch_softmax_fast<int32_t>(ctx, x, lut, one, causal, rows, t1, t2, (int32_t*)out);
   } else if (out_dtype == ANVIL_I8) {
-    hipLaunchKernelGGL(softmax_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream, x, lut, one,
+    ANVIL_LAUNCH(softmax_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream, x, lut, one,
                        causal, rows, t1, t2, (int8_t*)out, ctx->flags);
   } else {
-    hipLaunchKernelGGL(softmax_kernel<int32_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream, x, lut, one,
+    ANVIL_LAUNCH(softmax_kernel<int32_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream, x, lut, one,
                        causal, rows, t1, t2, (int32_t*)out, ctx->flags);
   }
   ANVIL_LAUNCHED();

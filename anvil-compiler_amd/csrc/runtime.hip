@@ -8,6 +8,7 @@
 namespace anvil {
 
 static thread_local std::string g_last_error;
+__thread KernelTimer g_timer;
 
 int set_error(int code, const char* fmt, ...) {
   char buf[1024];
@@ -83,6 +84,7 @@ int anvil_init(int device, anvil_ctx** out) {
 
 int anvil_destroy(anvil_ctx* ctx) {
   if (!ctx) return ANVIL_OK;
+  if (g_timer.stream == ctx->stream) g_timer = KernelTimer{};
   hipSetDevice(ctx->device);
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
   for (auto& ev : ctx->events)
@@ -146,7 +148,7 @@ int anvil_zero(anvil_ctx* ctx, void* dst, size_t bytes) {
   if (!dst) return set_error(ANVIL_E_VALUE, "anvil_zero: null pointer");
   size_t blocks = (bytes / 16 + 255) / 256;
   blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
-  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, (uint8_t*)dst, bytes);
+  ANVIL_LAUNCH(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, (uint8_t*)dst, bytes);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }
@@ -157,6 +159,21 @@ int anvil_event_record(anvil_ctx* ctx, int slot) {
   if (int r = check_ctx(ctx)) return r;
   if (!ctx->events[slot]) ANVIL_HIP(hipEventCreate(&ctx->events[slot]));
   ANVIL_HIP(hipEventRecord(ctx->events[slot], ctx->stream));
+  return ANVIL_OK;
+}
+
+int anvil_time_kernels(anvil_ctx* ctx, int slot0, int slot1) {
+  if (int r = check_ctx(ctx)) return r;
+  if (slot0 < 0 && slot1 < 0) {
+    if (g_timer.stream == ctx->stream) g_timer = KernelTimer{};
+    return ANVIL_OK;
+  }
+  if (slot0 < 0 || slot0 >= EVENT_SLOTS || slot1 < 0 || slot1 >= EVENT_SLOTS || slot0 == slot1)
+    return set_error(ANVIL_E_VALUE, "anvil_time_kernels: slots %d, %d must be two distinct slots in [0, %d)", slot0,
+                     slot1, EVENT_SLOTS);
+  for (int s : {slot0, slot1})
+    if (!ctx->events[s]) ANVIL_HIP(hipEventCreate(&ctx->events[s]));
+  g_timer = KernelTimer{ctx->stream, ctx->events[slot0], ctx->events[slot1]};
   return ANVIL_OK;
 }
 

@@ -7,15 +7,17 @@ Workload (default): config 5, the GPT-2-small-shaped int8 block (n_embd 768, 12 
 random-init N(0, 0.02) weights, N(0, 1) synthetic activations, per-tensor int8 calibrated on 8 seeded batches.
 A step is one forward of the block over the batch (every graph op on the GPU, graph outputs left in HBM); the
 quantized input is resident in HBM before the timed region. K steps are timed between two device synchronisations
-(host wall clock); the dominant kernel is bracketed by HIP events on the library's stream on every 10th timed step.
+(host wall clock). The dominant kernel's duration is measured inside the timed steps with HIP events bound to the
+kernel's own dispatch (hipExtLaunchKernel start / stop events), so it spans the kernel alone, like a rocprofv3
+kernel trace. --config 1, 3, 4 run the other blocks; --config 2 the standalone int8 linear sweep (six shapes, TOPS).
 
 Printed: one JSON line with the metric, the dominant kernel's roofline, a per-kernel breakdown from an untimed
-profiled pass, a stream-copy figure for the achievable HBM bandwidth, the PCIe-inclusive rate of `cm.run` on the host
-float input (never `value`), and the CPU baseline: this repo's literal numpy
-restatement of the reference interpreter (oracle/, int64 `@`, single-threaded per process) on P sequences of the
-same batch in P processes on this host's cores (exact, as batched evaluation equals per-sample evaluation), scaled
-to tokens/s. It runs before the GPU is first touched, so the worker processes are forked from a process with no
-GPU state.
+profiled pass (kernel-bound events again, so the figures add up to less than ms_per_step), a stream-copy figure for
+the achievable HBM bandwidth, the PCIe-inclusive rate of `cm.run` on the host float input (never `value`), and the
+CPU baseline: this repo's literal numpy restatement of the reference interpreter (oracle/, int64 `@`, single-threaded
+per process) on P sequences of the same batch in P processes on this host's cores (exact, as batched evaluation
+equals per-sample evaluation), scaled to tokens/s. It runs before the GPU is first touched, so the worker processes
+are forked from a process with no GPU state. The run exits non-zero when the GPU output differs from the CPU's.
 """
 import argparse
 import json
@@ -37,7 +39,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=5, choices=[1, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--keep", default="outputs", choices=["outputs", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -54,7 +56,66 @@ def main():
         sys.exit("bench.py: --steps must be >= 1 and --warmup >= 0")
     if args.copy_calibration:
         return copy_calibration()
+    line = bench_linear(args) if args.config == 2 else bench_block(args)
+    print(json.dumps(line), flush=True)
+    base = line.get("cpu_baseline") or {}
+    if base.get("matches_gpu_output") is False:
+        sys.exit("bench.py: the GPU output differs from the CPU baseline's on the sampled sequences")
 
+
+# Timing: every per-kernel figure comes from events bound to the kernels' own dispatch (anvil_time_kernels, through
+# hipExtLaunchKernel), so it spans the kernel alone, as a rocprofv3 kernel trace does, and no dispatch gap or event
+# packet. Slots 16 .. 16 + 2 * SLOTS hold the timed region's samples.
+SLOTS = 240
+
+
+def kernel_times(dev, steps, passes=3):
+    """Average device microseconds of each step's kernels over `passes` untimed passes."""
+    per = [0.0] * len(steps)
+    for _ in range(passes):
+        for i, (_, fn, a) in enumerate(steps):
+            dev.timed(16 + 2 * i, 17 + 2 * i, fn, *a)
+        dev.sync()
+        for i in range(len(steps)):
+            per[i] += 1e3 * dev.elapsed_ms(16 + 2 * i, 17 + 2 * i) / passes
+    return per
+
+
+def timed_steps(dev, steps, K, dom):
+    """K steps between device synchronisations (host wall clock); the kernels of step `dom` carry their own events
+    on every timed step (up to SLOTS of them, evenly spread). Returns (wall s, device ms, mean us of step dom)."""
+    every = max(1, -(-K // SLOTS))
+    dev.sync()
+    t0 = time.perf_counter()
+    dev.record(2)
+    n = 0
+    for k in range(K):
+        for i, (_, fn, a) in enumerate(steps):
+            if i == dom and k % every == 0 and n < SLOTS:
+                dev.timed(16 + 2 * n, 17 + 2 * n, fn, *a)
+                n += 1
+            else:
+                fn(*a)
+    dev.record(3)
+    dev.sync()
+    wall = time.perf_counter() - t0
+    dom_us = 1e3 * sum(dev.elapsed_ms(16 + 2 * j, 17 + 2 * j) for j in range(n)) / n
+    return wall, dev.elapsed_ms(2, 3), dom_us, n
+
+
+def roofline(kind, ops, nbytes, us, label, n):
+    if kind in ("gemm", "attention"):
+        achieved = ops / (us * 1e-6) / 1e12
+        return {"bound": "mfma", "kernel": label, "achieved": round(achieved, 1), "peak": round(PEAK_INT8_TOPS),
+                "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None, "algorithmic_ops": ops,
+                "avg_us": round(us, 2), "timed_launches": n}
+    achieved = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "kernel": label, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "algorithmic_bytes": nbytes,
+            "avg_us": round(us, 2), "timed_launches": n}
+
+
+def bench_block(args):
     import numpy as np
 
     import anvil_mi355x
@@ -69,7 +130,7 @@ def main():
     cpu, cpu_out = None, None
     if not args.no_cpu_baseline:
         cpu, cpu_out = cpu_baseline(built, xq, cm.outputs)
-    plan = cm.plan(nb)
+    plan = cm.plan(nb, args.keep)
     dev = cm.dev
     cm.upload_inputs(plan, {"x": xq})
     steps = plan.steps
@@ -77,86 +138,44 @@ def main():
     for _ in range(args.warmup):
         cm.launch(plan)
     dev.sync()
-
-    # untimed profiled pass: per-kernel device time, and the dominant kernel
-    per = [0.0] * len(steps)
-    passes = 3
-    for _ in range(passes):
-        for i, (_, fn, a) in enumerate(steps):
-            dev.record(0)
-            fn(*a)
-            dev.record(1)
-            per[i] += dev.elapsed_ms(0, 1) / passes
+    per = kernel_times(dev, steps)
     dom = max(range(len(steps)), key=lambda i: per[i])
-    dev.sync()
-
-    # timed region: K steps between device synchronisations; HIP events around the dominant kernel on every
-    # `every`-th step (an event pair on every step costs about 3 us a step, 0.8 %)
     K = args.steps
-    every = max(1, K // 30)
-    slots = min((K + every - 1) // every, 250)
-    dev.sync()
-    t0 = time.perf_counter()
-    dev.record(2)
-    for k in range(K):
-        for i, (_, fn, a) in enumerate(steps):
-            if i == dom and k % every == 0 and k // every < slots:
-                dev.record(10 + 2 * (k // every))
-                fn(*a)
-                dev.record(11 + 2 * (k // every))
-            else:
-                fn(*a)
-    dev.record(3)
-    dev.sync()
-    t1 = time.perf_counter()
-    wall_s = t1 - t0
-    device_ms = dev.elapsed_ms(2, 3)
-    dom_ms = sum(dev.elapsed_ms(10 + 2 * s, 11 + 2 * s) for s in range(slots)) / slots
-    tokens = nb * spec.seq * K
-    value = tokens / wall_s
+    wall_s, device_ms, dom_us, n = timed_steps(dev, steps, K, dom)
+    value = nb * spec.seq * K / wall_s
 
     kind, ops, nbytes = plan.works[dom]
-    if kind in ("gemm", "attention"):
-        achieved = ops / (dom_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "kernel": steps[dom][0], "achieved": round(achieved, 1), "peak": round(PEAK_INT8_TOPS),
-                "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
-                "algorithmic_ops": ops, "avg_us": round(dom_ms * 1e3, 2), "timed_launches": slots}
-    else:
-        achieved = nbytes / (dom_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "kernel": steps[dom][0], "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                "algorithmic_bytes": nbytes, "avg_us": round(dom_ms * 1e3, 2), "timed_launches": slots}
-
+    roof = roofline(kind, ops, nbytes, dom_us, steps[dom][0], n)
     roof["traffic"], src = measured_traffic(args.config, args.keep, steps[dom][0])
     if src:
         roof["traffic_source"] = src
 
-    kernels, g_ops, g_ms = {}, 0, 0.0
+    kernels, g_ops, g_us = {}, 0, 0.0
     for i, (label, _, _) in enumerate(steps):
         k_, o_, b_ = plan.works[i]
-        ms = per[i]
-        e = {"kind": k_, "us": round(ms * 1e3, 2)}
+        us = per[i]
+        e = {"kind": k_, "us": round(us, 2)}
         if k_ in ("gemm", "attention"):
-            e["TOPS"] = round(o_ / (ms * 1e-3) / 1e12, 1)
+            e["TOPS"] = round(o_ / (us * 1e-6) / 1e12, 1)
             e["frac_mfma"] = round(e["TOPS"] / PEAK_INT8_TOPS, 4)
             if k_ == "attention":                 # MFMA work actually issued: 32-key tiles up to the diagonal
                 e["executed_ops"] = attention_executed_ops(steps[i][2])
-                e["GBs"] = round(b_ / (ms * 1e-3) / 1e9, 1)
+                e["GBs"] = round(b_ / (us * 1e-6) / 1e9, 1)
             g_ops += o_
-            g_ms += ms
+            g_us += us
         else:
-            e["GBs"] = round(b_ / (ms * 1e-3) / 1e9, 1)
+            e["GBs"] = round(b_ / (us * 1e-6) / 1e9, 1)
             e["frac_hbm"] = round(e["GBs"] / PEAK_HBM_GBS, 4)
         kernels[label] = e
-    gemm_tops = g_ops / (g_ms * 1e-3) / 1e12 if g_ms else 0.0
+    gemm_tops = g_ops / (g_us * 1e-6) / 1e12 if g_us else 0.0
 
     if cpu is not None:
         got = cm.read(plan, cm.outputs)
         cpu["matches_gpu_output"] = all(np.array_equal(got[s][i:i + 1], o[s]) for i, o in cpu_out.items() for s in o)
-    e2e = end_to_end(cm, x, nb, spec.seq)
+    e2e = end_to_end(cm, x, nb, spec.seq, args.keep)
     stream = stream_copy(dev)
 
-    line = {
+    return {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(wall_s / K * 1e3, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
@@ -167,18 +186,80 @@ def main():
                    "layers": spec.layers},
         "device_ms_per_step": round(device_ms / K, 4),
         "gemm": {"TOPS": round(gemm_tops, 1), "frac_of_peak": round(gemm_tops / PEAK_INT8_TOPS, 4),
-                 "ops_per_step": g_ops, "us_per_step": round(g_ms * 1e3, 2),
-                 "covers": "every qlinear/qmatmul of the step at 2 M N K ops (attention dense T x T); the fused "
-                           "attention kernel's time, softmax included, counts as GEMM time"},
+                 "ops_per_step": g_ops, "us_per_step": round(g_us, 2),
+                 "covers": "every qlinear/qmatmul of the step at 2 M N K ops (attention dense T x T) over the kernel "
+                           "times below; the fused attention kernel's time, softmax included, counts as GEMM time"},
         "roofline": roof,
         "hbm_stream": stream,
         "end_to_end": e2e,
         "kernels": kernels,
-        "kernels_note": "per launch, HIP events around each kernel in an untimed pass of 3 steps (each figure includes "
-                        "the dispatch gap before its kernel); the timed figures are value and roofline.avg_us",
+        "kernels_us_sum": round(sum(per), 2),
+        "kernels_note": "per launch, device time of each step's kernels alone (events bound to the kernels' dispatch, "
+                        "hipExtLaunchKernel), mean of 3 untimed passes; ms_per_step adds the launch gaps",
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+
+
+def bench_linear(args):
+    """Config 2: the six int8 linear + requant shapes, each one qlinear graph compiled and run on its fast kernel. A
+    step runs the six GEMMs once each; value is their total ops over the timed steps' wall time."""
+    import numpy as np
+
+    import anvil_mi355x
+    from anvil_mi355x import models
+
+    lins = [models.linear_config(M, K) for M, K in models.LINEAR_SHAPES]
+    cpu = cpu_out = None
+    if not args.no_cpu_baseline:             # forked workers, before this process first touches the GPU
+        cpu, cpu_out = linear_cpu_baseline(lins)
+    cases = []
+    for (M, K), lin in zip(models.LINEAR_SHAPES, lins):
+        cm = anvil_mi355x.compile((lin.module, lin.consts))
+        plan = cm.plan(1)
+        cm.upload_inputs(plan, {"x": lin.x})
+        cases.append((M, K, lin, cm, plan))
+    dev = cases[0][3].dev
+    steps = [st for *_, plan in cases for st in plan.steps]
+    works = [w for *_, plan in cases for w in plan.works]
+    for _ in range(args.warmup):
+        for _, fn, a in steps:
+            fn(*a)
+    dev.sync()
+    per = kernel_times(dev, steps)
+    dom = max(range(len(steps)), key=lambda i: works[i][1])
+    K_ = args.steps
+    wall_s, device_ms, dom_us, n = timed_steps(dev, steps, K_, dom)
+    total_ops = sum(w[1] for w in works)
+    value = total_ops * K_ / wall_s / 1e12
+    shapes = {}
+    for (M, K, lin, cm, plan), us, (_, ops, nbytes) in zip(cases, per, works):
+        shapes[f"{M}x{K}x{K}"] = {
+            "us": round(us, 2), "TOPS": round(ops / (us * 1e-6) / 1e12, 1),
+            "frac_mfma": round(ops / (us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4),
+            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1), "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "ops": ops, "bytes": nbytes, "mult": lin.mult, "shift": lin.shift}
+    roof = roofline("gemm", works[dom][1], works[dom][2], dom_us, "y " + list(shapes)[dom], n)
+    if cpu is not None:
+        got = [cm.read(plan, ["y"], batch=False)["y"] for *_, cm, plan in cases]
+        cpu["matches_gpu_output"] = linear_matches(lins, got, cpu_out)
+    return {
+        "metric": METRIC, "value": round(value, 1), "unit": "TOPS", "n_gpus": 1, "steps": K_,
+        "warmup": args.warmup, "ms_per_step": round(wall_s / K_ * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "config2: int8 linear + per-tensor requant, A[M,K] x W[K,N], M in {256, 4096, 16384}, "
+                               "K = N in {768, 3072}, uniform int8 in [-127, 127]; a step = the six GEMMs once",
+                   "shapes": list(shapes)},
+        "device_ms_per_step": round(device_ms / K_, 4),
+        "gemm": {"TOPS": round(total_ops / (sum(per) * 1e-6) / 1e12, 1),
+                 "frac_of_peak": round(total_ops / (sum(per) * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4),
+                 "ops_per_step": total_ops, "us_per_step": round(sum(per), 2)},
+        "roofline": roof,
+        "shapes": shapes,
+        "kernels_note": "per shape, device time of its kernel alone (events bound to the kernel's dispatch), mean of "
+                        "3 untimed passes; M = 256 sits below the ridge (about 630 ops/byte), so frac_hbm is its "
+                        "second bound",
+        "cpu_baseline": cpu,
+    }
 
 
 def measured_traffic(config, keep, label):
@@ -259,38 +340,79 @@ def cpu_baseline(built, xq, outs):
     return rec, {i: o for i, _, o in res}
 
 
-def end_to_end(cm, x, nb, seq, calls=3):
+def end_to_end(cm, x, nb, seq, keep, calls=3):
     """The PCIe-inclusive rate, never `value`: cm.run on the host float input (upload, quantize on the device, the
-    forward, download of the int8 output and its float64 dequantization on the host), one untimed call then `calls`
-    timed ones."""
-    cm.run(x, batch=True)
+    forward, download of what `keep` returns and its float64 dequantization on the host), one untimed call then
+    `calls` timed ones."""
+    cm.run(x, batch=True, keep=keep)
     t0 = time.perf_counter()
     for _ in range(calls):
-        cm.run(x, batch=True)
+        cm.run(x, batch=True, keep=keep)
     dt = (time.perf_counter() - t0) / calls
     return {"tokens_s": round(nb * seq / dt, 1), "ms_per_call": round(dt * 1e3, 2), "calls": calls,
-            "input_bytes": int(x.nbytes), "covers": "cm.run(x, batch=True): float input upload, device quantize, "
-                                                    "forward, output download and host dequantize"}
+            "input_bytes": int(x.nbytes), "covers": f"cm.run(x, batch=True, keep={keep!r}): float input upload, device "
+                                                    "quantize, forward, download and host dequantize"}
 
 
 def stream_copy(dev):
-    """Achievable HBM bandwidth beside the 8 TB/s peak: a contiguous 1 GiB device copy on the library's copy kernel
-    (4-byte elements), 3 timed launches."""
+    """Achievable HBM bandwidth beside the 8 TB/s peak: a contiguous 1 GiB device copy on the library's dense copy
+    kernel (16 bytes a lane), 3 launches timed on the kernels alone."""
     n = 1 << 30
     src, dst = dev.alloc(n), dev.alloc(n)
     dev.zero(src, n)
     dev.copy_strided(src, dst, 4, [n // 4], [1])
     dev.sync()
-    dev.record(0)
+    ms = []
     for _ in range(3):
-        dev.copy_strided(src, dst, 4, [n // 4], [1])
-    dev.record(1)
-    dev.sync()
-    ms = dev.elapsed_ms(0, 1) / 3
+        dev.timed(6, 7, dev.copy_strided, src, dst, 4, [n // 4], [1])
+        dev.sync()
+        ms.append(dev.elapsed_ms(6, 7))
     src.free()
     dst.free()
+    ms = sum(ms) / len(ms)
     return {"GBs": round(2 * n / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
-            "kernel": "copy_strided_kernel<int>: 1 GiB read + 1 GiB written per launch"}
+            "kernel": "copy_dense16_kernel: 1 GiB read + 1 GiB written per launch, 16 bytes a lane"}
+
+
+def _cpu_linear(i):
+    """Sample rows of linear shape i through the literal int64 path (numpy `@`, one core): (i, rows, seconds, out)."""
+    from oracle import semantics as sem
+    lin, rows = _CPU["lins"][i], _CPU["rows"][i]
+    t0 = time.perf_counter()
+    out = sem.qmatmul(lin.x[:rows], lin.consts["w"], lin.mult, lin.shift)
+    return i, rows, time.perf_counter() - t0, out
+
+
+def linear_cpu_baseline(lins):
+    """The literal numpy path of the reference's qmatmul (int64 `@`, anvil/semantics.py:95-103) on a bounded sample of
+    rows of each config-2 shape (about 4e8 multiply-adds each), one process per shape. Returns the record and the
+    sampled outputs, which linear_matches compares with the GPU's."""
+    import multiprocessing as mp
+    rows = [max(8, min(len(lin.x), int(4e8 // (lin.x.shape[1] * lin.consts["w"].shape[1])))) for lin in lins]
+    _CPU.update(lins=lins, rows=rows)
+    t0 = time.perf_counter()
+    with mp.get_context("fork").Pool(len(lins)) as pool:
+        res = pool.map(_cpu_linear, range(len(lins)))
+    wall = time.perf_counter() - t0
+    ops = sum(2 * r * lin.x.shape[1] * lin.consts["w"].shape[1] for lin, r in zip(lins, rows))
+    rec = {"value": round(ops / wall / 1e12, 6), "unit": "TOPS", "cores": len(lins), "kind": "port",
+           "sample": f"rows {rows} of the six shapes (in order), one process per shape, literal int64 numpy path, "
+                     f"{wall:.1f} s wall; host os.cpu_count()={os.cpu_count()}",
+           "per_shape_GMACs": [round(r * lin.x.shape[1] * lin.consts["w"].shape[1] / dt / 1e9, 3)
+                               for lin, (_, r, dt, _) in zip(lins, res)],
+           "seconds": round(wall, 2),
+           "full_output_checked": "every element of the six GPU outputs against the float64-BLAS oracle"}
+    return rec, [out for *_, out in res]
+
+
+def linear_matches(lins, got, sampled):
+    """The GPU outputs equal the literal path's sampled rows, and in full the float64-BLAS oracle (exact here)."""
+    import numpy as np
+
+    from oracle import semantics as sem
+    return bool(all(np.array_equal(g_[:len(o)], o) for g_, o in zip(got, sampled)) and
+                all(np.array_equal(g_, sem.qmatmul(lin.x, lin.consts["w"], lin.mult, lin.shift, fast=True))
+                    for lin, g_ in zip(lins, got)))
 
 
 if __name__ == "__main__":

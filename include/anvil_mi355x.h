@@ -61,6 +61,12 @@ int anvil_zero(anvil_ctx* ctx, void* dst, size_t bytes);
 /* Events on the context's stream, in 512 slots: record two, then read the elapsed milliseconds between them. */
 int anvil_event_record(anvil_ctx* ctx, int slot);
 int anvil_event_elapsed(anvil_ctx* ctx, int slot0, int slot1, float* ms);
+/* Kernel-bound timing (no reference counterpart: the reference times ops in simulator cycles, anvil/driver.py:
+ * 313-319). Until disarmed, the kernels this host thread launches on the context's stream carry the events of
+ * slot0 and slot1 inside their dispatch (hipExtLaunchKernel): slot0 marks the first such kernel's start, slot1 the
+ * last one's end, so anvil_event_elapsed(slot0, slot1) spans the kernels alone, without the dispatch gap or event
+ * packets that anvil_event_record brackets. anvil_time_kernels(ctx, -1, -1) disarms. */
+int anvil_time_kernels(anvil_ctx* ctx, int slot0, int slot1);
 
 /* ------------------------------------------------------------------------------------------------ ops */
 

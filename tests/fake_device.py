@@ -79,6 +79,11 @@ class FakeDevice:
     def record(self, slot):
         pass
 
+    def timed(self, slot0, slot1, fn, *args):
+        self.record(slot0)
+        fn(*args)
+        self.record(slot1)
+
     def elapsed_ms(self, a, b):
         return 0.0
 

@@ -125,3 +125,23 @@ def test_wide_row_bound_is_tight_by_brute_force():
     assert max(row.xmax) == max(k for k, _ in seen)
     for k, col in row.xmax.items():
         assert col.max() == max(x for (kk, _), x in seen.items() if kk == k)
+
+
+def test_block_digest_fixture_matches_the_oracle():
+    """The committed per-sequence digests (tests/golden/block_digests.json) are the oracle's on the current graphs:
+    config 1 in full, and the first and last sequence of config 3."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import make_block_digests as mk
+    from oracle import interp
+    gold = json.loads((Path(__file__).resolve().parent / "golden" / "block_digests.json").read_text())
+    for n, seqs in ((1, [0]), (3, [0, 63])):
+        built, cm, xq = mk.config_inputs(n)
+        g = gold["configs"][str(n)]
+        assert g["constants_sha256"] == CONSTANTS_SHA256[n] and g["batch"] == len(xq)
+        syms = mk.graph_values(built)
+        assert [s for s, _ in syms] == g["values"]
+        for i in seqs:
+            r = interp.run(built.module, {"x": xq[i:i + 1]}, built.consts, batch=True, fast=True)
+            assert {s: mk.value_digest(r.values[s][0], dt) for s, dt in syms} == g["sequences"][i]
