@@ -38,7 +38,8 @@ class FakeBuffer:
 
 
 class FakeDevice:
-    def __init__(self, heap_bytes=1 << 28):
+    def __init__(self, heap_bytes=1 << 28, fast=False):
+        self.fast = fast             # matmuls in float64 BLAS (exact for int8 operands), for large graphs
         self.heap = np.zeros(heap_bytes, dtype=np.uint8)
         self.top = 0
         self.lock = threading.Lock()
@@ -102,7 +103,8 @@ class FakeDevice:
         a = self.view(A, "i8", (b0, b1, M, K), (sa0, sa1, lda, 1)).astype(np.int64)
         bt = self.view(Bt, "i8", (b0, b1, N, K), (sb0, sb1, ldb, 1)).astype(np.int64)
         lt = None if lut is None else self.view(lut, "i8", (256,), (1,)).astype(np.int64)
-        out = self._guard(lambda: sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, out_dtype))
+        out = self._guard(lambda: sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, out_dtype,
+                                                      fast=self.fast))
         if out is not None:
             self.store(Cp, out_dtype, (b0, b1, M, N), (sc0, sc1, ldc, 1), out)
 
@@ -144,7 +146,7 @@ class FakeDevice:
         r = self.view(R, "i8", (b0, b1, M, N), (sr0, sr1, ldr, 1)).astype(np.int64)
 
         def both():
-            y = sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, "i8")
+            y = sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, "i8", fast=self.fast)
             return y, sem.add_requant(r, y, ma, mb, shift2, "i8")
         out = self._guard(both)
         if out is not None:
@@ -162,9 +164,9 @@ class FakeDevice:
         lv = self.view(lut, "i32", (256,), (1,)).astype(np.int64)
 
         def chain():
-            scores = sem.qmatmul(q, np.swapaxes(k, -1, -2), ms, ss)
+            scores = sem.qmatmul(q, np.swapaxes(k, -1, -2), ms, ss, fast=self.fast)
             p = sem.softmax_lut(scores, lv, one, causal)
-            return sem.qmatmul(p, np.swapaxes(vt, -1, -2), mo, so)
+            return sem.qmatmul(p, np.swapaxes(vt, -1, -2), mo, so, fast=self.fast)
         r = self._guard(chain)
         if r is not None:
             self.store(O, "i8", (b0, b1, T, D), (st[9], st[10], st[11], 1), r)
