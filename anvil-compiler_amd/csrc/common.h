@@ -30,6 +30,9 @@ struct anvil_ctx {
   hipEvent_t events[EVENT_SLOTS] = {};   // created on first use of a slot
   int num_cu = 0;
   int gemm_cfg = 0;               // ANVIL_GEMM_CFG at init: pins one GEMM tile shape (benchmarking); 0 = by problem
+  // split-K workspace of anvil_gemm_i8_ex (int32 partial tiles), allocated on first use and grown as needed
+  int* ws = nullptr;
+  long long ws_elems = 0;
 };
 
 namespace anvil {
@@ -37,6 +40,8 @@ namespace anvil {
 int set_error(int code, const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
 int check_ctx(anvil_ctx* ctx);
+// zero `bytes` of device memory with a fill kernel on stream s (no memset node: safe inside a captured graph)
+int zero_fill(hipStream_t s, void* dst, size_t bytes);
 
 #define ANVIL_HIP(call)                                        \
   do {                                                         \

@@ -55,6 +55,10 @@ struct GemmArgs {
   int ma, mb, shift2, rnd2;
   int res, store_y, vec_res;
   int nbatch;                     // batch0 * batch1 (persistent kernel)
+  // split-K (fast kernel, batch 1): workgroup (tile, z) stores the int32 sums of K bytes [z kchunk, (z + 1) kchunk)
+  // as partial tile (tile, z) of ws; splitk_reduce adds the partial tiles up
+  int* ws;
+  int kchunk, splits;
 };
 
 constexpr int G_THREADS = 256;
@@ -433,7 +437,11 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
 
 // One output tile of the fast kernel: logical tile pid of batch entry bz (the XCD remap below assumes pid and the
 // workgroup id agree modulo 8).
-template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24>
+template <int BM, int BN, int WM, int WN, int TM, int TN, int OSZ, bool MUL24>
+__device__ void splitk_finish(const GemmArgs& g, const v16i (&acc)[TN][TM], const int8_t* lut_s, int tile, int m0,
+                              int n0, int mrow, int ncol);
+
+template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool SPLIT = false>
 __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int bz) {
   constexpr int BK = 64, CPR = BK / 16;
   constexpr int WGN = 4 / WGM;
@@ -469,11 +477,13 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
   const int m0 = tile_m * BM, n0 = tile_n * BN;
   if (g.causal == 1 && n0 > m0 + BM - 1) return;
 
-  const int b0 = bz / g.batch1, b1 = bz % g.batch1;
-  const int8_t* Ab = g.A + b0 * g.sa0 + b1 * g.sa1 + (long long)m0 * g.lda;
-  const int8_t* Bb = g.B + b0 * g.sb0 + b1 * g.sb1 + (long long)n0 * g.ldb;
+  // split-K: bz is the K chunk (the batch is 1), and the chunk's first byte becomes the operands' K origin
+  const int b0 = SPLIT ? 0 : bz / g.batch1, b1 = SPLIT ? 0 : bz % g.batch1;
+  const int kbeg = SPLIT ? bz * g.kchunk : 0;
+  const int8_t* Ab = g.A + b0 * g.sa0 + b1 * g.sa1 + (long long)m0 * g.lda + kbeg;
+  const int8_t* Bb = g.B + b0 * g.sb0 + b1 * g.sb1 + (long long)n0 * g.ldb + kbeg;
   const int rows_a = min(g.M - m0, BM), rows_b = min(g.N - n0, BN);
-  const int K = g.causal == 2 ? min(g.K, m0 + BM) : g.K;
+  const int K = SPLIT ? min(g.K - kbeg, g.kchunk) : (g.causal == 2 ? min(g.K, m0 + BM) : g.K);
   const __amdgpu_buffer_rsrc_t ra = uniform_rsrc(Ab, (int)(rows_a * g.lda));
   const __amdgpu_buffer_rsrc_t rb = uniform_rsrc(Bb, (int)(rows_b * g.ldb));
 
@@ -584,6 +594,11 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
     if (kt < nk) step(kt, L0, L3, L1);
     if (kt + 1 < nk) step(kt + 1, L1, L0, L2);
     if (kt + 2 < nk) step(kt + 2, L2, L1, L3);
+  }
+  if constexpr (SPLIT) {
+    splitk_finish<BM, BN, WM, WN, TM, TN, OSZ, MUL24>(g, acc, lut_s, tile_m * g.tiles_n + tile_n, m0, n0,
+                                                      wm * WM + l32, wn * WN + 4 * half);
+    return;
   }
 
   // the staged tile leaves in 16-byte chunks, chunk idx = t + pass * G_THREADS of the tile: row idx / CH_ROW,
@@ -760,6 +775,74 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
         }
     }
   }
+}
+
+// Split-K end of a tile: this K chunk's int32 accumulators become partial tile (tile, chunk) of ws, BM x BN
+// row-major, with plain 16-byte stores; splitk_reduce sums a tile's chunks in the next launch (the kernel boundary
+// is the only synchronisation). Accumulator r of lane l in tile (i, j) is tile row mrow + 32 j, column
+// ncol + 32 i + 8 (r / 4) + r % 4 (mrow, ncol relative to the tile).
+template <int BM, int BN, int WM, int WN, int TM, int TN, int OSZ, bool MUL24>
+__device__ void splitk_finish(const GemmArgs& g, const v16i (&acc)[TN][TM], const int8_t* lut_s, int tile, int m0,
+                              int n0, int mrow, int ncol) {
+  int* part = g.ws + ((long long)tile * g.splits + blockIdx.y) * (BM * BN);
+#pragma unroll
+  for (int j = 0; j < TM; ++j)
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<v4i*>(part + (mrow + 32 * j) * BN + ncol + 32 * i + 8 * q) =
+            v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+  wait_vmcnt(0);                                         // trailing zero-fill stage loads land before exit
+}
+
+// The second launch of a split-K product: workgroup (tile, band) sums the g.splits partial tiles of 16 rows of one
+// 128 x 128 output tile, four consecutive sums a thread, and requantizes (+ LUT) them into C.
+template <int OSZ, bool MUL24>
+__global__ __launch_bounds__(G_THREADS) void splitk_reduce(GemmArgs g) {
+  constexpr int T = 128, BAND = 16;
+  __shared__ int8_t lut_s[256];
+  const int tile = blockIdx.x / (T / BAND), band = blockIdx.x % (T / BAND);
+  const int tm = tile / g.tiles_n, tn = tile % g.tiles_n;
+  const bool lut = OSZ == 1 && g.lut;
+  if (lut) lut_s[threadIdx.x] = g.lut[threadIdx.x];
+  __syncthreads();
+  const int rr = band * BAND + threadIdx.x / 32 * 2, c4 = threadIdx.x % 32 * 4;
+  const int lo = OSZ == 1 ? -128 : -32768, hi = OSZ == 1 ? 127 : 32767;
+  const int* tp = g.ws + (long long)tile * g.splits * (T * T);
+  char* Cb = reinterpret_cast<char*>(g.C);
+  const int n = tn * T + c4;
+  if (n >= g.N) return;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {                          // two rows a thread
+    const int m = tm * T + rr + h;
+    if (m >= g.M) break;
+    v4i a = *reinterpret_cast<const v4i*>(tp + (rr + h) * T + c4);
+    for (int z = 1; z < g.splits; ++z) a += *reinterpret_cast<const v4i*>(tp + (long long)z * (T * T) + (rr + h) * T + c4);
+    int v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int x = MUL24 ? (__mul24(a[e], g.mult) + g.rnd) : (a[e] * g.mult + g.rnd);
+      v[e] = min(max(x >> g.shift, lo), hi);
+      if (lut) v[e] = lut_s[v[e] + 128];
+    }
+    char* c = Cb + ((long long)m * g.ldc + n) * OSZ;
+    if (OSZ == 1 && g.vec_store && n + 3 < g.N) {
+      *reinterpret_cast<unsigned*>(c) = pack4(v[0], v[1], v[2], v[3]);
+    } else {
+      for (int e = 0; e < 4 && n + e < g.N; ++e) {
+        if (OSZ == 1)
+          c[e] = (char)v[e];
+        else
+          reinterpret_cast<int16_t*>(c)[e] = (int16_t)v[e];
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24>
+__global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8_splitk(GemmArgs g) {
+  fast_tile<BM, BN, WGM, NS, OSZ, MUL24, true>(g, blockIdx.x, blockIdx.y);
 }
 
 template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24>
@@ -1016,6 +1099,41 @@ static bool launch_fast_group(GemmArgs* gs, const int* batch, int n, int osz, hi
   return true;
 }
 
+constexpr int SPLITK_MAX = 4;                             // K chunks of one product (partial tiles kept per tile)
+
+// Split-K on 128 x 128 tiles (three LDS stages, three workgroups per CU): grid (tiles, splits) storing partial
+// tiles, then the reduction, eight workgroups per tile.
+template <bool MUL24>
+static void launch_splitk(GemmArgs& g, int osz, hipStream_t s) {
+  g.tiles_m = (g.M + 127) / 128;
+  g.tiles_n = (g.N + 127) / 128;
+  dim3 grid(g.tiles_m * g.tiles_n, g.splits);
+  const dim3 rgrid(g.tiles_m * g.tiles_n * 8);
+  if (osz == 1) {
+    ANVIL_LAUNCH((gemm_i8_splitk<128, 128, 2, 3, 1, MUL24>), grid, dim3(G_THREADS), 0, s, g);
+    ANVIL_LAUNCH((splitk_reduce<1, MUL24>), rgrid, dim3(G_THREADS), 0, s, g);
+  } else {
+    ANVIL_LAUNCH((gemm_i8_splitk<128, 128, 2, 3, 2, MUL24>), grid, dim3(G_THREADS), 0, s, g);
+    ANVIL_LAUNCH((splitk_reduce<2, MUL24>), rgrid, dim3(G_THREADS), 0, s, g);
+  }
+}
+
+// Whether a fast-path product splits K, and into how many chunks: a single product (batch 1, no causal mode or fused
+// add) with K >= 2048 whose 128 x 128 output tiles fill at most a quarter of the CUs splits into two to SPLITK_MAX
+// chunks of whole 64-byte K blocks; `force` (ANVIL_GEMM_SPLITK) splits any such product. Measured on MI355X (two
+// launches, partial tiles through the workspace): 256 x 3072 x 3072 (48 tiles) 22.1 -> 17.8 us; at K = 768
+// (256 x 768 x 768, 12 tiles) the second launch costs more than the split saves, 11.4 -> 13.3 us.
+static bool splitk_plan(const GemmArgs& g, int batch, int num_cu, bool force, int& splits, int& kchunk) {
+  if (batch != 1 || g.causal != 0 || g.res) return false;
+  const long long tiles = (long long)((g.M + 127) / 128) * ((g.N + 127) / 128);
+  if (!force && (tiles * 4 > num_cu || g.K < 2048)) return false;
+  long long want = std::max<long long>(2, (2ll * num_cu + tiles - 1) / tiles);
+  want = std::min<long long>(std::min<long long>(want, SPLITK_MAX), std::max(1, g.K / 128));
+  kchunk = (int)(((g.K + want - 1) / want + 63) / 64 * 64);
+  splits = (g.K + kchunk - 1) / kchunk;
+  return force || splits >= 2;
+}
+
 // The fast-path configuration of a product, named by the context's benchmarking override values: 39 and 40 the
 // persistent 256 x 256 (K blocks of 64) and 256 x 128 (K blocks of 128) kernels, 11 - 20 the one-tile-per-workgroup
 // shapes of the switch in launch_fast_choice. An override the product cannot take falls through to the rules.
@@ -1117,7 +1235,7 @@ struct AddEpilogue {
 struct Prepared {
   GemmArgs g;
   int osz, batch;
-  bool checked, vec, fast, mul24;
+  bool checked, vec, fast, mul24, force_split;
 };
 
 // Argument checks that need no context (a group checks every member before any launch).
@@ -1133,8 +1251,13 @@ static int gemm_validate(const int8_t* A, const int8_t* Bt, const void* C, int b
   if (out_dtype != ANVIL_I8 && out_dtype != ANVIL_I16)
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: result dtype must be i8 or i16");
   if (lut && out_dtype != ANVIL_I8) return set_error(ANVIL_E_VALUE, "a LUT epilogue needs an i8 result");
-  if (flags & ~(ANVIL_GEMM_UNCHECKED | ANVIL_GEMM_CAUSAL_SKIP | ANVIL_GEMM_CAUSAL_K | ANVIL_GEMM_MUL24))
+  if (flags & ~(ANVIL_GEMM_UNCHECKED | ANVIL_GEMM_CAUSAL_SKIP | ANVIL_GEMM_CAUSAL_K | ANVIL_GEMM_MUL24 |
+                ANVIL_GEMM_SPLITK))
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: unknown flags %d", flags);
+  if ((flags & ANVIL_GEMM_SPLITK) && (!(flags & ANVIL_GEMM_UNCHECKED) ||
+                                      (flags & (ANVIL_GEMM_CAUSAL_SKIP | ANVIL_GEMM_CAUSAL_K)) || add ||
+                                      (long long)batch0 * batch1 != 1))
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: SPLITK needs UNCHECKED, batch 1, no causal mode and no fused add");
   if ((flags & ANVIL_GEMM_MUL24) && (mult >= (1 << 23) || mult < -(1 << 23)))
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: MUL24 needs |mult| < 2^23 (got %d)", mult);
   if ((flags & ANVIL_GEMM_CAUSAL_SKIP) && (flags & ANVIL_GEMM_CAUSAL_K))
@@ -1210,16 +1333,51 @@ static int gemm_prepare(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void*
   p.vec = vec;
   p.fast = fast;
   p.mul24 = (flags & ANVIL_GEMM_MUL24) != 0;
+  p.force_split = (flags & ANVIL_GEMM_SPLITK) != 0;
+  if (p.force_split && !fast)
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: SPLITK needs 16-byte aligned operands with K a multiple of 16");
   return ANVIL_OK;
 }
 
-static void gemm_launch(anvil_ctx* ctx, Prepared& p) {
-  if (!p.fast) return launch_gemm(p.g, p.checked, p.osz, p.vec, p.batch, ctx->stream, ctx->gemm_cfg);
+// The context's split-K workspace, grown to hold `sums` partial sums (written before they are read: no clearing).
+static int ensure_workspace(anvil_ctx* ctx, long long sums) {
+  if (ctx->ws_elems >= sums) return ANVIL_OK;
+  ANVIL_HIP(hipStreamSynchronize(ctx->stream));
+  if (ctx->ws) ANVIL_HIP(hipFree(ctx->ws));
+  ctx->ws = nullptr;
+  ctx->ws_elems = 0;
+  ANVIL_HIP(hipMalloc(&ctx->ws, sizeof(int) * sums));
+  ctx->ws_elems = sums;
+  return ANVIL_OK;
+}
+
+// Launch a prepared product. A split-K product keeps its partial tiles in the context's workspace (allocated on
+// first use).
+static int gemm_launch(anvil_ctx* ctx, Prepared& p) {
+  if (!p.fast) {
+    launch_gemm(p.g, p.checked, p.osz, p.vec, p.batch, ctx->stream, ctx->gemm_cfg);
+    return ANVIL_OK;
+  }
+  int splits = 0, kchunk = 0;
+  if (splitk_plan(p.g, p.batch, ctx->num_cu, p.force_split, splits, kchunk)) {
+    const long long tiles = (long long)((p.g.M + 127) / 128) * ((p.g.N + 127) / 128);
+    const long long sums = tiles * splits * 128 * 128;   // one int32 partial tile per (tile, chunk)
+    if (int r = ensure_workspace(ctx, sums)) return r;
+    p.g.ws = ctx->ws;
+    p.g.splits = splits;
+    p.g.kchunk = kchunk;
+    if (p.mul24)
+      launch_splitk<true>(p.g, p.osz, ctx->stream);
+    else
+      launch_splitk<false>(p.g, p.osz, ctx->stream);
+    return ANVIL_OK;
+  }
   const int choice = fast_choice(p.g, p.batch, ctx->gemm_cfg, ctx->num_cu);
   if (p.mul24)
     launch_fast_choice<true>(p.g, p.osz, p.batch, ctx->stream, choice, ctx->num_cu);
   else
     launch_fast_choice<false>(p.g, p.osz, p.batch, ctx->stream, choice, ctx->num_cu);
+  return ANVIL_OK;
 }
 
 static int gemm_entry(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
@@ -1228,7 +1386,7 @@ static int gemm_entry(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C
   Prepared p;
   if (int r = gemm_prepare(ctx, A, Bt, C, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags, add, p))
     return r;
-  gemm_launch(ctx, p);
+  if (int r = gemm_launch(ctx, p)) return r;
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }
@@ -1260,7 +1418,8 @@ extern "C" int anvil_gemm_i8_group(anvil_ctx* ctx, const anvil_gemm_desc* d, int
                      : launch_fast_group<256, 128, 2, 3, false>(gs, batch, count, p[0].osz, ctx->stream);
   }
   if (!one)
-    for (int i = 0; i < count; ++i) gemm_launch(ctx, p[i]);
+    for (int i = 0; i < count; ++i)
+      if (int r = gemm_launch(ctx, p[i])) return r;
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }

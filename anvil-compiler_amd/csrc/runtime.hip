@@ -44,6 +44,14 @@ __global__ void zero_kernel(uint8_t* __restrict__ p, size_t n) {
   }
 }
 
+int zero_fill(hipStream_t s, void* dst, size_t bytes) {
+  size_t blocks = (bytes / 16 + 255) / 256;
+  blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
+  ANVIL_LAUNCH(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (uint8_t*)dst, bytes);
+  ANVIL_LAUNCHED();
+  return ANVIL_OK;
+}
+
 }  // namespace anvil
 
 using namespace anvil;
@@ -90,6 +98,7 @@ int anvil_destroy(anvil_ctx* ctx) {
   for (auto& ev : ctx->events)
     if (ev) hipEventDestroy(ev);
   if (ctx->flags) hipFree(ctx->flags);
+  if (ctx->ws) hipFree(ctx->ws);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
   return ANVIL_OK;
@@ -146,11 +155,7 @@ int anvil_zero(anvil_ctx* ctx, void* dst, size_t bytes) {
   if (int r = check_ctx(ctx)) return r;
   if (!bytes) return ANVIL_OK;
   if (!dst) return set_error(ANVIL_E_VALUE, "anvil_zero: null pointer");
-  size_t blocks = (bytes / 16 + 255) / 256;
-  blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
-  ANVIL_LAUNCH(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, (uint8_t*)dst, bytes);
-  ANVIL_LAUNCHED();
-  return ANVIL_OK;
+  return zero_fill(ctx->stream, dst, bytes);
 }
 
 int anvil_event_record(anvil_ctx* ctx, int slot) {

@@ -70,14 +70,21 @@ SLOTS = 240
 
 
 def kernel_times(dev, steps, passes=3):
-    """Average device microseconds of each step's kernels over `passes` untimed passes."""
-    per = [0.0] * len(steps)
-    for _ in range(passes):
-        for i, (_, fn, a) in enumerate(steps):
-            dev.timed(16 + 2 * i, 17 + 2 * i, fn, *a)
-        dev.sync()
-        for i in range(len(steps)):
-            per[i] += 1e3 * dev.elapsed_ms(16 + 2 * i, 17 + 2 * i) / passes
+    """Average device microseconds of each launch: passes * len(steps) steps back to back, launch k % len(steps)
+    carrying events in step k, so each launch is measured among neighbours that run as in the timed region (a kernel
+    with events attached releases its caches on completion, which slows the next one) and no synchronisation idles
+    the device in between."""
+    n = len(steps)
+    per = [0.0] * n
+    for k in range(passes * n):
+        for j, (_, fn, a) in enumerate(steps):
+            if j == k % n:
+                dev.timed(16 + 2 * k, 17 + 2 * k, fn, *a)
+            else:
+                fn(*a)
+    dev.sync()
+    for k in range(passes * n):
+        per[k % n] += 1e3 * dev.elapsed_ms(16 + 2 * k, 17 + 2 * k) / passes
     return per
 
 
@@ -194,8 +201,9 @@ def bench_block(args):
         "end_to_end": e2e,
         "kernels": kernels,
         "kernels_us_sum": round(sum(per), 2),
-        "kernels_note": "per launch, device time of each step's kernels alone (events bound to the kernels' dispatch, "
-                        "hipExtLaunchKernel), mean of 3 untimed passes; ms_per_step adds the launch gaps",
+        "kernels_note": "per launch, device time of each launch's kernels alone (events bound to the kernels' dispatch, "
+                        "hipExtLaunchKernel), mean of 3 untimed back-to-back steps in which only that launch carries "
+                        "events; ms_per_step adds the launch gaps",
         "cpu_baseline": cpu,
     }
 

@@ -89,12 +89,19 @@ int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, in
  *   ANVIL_GEMM_CAUSAL_K     A[m][k] is zero for k > m (a causal softmax output): the K loop of a row tile stops at
  *                           its last row, which leaves every result unchanged.
  *   ANVIL_GEMM_MUL24        (with UNCHECKED) every |acc| and |mult| is below 2^23, so the requant product is one
- *                           24-bit multiply. */
+ *                           24-bit multiply.
+ *   ANVIL_GEMM_SPLITK       (with UNCHECKED, batch 1, no causal mode) split K into up to four chunks: one launch
+ *                           stores each (output tile, chunk)'s int32 partial sums in a workspace, a second one adds them
+ *                           up and requantizes. Integer addition is exact, so the result is the same; the library picks
+ *                           it by itself for products with few output tiles (M = 256), the flag forces it. The
+ *                           workspace (one 128 x 128 int32 partial tile per output tile and chunk) belongs to the
+ *                           context, allocated on first use. */
 enum anvil_gemm_flags {
   ANVIL_GEMM_UNCHECKED = 1,
   ANVIL_GEMM_CAUSAL_SKIP = 2,
   ANVIL_GEMM_CAUSAL_K = 4,
-  ANVIL_GEMM_MUL24 = 8
+  ANVIL_GEMM_MUL24 = 8,
+  ANVIL_GEMM_SPLITK = 16
 };
 int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,

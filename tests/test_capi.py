@@ -57,6 +57,10 @@ def test_gemm_argument_validation_precedes_the_device():
         gemm(1, 1, 0, 16, 16, st, 1, 3, None, 1, 0)
     with pytest.raises(ValueError, match="LUT epilogue needs an i8"):
         gemm(1, 1, 16, 16, 16, st, 1, 3, p, 2, 0)
+    with pytest.raises(ValueError, match="SPLITK needs UNCHECKED"):
+        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 16)
+    with pytest.raises(ValueError, match="SPLITK needs UNCHECKED"):
+        gemm(2, 1, 16, 16, 16, st, 1, 3, None, 1, 17)
     with pytest.raises(ValueError, match="unknown flags"):
         gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 64)
     with pytest.raises(ValueError, match="exclude each other"):
