@@ -50,6 +50,7 @@ SIGNATURES = {
     "anvil_time_kernels": [_p, _i, _i],
     "anvil_gemm_i8": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i],
     "anvil_gemm_i8_ex": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _i],
+    "anvil_gemm_i8_noalloc": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _i],
     "anvil_gemm_i8_group": [_p, _p, _i],
     "anvil_gemm_i8_add": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _p, _i32, _i32, _i, _p, _p, _i],
     "anvil_rmsnorm_int": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p],
@@ -212,6 +213,13 @@ class Device:
         self.lib.call("anvil_gemm_i8_ex", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)), C.c_void_p(_ptr(Cp)),
                       batch0, batch1, M, N, K, st, int(mult), shift, C.c_void_p(_ptr(lut) if lut is not None else 0),
                       DTYPE_CODE[out_dtype], int(flags))
+
+    def gemm_i8_noalloc(self, A, Bt, Cp, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags=0):
+        """anvil_gemm_i8_noalloc: gemm_i8 with split-K partials in the library's static scratch (allocates nothing)."""
+        st = (C.c_int64 * 9)(*[int(s) for s in strides])
+        self.lib.call("anvil_gemm_i8_noalloc", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)),
+                      C.c_void_p(_ptr(Cp)), batch0, batch1, M, N, K, st, int(mult), shift,
+                      C.c_void_p(_ptr(lut) if lut is not None else 0), DTYPE_CODE[out_dtype], int(flags))
 
     def gemm_i8_group(self, calls):
         """Independent gemm_i8 calls (tuples of its arguments) in one anvil_gemm_i8_group call."""

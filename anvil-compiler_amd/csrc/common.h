@@ -42,6 +42,8 @@ int hip_fail(hipError_t e, const char* what);
 int check_ctx(anvil_ctx* ctx);
 // zero `bytes` of device memory with a fill kernel on stream s (no memset node: safe inside a captured graph)
 int zero_fill(hipStream_t s, void* dst, size_t bytes);
+// once per device, with that device current: the device address of the GEMM's static split-K scratch
+int gemm_scratch_setup(int device);
 
 #define ANVIL_HIP(call)                                        \
   do {                                                         \

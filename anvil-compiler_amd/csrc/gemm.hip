@@ -26,6 +26,7 @@
 // causal = 1: tiles strictly above the diagonal (every n > every m) are skipped (their values are never read);
 // causal = 2: the K loop stops at m0 + BM (A[m][k] = 0 for k > m, e.g. a causal softmax output).
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1220,6 +1221,27 @@ static void launch_gemm(GemmArgs& g, bool checked, int osz, bool vec, int batch,
     launch_cfg<256, 256, 64, 2, 2, false>(g, osz, vec, batch, s);
 }
 
+// Static split-K scratch of anvil_gemm_i8_noalloc: SCRATCH_SUMS int32 partial sums. Each device holds its own copy
+// until the process ends; the library only ever uses it through the per-device address hipGetSymbolAddress returns
+// (the array's name is a host-side stand-in in host code). A split-K run writes every partial sum before it reads it,
+// so nothing needs clearing between calls; anvil_gemm_i8_noalloc calls that overlap on one device race.
+constexpr long long SCRATCH_SUMS = 1ll << 22;     // 16 MiB: 64 tiles of 128 x 128 in four K chunks
+constexpr int SCRATCH_DEVICES = 64;
+static __device__ __align__(256) int scratch[SCRATCH_SUMS];
+static int* g_scratch[SCRATCH_DEVICES];
+static std::mutex g_scratch_mu;
+
+int gemm_scratch_setup(int device) {
+  if (device < 0 || device >= SCRATCH_DEVICES)
+    return set_error(ANVIL_E_VALUE, "device %d beyond the %d the static GEMM scratch serves", device, SCRATCH_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[device]) return ANVIL_OK;
+  void* ptr = nullptr;
+  ANVIL_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  g_scratch[device] = static_cast<int*>(ptr);
+  return ANVIL_OK;
+}
+
 }  // namespace anvil
 
 using namespace anvil;
@@ -1352,8 +1374,8 @@ static int ensure_workspace(anvil_ctx* ctx, long long sums) {
 }
 
 // Launch a prepared product. A split-K product keeps its partial tiles in the context's workspace (allocated on
-// first use).
-static int gemm_launch(anvil_ctx* ctx, Prepared& p) {
+// first use), or with `noalloc` in the static scratch, within whose size it must then fit.
+static int gemm_launch(anvil_ctx* ctx, Prepared& p, bool noalloc = false) {
   if (!p.fast) {
     launch_gemm(p.g, p.checked, p.osz, p.vec, p.batch, ctx->stream, ctx->gemm_cfg);
     return ANVIL_OK;
@@ -1362,8 +1384,17 @@ static int gemm_launch(anvil_ctx* ctx, Prepared& p) {
   if (splitk_plan(p.g, p.batch, ctx->num_cu, p.force_split, splits, kchunk)) {
     const long long tiles = (long long)((p.g.M + 127) / 128) * ((p.g.N + 127) / 128);
     const long long sums = tiles * splits * 128 * 128;   // one int32 partial tile per (tile, chunk)
-    if (int r = ensure_workspace(ctx, sums)) return r;
-    p.g.ws = ctx->ws;
+    if (noalloc) {
+      if (sums > SCRATCH_SUMS)
+        return set_error(ANVIL_E_VALUE,
+                         "anvil_gemm_i8_noalloc: a split-K product of %lld partial sums (%lld tiles of 128 x 128 in "
+                         "%d K chunks) exceeds the static scratch (%lld sums)", sums, tiles, splits, SCRATCH_SUMS);
+      if (!g_scratch[ctx->device]) return set_error(ANVIL_E_RUNTIME, "anvil_gemm_i8_noalloc: scratch not set up");
+      p.g.ws = g_scratch[ctx->device];
+    } else {
+      if (int r = ensure_workspace(ctx, sums)) return r;
+      p.g.ws = ctx->ws;
+    }
     p.g.splits = splits;
     p.g.kchunk = kchunk;
     if (p.mul24)
@@ -1382,11 +1413,11 @@ static int gemm_launch(anvil_ctx* ctx, Prepared& p) {
 
 static int gemm_entry(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
                       int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
-                      int flags, const AddEpilogue* add) {
+                      int flags, const AddEpilogue* add, bool noalloc = false) {
   Prepared p;
   if (int r = gemm_prepare(ctx, A, Bt, C, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags, add, p))
     return r;
-  if (int r = gemm_launch(ctx, p)) return r;
+  if (int r = gemm_launch(ctx, p, noalloc)) return r;
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }
@@ -1428,6 +1459,12 @@ extern "C" int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* B
                                 int M, int N, int K, const int64_t* strides, int32_t mult, int shift,
                                 const int8_t* lut, int out_dtype, int flags) {
   return gemm_entry(ctx, A, Bt, C, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags, nullptr);
+}
+
+extern "C" int anvil_gemm_i8_noalloc(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0,
+                                     int batch1, int M, int N, int K, const int64_t* strides, int32_t mult, int shift,
+                                     const int8_t* lut, int out_dtype, int flags) {
+  return gemm_entry(ctx, A, Bt, C, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags, nullptr, true);
 }
 
 extern "C" int anvil_gemm_i8_add(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, int8_t* C, int batch0,

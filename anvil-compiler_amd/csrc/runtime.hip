@@ -86,6 +86,10 @@ int anvil_init(int device, anvil_ctx** out) {
     anvil_destroy(c);
     return hip_fail(e, "anvil_init");
   }
+  if (int r = gemm_scratch_setup(device)) {
+    anvil_destroy(c);
+    return r;
+  }
   *out = c;
   return ANVIL_OK;
 }
