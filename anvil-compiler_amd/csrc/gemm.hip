@@ -890,7 +890,7 @@ constexpr int persist_occupancy() { return NS * (BM + BN) * BK + 256 <= 80 * 102
 template <int BM, int BN, int BK, int NS, int NW, int WGN, int OSZ, bool MUL24>
 __global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) void gemm_i8_persist(GemmArgs g) {
   constexpr int CPR = BK / 16, KS = BK / 32, WGM = NW / WGN;
-  static_assert(NS >= 3 && NS <= 6, "three to six LDS stages");
+  static_assert(NS >= 2 && NS <= 6, "two to six LDS stages");
   constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
   static_assert(WGM * WGN == NW && TM >= 1 && TN >= 1, "wave grid");
   static_assert(KS % 2 == 0, "fragment sets alternate within a stage");
@@ -900,7 +900,7 @@ __global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) voi
   constexpr int STAGE = (BM + BN) * BK;
   __shared__ __attribute__((aligned(1024))) int8_t L0[STAGE];
   __shared__ __attribute__((aligned(1024))) int8_t L1[STAGE];
-  __shared__ __attribute__((aligned(1024))) int8_t L2[STAGE];
+  __shared__ __attribute__((aligned(1024))) int8_t L2[NS > 2 ? STAGE : 16];
   __shared__ __attribute__((aligned(1024))) int8_t L3[NS > 3 ? STAGE : 16];
   __shared__ __attribute__((aligned(1024))) int8_t L4[NS > 4 ? STAGE : 16];
   __shared__ __attribute__((aligned(1024))) int8_t L5[NS > 5 ? STAGE : 16];
@@ -1142,12 +1142,19 @@ static int fast_choice(const GemmArgs& g, int batch, int cfg, int num_cu) {
   // the persistent 256 x 256 kernel: one workgroup of 8 waves per CU, four 32 KiB LDS stages, wave tiles 64 x 128
   const bool persist_ok = g.causal == 0 && ((g.K + 63) / 64) % 4 == 0;
   const bool persist128_ok = g.causal == 0 && ((g.K + 127) / 128) % 3 == 0;
-  if ((cfg == 39 && persist_ok) || (cfg == 40 && persist128_ok) || (cfg >= 11 && cfg <= 20)) return cfg;
+  const bool persist128x2_ok = g.causal == 0 && ((g.K + 127) / 128) % 2 == 0;
+  if ((cfg == 39 && persist_ok) || (cfg == 40 && persist128_ok) || ((cfg == 41 || cfg == 42) && persist128x2_ok) ||
+      (cfg >= 11 && cfg <= 20))
+    return cfg;
   // measured on MI355X (block GEMM shapes, K 768 and 3072): wide products with at least six 256 x 256 tiles per CU
   // take the persistent kernel (it halves the L2 traffic per MFMA of the 256 x 128 tile); 256 x 128 tiles with three
   // LDS stages (72 KiB) run two workgroups per CU, which hide each other's pipeline fill and epilogue; small problems
   // keep the 128 x 128 tile (more workgroups)
   const long long tiles256 = (long long)((g.M + 255) / 256) * ((g.N + 255) / 256) * batch;
+  // Wide and long (N, K >= 2048): 256 x 256 tiles with 128-byte K blocks in two LDS stages (128 KiB). Its loads fetch
+  // whole 128-byte lines of each row, and a stage (four k-steps) covers the next one's latency once K is long.
+  // Measured: 16384 x 3072 x 3072 147 us against 188 us on 64-byte K blocks; at K = 768 (fc) it loses, 100 vs 97 us.
+  if (persist128x2_ok && g.N >= 2048 && g.K >= 2048 && tiles256 >= (long long)num_cu) return 41;
   if (persist_ok && g.N >= 2048 && tiles256 >= 6ll * num_cu) return 39;
   // Long K, N below 2048 (the block's proj, K 3072, N 768): the persistent kernel on 256 x 128 tiles with 128-byte
   // K blocks. Its loads fetch 128 contiguous bytes of each row (the 64-byte rows of a K block of 64 reach about half
@@ -1168,6 +1175,8 @@ static void launch_fast_choice(GemmArgs& g, int osz, int batch, hipStream_t s, i
   switch (choice) {
     case 39: return launch_persist<256, 256, 64, 4, MUL24, 8, 2>(g, osz, batch, num_cu, s);
     case 40: return launch_persist<256, 128, 128, 3, MUL24, 8, 2>(g, osz, batch, num_cu, s);
+    case 41: return launch_persist<256, 256, 128, 2, MUL24, 8, 2>(g, osz, batch, num_cu, s);
+    case 42: return launch_persist<256, 128, 128, 2, MUL24, 8, 2>(g, osz, batch, num_cu, s);
     case 11: return launch_fast<256, 256, 2, 3, MUL24>(g, osz, batch, s);
     case 12: return launch_fast<256, 256, 2, 4, MUL24>(g, osz, batch, s);
     case 14: return launch_fast<128, 128, 2, 4, MUL24>(g, osz, batch, s);

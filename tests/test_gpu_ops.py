@@ -362,6 +362,16 @@ def test_gemm_wide_products_take_the_persistent_kernel(dev, M, N, K, dtype, lut,
     _check_sampled_gemm(dev, M, N, K, dtype, lut, add, 41)
 
 
+@pytest.mark.parametrize("M,N,K,dtype,lut,add", [(16384 + 37, 3072, 3072, "i8", True, False),
+                                                 (20000, 2080, 2048, "i16", False, False),
+                                                 (16384, 3072, 3072, "i8", False, True),
+                                                 (8192 + 5, 2048 + 48, 2304, "i8", False, False)])
+def test_gemm_wide_long_k_two_stages(dev, M, N, K, dtype, lut, add):
+    """N and K >= 2048 (config 2's 16384 x 3072 x 3072) run on the persistent 256 x 256 kernel with 128-byte K blocks in
+    two LDS stages: ragged rows and columns, a LUT, an i16 result and the fused residual add."""
+    _check_sampled_gemm(dev, M, N, K, dtype, lut, add, 47)
+
+
 @pytest.mark.parametrize("M,N,K,dtype,lut,add", [(32768 + 37, 768, 3072, "i8", False, False),
                                                  (32768, 1536, 2048, "i8", True, False),
                                                  (33000, 768, 2048, "i16", False, False),
