@@ -556,9 +556,200 @@ extern "C" int anvil_rmsnorm_int(anvil_ctx* ctx, const void* x, int x_dtype, con
   return anvil_rmsnorm_int_ex(ctx, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out, 0);
 }
 
+namespace anvil {
+
+// ------------------------------------------------------------------------------ fast softmax_lut, int8 result
+// The int8-result form of softmax_fast (one <= 127), with every per-element step one instruction and no integer
+// division. Per 16-byte chunk a lane keeps nk bytes (its causal prefix); the others become -128, which leaves the
+// row max unchanged (the reference's max starts at -128) and adds (16 - nk) lut[127 - m] to the exp sum, subtracted
+// once per chunk. Byte b of a chunk becomes the table index d = x - m + 255 in [0, 255] (one SDWA add into its
+// byte), then the byte offset 4 d (one SDWA shift), used for the exp table and, at the same address plus a
+// constant, for the row's probability table, whose entries are the exact quotients (lut[d] one + S // 2) // S in
+// float64: y = fma(lut[d], A, B) with A = fl(one fl(1 / S)), B = fl(fl((S // 2) fl(1 / S)) + 2^-40) - 1/2 lies within
+// 2^-44 of n / S - 1/2 + 2^-40 (n = lut[d] one + S // 2 < 2^31, n / S < 128), and a non-integer n / S is at least
+// 1 / S > 2^-31 from an integer, so y + 1.5 2^52 rounds to floor(n / S) exactly. One wavefront per row; a 64-lane
+// workgroup, so both tables sit at fixed LDS addresses.
+
+template <int B>
+__device__ __forceinline__ int max_sbyte(int acc, unsigned x) {      // max(acc, signed byte B of x)
+  int d;
+  if constexpr (B == 0)
+    asm("v_max_i32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(d) : "v"(acc), "v"(x));
+  else if constexpr (B == 1)
+    asm("v_max_i32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+        : "=v"(d) : "v"(acc), "v"(x));
+  else if constexpr (B == 2)
+    asm("v_max_i32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+        : "=v"(d) : "v"(acc), "v"(x));
+  else
+    asm("v_max_i32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=v"(d) : "v"(acc), "v"(x));
+  return d;
+}
+
+// byte B of x plus k (mod 256) written into byte B of acc, the other bytes of acc kept
+template <int B>
+__device__ __forceinline__ void add_byte(unsigned& acc, unsigned x, unsigned k) {
+  if constexpr (B == 0)
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:BYTE_0"
+        : "+v"(acc) : "v"(k), "v"(x));
+  else if constexpr (B == 1)
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:BYTE_1"
+        : "+v"(acc) : "v"(k), "v"(x));
+  else if constexpr (B == 2)
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:BYTE_2"
+        : "+v"(acc) : "v"(k), "v"(x));
+  else
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:BYTE_3"
+        : "+v"(acc) : "v"(k), "v"(x));
+}
+
+// 4 * (byte B of x), zero-extended
+template <int B>
+__device__ __forceinline__ unsigned off4(unsigned x, unsigned two) {
+  unsigned d;
+  if constexpr (B == 0)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(d) : "v"(two), "v"(x));
+  else if constexpr (B == 1)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+        : "=v"(d) : "v"(two), "v"(x));
+  else if constexpr (B == 2)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+        : "=v"(d) : "v"(two), "v"(x));
+  else
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=v"(d) : "v"(two), "v"(x));
+  return d;
+}
+
+template <int R>
+__global__ __launch_bounds__(64) void softmax_i8_fast(const int8_t* __restrict__ x, const int* __restrict__ lut,
+                                                      int one, int causal, long long rows, int t1, int t2,
+                                                      int8_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) int lut_s[256];
+  __shared__ __attribute__((aligned(16))) int ptab[256];
+  __shared__ double lutd_s[256];
+  const int lane = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int v = lut[lane + 64 * k];
+    lut_s[lane + 64 * k] = v;
+    lutd_s[lane + 64 * k] = (double)v;
+  }
+  __syncthreads();
+  const int chunks = t2 >> 4;
+  const unsigned two = 2;
+  const char* lutb = reinterpret_cast<const char*>(lut_s);
+  const char* ptb = reinterpret_cast<const char*>(ptab);
+  for (long long row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int i = (int)(row % t1);
+    const int kept = causal ? min(i + 1, t2) : t2;
+    const int8_t* xr = x + row * t2;
+    v4i xv[R];
+    unsigned mk[R][4];
+    int nk[R];
+    int m0 = -128, m1 = -128, m2 = -128, m3 = -128;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = lane + 64 * r;
+      nk[r] = c < chunks ? min(max(kept - 16 * c, 0), 16) : 0;
+      xv[r] = v4i{0, 0, 0, 0};
+      if (nk[r] > 0) xv[r] = *reinterpret_cast<const v4i*>(xr + 16 * c);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) mk[r][q] = 0xffffffffu;
+      if (nk[r] < 16) {                                  // the causal edge, or a chunk past it: masked bytes -> -128
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int kq = min(max(nk[r] - 4 * q, 0), 4);
+          mk[r][q] = kq >= 4 ? 0xffffffffu : (1u << (8 * kq)) - 1u;
+          xv[r][q] = (int)(((unsigned)xv[r][q] & mk[r][q]) | (0x80808080u & ~mk[r][q]));
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const unsigned w = (unsigned)xv[r][q];
+        m0 = max_sbyte<0>(m0, w);
+        m1 = max_sbyte<1>(m1, w);
+        m2 = max_sbyte<2>(m2, w);
+        m3 = max_sbyte<3>(m3, w);
+      }
+    }
+    const int m = wave_max(max(max(m0, m1), max(m2, m3)));
+    const unsigned kadd = (unsigned)(255 - m);           // d = x - m + 255, in [0, 255]: byte add mod 256
+    unsigned off[R][16];
+    int S = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        unsigned dq = 0;
+        const unsigned w = (unsigned)xv[r][q];
+        add_byte<0>(dq, w, kadd);
+        add_byte<1>(dq, w, kadd);
+        add_byte<2>(dq, w, kadd);
+        add_byte<3>(dq, w, kadd);
+        off[r][4 * q + 0] = off4<0>(dq, two);
+        off[r][4 * q + 1] = off4<1>(dq, two);
+        off[r][4 * q + 2] = off4<2>(dq, two);
+        off[r][4 * q + 3] = off4<3>(dq, two);
+      }
+#pragma unroll
+      for (int b = 0; b < 16; ++b) S += *reinterpret_cast<const int*>(lutb + off[r][b]);
+      S -= (16 - nk[r]) * lut_s[127 - m];                 // the masked bytes' share
+    }
+    S = wave_sum32(S);
+    // the row's probability table, entry d at ptab[d] (A and B exact to 2^-52 relative; see above)
+    const double inv = 1.0 / (double)S;
+    const double A = (double)one * inv;
+    const double Bc = (double)(S >> 1) * inv + 0x1p-40 - 0.5;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int d = lane + 64 * k;
+      ptab[d] = __double2loint(__builtin_fma(lutd_s[d], A, Bc) + 0x1.8p52);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");     // table entries written by other lanes of the wave
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = lane + 64 * r;
+      if (c >= chunks) continue;
+      v4i ov;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int p0 = *reinterpret_cast<const int*>(ptb + off[r][4 * q]);
+        const int p1 = *reinterpret_cast<const int*>(ptb + off[r][4 * q + 1]);
+        const int p2 = *reinterpret_cast<const int*>(ptb + off[r][4 * q + 2]);
+        const int p3 = *reinterpret_cast<const int*>(ptb + off[r][4 * q + 3]);
+        ov[q] = (int)(pack4(p0, p1, p2, p3) & mk[r][q]);  // masked keys: probability 0
+      }
+      *reinterpret_cast<v4i*>(out + row * t2 + 16 * c) = ov;
+    }
+    __builtin_amdgcn_wave_barrier();                     // the table is rewritten for the wave's next row
+  }
+}
+
+}  // namespace anvil
+
 template <typename TO>
 static void launch_softmax_fast(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, int one, int causal,
                                 long long rows, int t1, int t2, TO* out) {
+  if constexpr (sizeof(TO) == 1) {
+    const long long cap = (long long)ctx->num_cu * 32;  // one 64-lane workgroup per row, grid-stride
+    const unsigned grid = (unsigned)(rows < cap ? rows : cap);
+    if (t2 <= 1024)
+      ANVIL_LAUNCH((softmax_i8_fast<1>), dim3(grid), dim3(64), 0, ctx->stream, x, lut, one, causal, rows, t1, t2,
+                   out);
+    else if (t2 <= 2048)
+      ANVIL_LAUNCH((softmax_i8_fast<2>), dim3(grid), dim3(64), 0, ctx->stream, x, lut, one, causal, rows, t1, t2,
+                   out);
+    else
+      ANVIL_LAUNCH((softmax_i8_fast<4>), dim3(grid), dim3(64), 0, ctx->stream, x, lut, one, causal, rows, t1, t2,
+                   out);
+    return;
+  }
   const unsigned grid = row_grid(rows, ctx->num_cu);
   if (t2 <= 1024)
     ANVIL_LAUNCH((softmax_fast<1, TO>), dim3(grid), dim3(R_THREADS), 0, ctx->stream, x, lut, one, causal, rows,
