@@ -35,6 +35,7 @@ __device__ __forceinline__ int wave_sum32(int v) {
 }
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ int sbyte(const v4i& v, int b) {   // signed byte b (0..15) of a 16-byte chunk
   return (int)(int8_t)((unsigned)v[b >> 2] >> (8 * (b & 3)));
@@ -388,6 +389,165 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
   }
 }
 
+// ------------------------------------------------------------------------------- fast rmsnorm_int, int16 rows
+// The proven form of a wide (int16) row: ss = e + sum((x^2 + 2^(c-1)) >> c), out = requant(x w lut[i], M, s + k).
+// A row of cols = 8 n entries is n chunks of 16 bytes (8 entries); L lanes (the power of two >= n, at most 64)
+// take a row, so a wave holds 64 / L rows and lane sub of row rr handles chunks c L + sub (c < CH). Lanes past n
+// and rows past the last get buffer offsets beyond the descriptor (loads 0, stores nothing), as in rmsnorm_fast.
+// The row sum is reduced over the L lanes (DPP within 16 lanes, swizzles across), so every lane of a row holds it
+// and forms that row's table index, multiplier, shift and clamp bounds itself; the table sits in LDS (lut_len words
+// of dynamic LDS, staged once per workgroup), so its per-lane reads do not wait behind the next group's row loads. Each entry's square is one 24-bit
+// multiply of its sign-extended half (SDWA); x w is one 24-bit multiply of that half by the sign-extended weight
+// byte, |x w| <= 2^22. With s24 (every |lut[i] M| < 2^23) x w (lut[i] M) + rnd is one 24-bit multiply-add; without
+// it the product wraps in 32 bits, which is exact because x w lut[i] M + rnd is proven to fit int32.
+template <int H, int B>
+__device__ __forceinline__ int mul_half_byte(unsigned x, unsigned w) {   // sext(half H of x) * sext(byte B of w)
+  int d;
+  if constexpr (H == 0 && B == 0)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:BYTE_0"
+        : "=v"(d) : "v"(x), "v"(w));
+  else if constexpr (H == 1 && B == 1)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:BYTE_1"
+        : "=v"(d) : "v"(x), "v"(w));
+  else if constexpr (H == 0 && B == 2)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:BYTE_2"
+        : "=v"(d) : "v"(x), "v"(w));
+  else
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:BYTE_3"
+        : "=v"(d) : "v"(x), "v"(w));
+  static_assert((H == 0 && (B == 0 || B == 2)) || (H == 1 && (B == 1 || B == 3)), "entry 2q + H sits in byte B");
+  return d;
+}
+
+template <int H>
+__device__ __forceinline__ int square_half(unsigned x) {                 // sext(half H of x)^2
+  int d;
+  if constexpr (H == 0)
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_0"
+        : "=v"(d) : "v"(x));
+  else
+    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:WORD_1"
+        : "=v"(d) : "v"(x));
+  return d;
+}
+
+template <int L>
+__device__ __forceinline__ int lane_group_sum(int v) {                   // sum over aligned groups of L lanes
+  if constexpr (L > 1) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);    // quad_perm [1,0,3,2]
+  if constexpr (L > 2) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);    // quad_perm [2,3,0,1]
+  if constexpr (L > 4) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);   // row_half_mirror
+  if constexpr (L > 8) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);   // row_mirror
+  if constexpr (L > 16) v += __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 0x1F);           // lane ^ 16
+  if constexpr (L > 32) v += __shfl_xor(v, 32);
+  return v;
+}
+
+constexpr int WIDE_LUT_MAX = 4096;                               // table words the wide kernel stages in LDS
+
+template <int L, int CH>
+__global__ __launch_bounds__(R_THREADS) void rmsnorm_wide_fast(const int16_t* __restrict__ x,
+                                                                const int8_t* __restrict__ w,
+                                                                const int* __restrict__ lut, int lut_len, int mult,
+                                                                int shift, int c, int e, int s24, long long rows,
+                                                                int cols, int8_t* __restrict__ out) {
+  static_assert(CH == 1 || L == 64, "several chunks a lane only with a whole wave a row");
+  constexpr int RW = 64 / L;                                     // rows a wave holds at once
+  extern __shared__ int wide_lut[];
+  for (int i0 = threadIdx.x; i0 < lut_len; i0 += 4 * R_THREADS) {   // four table reads in flight a lane
+    int v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = i0 + j * R_THREADS < lut_len ? lut[i0 + j * R_THREADS] : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (i0 + j * R_THREADS < lut_len) wide_lut[i0 + j * R_THREADS] = v[j];
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, rr = lane / L, sub = lane % L;
+  const int n = cols >> 3;                                       // 16-byte chunks of x a row
+  v2i wv[CH];
+  unsigned xoff[CH], ooff[CH];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int ch = k * L + sub;
+    const bool on = ch < n;
+    wv[k] = on ? *reinterpret_cast<const v2i*>(w + 8 * ch) : v2i{0, 0};
+    xoff[k] = on ? (unsigned)(rr * 2 * cols + 16 * ch) : OOB;
+    ooff[k] = on ? (unsigned)(rr * cols + 8 * ch) : OOB;
+  }
+  const int rc = c ? 1 << (c - 1) : 0;
+  const long long step = (long long)gridDim.x * R_WAVES * RW;
+  auto group = [&](const void* base, long long r0, int row_bytes) {   // a raw buffer over rows r0 .. r0 + RW - 1
+    const long long nr = r0 < rows ? std::min<long long>(RW, rows - r0) : 0;
+    return uniform_rsrc((const char*)base + (r0 < rows ? r0 : 0) * row_bytes, (int)(nr * row_bytes));
+  };
+  auto load = [&](long long r0, v4i* xv) {
+    const __amdgpu_buffer_rsrc_t rs = group(x, r0, 2 * cols);
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+      xv[k] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, xoff[k], 0, 0));
+  };
+  auto process = [&](const v4i* xv, long long r0) {
+    int ss = 0;
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const unsigned xd = (unsigned)xv[k][q];
+        ss += (unsigned)(square_half<0>(xd) + rc) >> c;         // proven: x^2 + rnd and the sum fit int32
+        ss += (unsigned)(square_half<1>(xd) + rc) >> c;
+      }
+    int t = lane_group_sum<L>(ss) + e;
+    int kk = 0;
+    while (t >= lut_len) {
+      t >>= 2;
+      ++kk;
+    }
+    const int sh = shift + kk;                                   // proven at most 31
+    const int rm = wide_lut[t] * mult;                           // wraps unless s24; the products stay exact
+    const int rnd = sh ? 1 << (sh - 1) : 0;
+    const int lo = sh >= 24 ? INT32_MIN : -128 * (1 << sh), hi = sh >= 24 ? INT32_MAX : 128 * (1 << sh) - 1;
+    const __amdgpu_buffer_rsrc_t ws = group(out, r0, cols);
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      int xw[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const unsigned xd = (unsigned)xv[k][q], wd = (unsigned)wv[k][q >> 1];
+        if (q & 1) {
+          xw[2 * q] = mul_half_byte<0, 2>(xd, wd);
+          xw[2 * q + 1] = mul_half_byte<1, 3>(xd, wd);
+        } else {
+          xw[2 * q] = mul_half_byte<0, 0>(xd, wd);
+          xw[2 * q + 1] = mul_half_byte<1, 1>(xd, wd);
+        }
+      }
+      int y[8];
+      if (s24) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = med3i(mad_i24v(xw[j], rm, rnd), lo, hi);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = med3i((int)((unsigned)xw[j] * (unsigned)rm + (unsigned)rnd), lo, hi);
+      }
+      const v2i o = {(int)sra_pack4v(y[0], y[1], y[2], y[3], sh), (int)sra_pack4v(y[4], y[5], y[6], y[7], sh)};
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, o), ws,
+                                            ooff[k], 0, 0);
+    }
+  };
+  long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * RW;
+  v4i xa[CH], xb[CH];
+  load(row0, xa);
+  while (row0 < rows) {
+    load(row0 + step, xb);
+    process(xa, row0);
+    row0 += step;
+    if (row0 >= rows) break;
+    load(row0 + step, xa);
+    process(xb, row0);
+    row0 += step;
+  }
+}
+
 static unsigned row_grid(long long rows, int device_cus) {
   long long blocks = (rows + R_WAVES - 1) / R_WAVES;
   const long long cap = (long long)device_cus * 16;            // enough resident waves to cover HBM latency
@@ -497,6 +657,7 @@ __global__ __launch_bounds__(R_THREADS) void softmax_kernel(const int8_t* __rest
 using namespace anvil;
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+static bool al8(const void* p) { return ((uintptr_t)p & 7) == 0; }
 
 extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* w, const int32_t* lut,
                                     int lut_len, int32_t mult, int shift, int ss_shift, int32_t ss_init, int64_t rows,
@@ -537,6 +698,30 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
     else
       ANVIL_LAUNCH(rmsnorm_fast<false>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
                          mult, shift, (long long)rows, cols, out);
+  } else if ((flags & ANVIL_OP_UNCHECKED) && x_dtype == ANVIL_I16 && cols % 8 == 0 && cols <= 2048 &&
+             lut_len <= WIDE_LUT_MAX && al16(x) && al8(w) && al8(out)) {
+    const int n = cols / 8;                                     // 16-byte chunks a row
+    int L = 1;                                                  // lanes a row: the power of two >= n, at most 64
+    while (L < n && L < 64) L <<= 1;
+    const long long groups = (rows + 64 / L - 1) / (64 / L);
+    const dim3 grid((unsigned)std::min<long long>((groups + R_WAVES - 1) / R_WAVES, 8ll * ctx->num_cu));
+    const int s24 = (flags & ANVIL_RMS_S24) ? 1 : 0;
+    auto launch = [&](auto kernel) {
+      ANVIL_LAUNCH(kernel, grid, dim3(R_THREADS), 4 * lut_len, ctx->stream, (const int16_t*)x, w, lut, lut_len, mult,
+                   shift, ss_shift, ss_init, s24, (long long)rows, cols, out);
+    };
+    switch (n > 64 ? 64 * ((n + 63) / 64) : L) {
+      case 1: launch(rmsnorm_wide_fast<1, 1>); break;
+      case 2: launch(rmsnorm_wide_fast<2, 1>); break;
+      case 4: launch(rmsnorm_wide_fast<4, 1>); break;
+      case 8: launch(rmsnorm_wide_fast<8, 1>); break;
+      case 16: launch(rmsnorm_wide_fast<16, 1>); break;
+      case 32: launch(rmsnorm_wide_fast<32, 1>); break;
+      case 64: launch(rmsnorm_wide_fast<64, 1>); break;
+      case 128: launch(rmsnorm_wide_fast<64, 2>); break;
+      case 192: launch(rmsnorm_wide_fast<64, 3>); break;
+      default: launch(rmsnorm_wide_fast<64, 4>); break;
+    }
   } else if (x_dtype == ANVIL_I8) {
     ANVIL_LAUNCH(rmsnorm_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
                        (const int8_t*)x, w, lut, lut_len, mult, shift, ss_shift, ss_init, (long long)rows, cols, out,

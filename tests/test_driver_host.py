@@ -260,3 +260,20 @@ def test_float_inputs_are_quantized_on_the_device_as_on_the_host(fake, cfg1, dty
     r = cm.run(x, batch=True, keep="all")
     assert np.array_equal(r.ints["x"], cm.quantize_input(x))
     assert [c for c in fake.calls if c[0] == "quantize"][0][2] == (dtype == np.float64)
+
+
+def test_wide_frozen_model_selects_the_fast_wide_rmsnorm(fake):
+    """The reference's v2 frozen model (i16 residual stream) passes the proof, so its four wide rmsnorm steps run
+    UNCHECKED (the wide kernel for int16 rows of 32 entries), with RMS_S24 where every |lut[i] M| < 2^23; results
+    equal the oracle's."""
+    text, consts, x = helpers.reference_model("v2")
+    m = anvil_mi355x.parse_ir(text)
+    cm = anvil_mi355x.compile((m, consts))
+    assert cm.proven
+    xs = np.random.default_rng(5).integers(-32768, 32768, (2, 16, 32))
+    res = cm.run(xs, "mi355x", quantized=True, batch=True)
+    want = interp.run(m, {"x": xs}, consts, batch=True)
+    assert np.array_equal(res.ints["L1.out"], want.values["L1.out"])
+    rms = [c for c in fake.calls if c[0] == "rmsnorm"]
+    assert len(rms) == 4 and all(c[1:3] == (32, 32) and c[3] & rt.OP_UNCHECKED for c in rms)
+    assert all(c[3] & rt.RMS_S24 for c in rms)

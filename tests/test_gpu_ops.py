@@ -156,15 +156,56 @@ def test_rmsnorm_shift_reaching_int32_bounds(dev, d):
     assert np.abs(want).max() > 0
 
 
-def test_rmsnorm_i16_wide(dev):
-    d = 32
-    rng = np.random.default_rng(8)
+def _wide_case(d, rows, seed):
+    """A proven wide rmsnorm (table, s, c, e from the quantizer for |x| <= 2^15) and rows over the full int16 range:
+    random rows, the extreme constant rows, a zero row and quiet rows (small sums: low table indexes, k = 0)."""
+    rng = np.random.default_rng([8, d, seed])
     w = rng.integers(-127, 128, d)
-    lut, s, c, e = Q.wide_rsqrt_table(4e-4, 0.01, 0.02, 127, d, 1e-6, 1 << 15)
-    x = np.concatenate([rng.integers(-(1 << 15), 1 << 15, (100, d)), np.full((1, d), -(1 << 15)),
-                        np.full((1, d), (1 << 15) - 1), np.zeros((1, d), int)])
+    lut, s, c, e = Q.wide_rsqrt_table(4e-4, 0.01, 0.02, int(np.abs(w).max()), d, 1e-6, 1 << 15)
+    x = np.concatenate([rng.integers(-(1 << 15), 1 << 15, (rows, d)), np.full((1, d), -(1 << 15)),
+                        np.full((1, d), (1 << 15) - 1), np.zeros((1, d), int), rng.integers(-40, 41, (rows // 4, d))])
+    return x, w, lut, s, c, e
+
+
+@pytest.mark.parametrize("flags", [0, rt.OP_UNCHECKED, rt.OP_UNCHECKED | rt.RMS_S24])
+@pytest.mark.parametrize("d", [8, 16, 24, 32, 40, 128, 504, 512, 520, 768, 1536, 2048])
+def test_rmsnorm_i16_wide(dev, d, flags):
+    """int16 rows with square shift c and sum offset e. UNCHECKED selects the wide kernel: L lanes a row (the power
+    of two >= d / 8, at most 64; lanes past the row idle when d / 8 is not one), up to four 16-byte chunks a lane
+    for d > 512; with RMS_S24 (asserted to hold) the 24-bit multiply-add, without it the 32-bit wrapping product."""
+    x, w, lut, s, c, e = _wide_case(d, 300, 0)
+    if flags & rt.RMS_S24:
+        assert int(np.abs(lut).max()) < (1 << 23)
     want = sem.rmsnorm_wide(x, w, lut, 1, s, c, e, "i16")
-    assert np.array_equal(_rms(dev, x, "i16", w, lut, 1, s, c, e), want)
+    assert c > 0 or d == 1
+    assert np.array_equal(_rms(dev, x, "i16", w, lut, 1, s, c, e, flags=flags), want)
+
+
+@pytest.mark.parametrize("d", [8, 32, 768])
+def test_rmsnorm_i16_wide_walks_many_row_groups(dev, d):
+    """More row groups than the grid has waves (eight workgroups of four waves per CU, 64 / L rows a group): each
+    wave walks three or more groups through both row buffers, and the last group is ragged."""
+    lanes = min(64, 1 << max(0, (d // 8 - 1).bit_length()))
+    rows = 8 * 4 * 256 * (64 // lanes) * 3 + 5
+    rng = np.random.default_rng([63, d])
+    w = rng.integers(-127, 128, d)
+    lut, s, c, e = Q.wide_rsqrt_table(4e-4, 0.01, 0.02, int(np.abs(w).max()), d, 1e-6, 1 << 15)
+    x = rng.integers(-(1 << 15), 1 << 15, (rows, d))
+    want = sem.rmsnorm_wide(x, w, lut, 1, s, c, e, "i16")
+    flags = rt.OP_UNCHECKED | (rt.RMS_S24 if int(np.abs(lut).max()) < (1 << 23) else 0)
+    assert np.array_equal(_rms(dev, x, "i16", w, lut, 1, s, c, e, flags=flags), want)
+
+
+def test_rmsnorm_i16_wide_multiplier(dev):
+    """A multiplier M != 1 with the table scaled down by the same factor, so every product stays proven: the wide
+    kernel forms lut[i] M per row (wrapping in 32 bits without RMS_S24), and the checked kernel agrees."""
+    d = 64
+    x, w, lut, s, c, e = _wide_case(d, 200, 1)
+    m = 5
+    lut = lut // m
+    want = sem.rmsnorm_wide(x, w, lut, m, s, c, e, "i16")
+    for flags in (0, rt.OP_UNCHECKED):
+        assert np.array_equal(_rms(dev, x, "i16", w, lut, m, s, c, e, flags=flags), want)
 
 
 def _softmax(dev, x, lut, one, causal, dtype="i8", flags=0):
