@@ -50,7 +50,15 @@ struct AttnArgs {
   int one, causal;
   int mo, so, rndo;    // output requant
   int nqt;             // query tiles of 32 rows per head
+  unsigned long long mq, mb;   // n / nqt and n / batch1 as (n m) >> (32 + k): m = ceil(2^(32+k) / d), 2^k >= d
+  int kq, kb;
 };
+
+// n / d for a uniform n < 2^32 by one 64-bit multiply-high (scalar ALU): with m = ceil(2^(32+k) / d) and 2^k >= d,
+// m < 2^33 and the error n (m d - 2^(32+k)) / (d 2^(32+k)) stays below 1 / d, so the floor is exact.
+__device__ __forceinline__ unsigned udiv_magic(unsigned n, unsigned long long m, int k) {
+  return (unsigned)(((unsigned long long)n * m) >> (32 + k));
+}
 
 constexpr int A_THREADS = 256;
 
@@ -73,7 +81,7 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
   static_assert(2 * 32 * OROW * 4 >= 32 * 256, "the per-row p tables fit in the partial-O space");
   __shared__ __attribute__((aligned(16))) int lut_s[256];
-  __shared__ double lutd_s[256];                            // the LUT as doubles, for the p tables
+  __shared__ double lutd_s[260];                            // the LUT as doubles, for the p tables (+ 4 zeros)
   __shared__ __attribute__((aligned(16))) int red_m[4][32];   // after the max: the rows' (A, B) as doubles
   __shared__ int red_s[4][32];
   __shared__ int dlow_s[32];
@@ -89,10 +97,10 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   const int nblk = gridDim.x;
   int pid = blockIdx.x;
   if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
-  const int bh = pid / a.nqt;
-  const int qt = a.nqt - 1 - pid % a.nqt;
+  const int bh = (int)udiv_magic((unsigned)pid, a.mq, a.kq);
+  const int qt = a.nqt - 1 - (pid - bh * a.nqt);
   const int q0 = qt * 32;
-  const int b0 = bh / a.batch1, b1 = bh % a.batch1;
+  const int b0 = (int)udiv_magic((unsigned)bh, a.mb, a.kb), b1 = bh - b0 * a.batch1;
   const int qrow = q0 + l32;
   const int ntiles = a.causal ? qt + 1 : a.nqt;
 
@@ -180,6 +188,7 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   if (half == 0) red_m[w][l32] = mx;
   lut_s[t] = lutv;
   lutd_s[t] = (double)lutv;
+  if (t < 4) lutd_s[256 + t] = 0.0;                      // read by the top dword of a row table (scores above the max)
   // the p tables (8 KiB of the partial-O space, filled after the next barrier) start zeroed, 32 bytes a thread
   int8_t* ptab = reinterpret_cast<int8_t*>(&opart[0][0]);
   *reinterpret_cast<v4i*>(ptab + 32 * t) = v4i{0, 0, 0, 0};
@@ -211,7 +220,7 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   });
   S += __shfl_xor(S, 32, 64);
   if (half == 0) red_s[w][l32] = S;
-  const bool mono = __syncthreads_and(t == 255 || lut_s[t] <= lut_s[t + 1]) != 0;   // lut_s is visible here
+  __syncthreads();
 
   // ---- 3. probabilities, O_w = P V over this wave's tiles
   // p depends on the row and the score only, so each row gets a byte table of (lut[d] one + S // 2) // S over the
@@ -224,6 +233,9 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   double* qab = reinterpret_cast<double*>(&red_m[0][0]);  // [0, 32): A, [32, 64): B; red_m is read before the last barrier
   if (w == 0) {
     S = red_s[0][l32] + red_s[1][l32] + red_s[2][l32] + red_s[3][l32];
+    const v4i l4 = *reinterpret_cast<const v4i*>(lut_s + 4 * lane);      // lane l checks entries 4 l .. 4 l + 4
+    const int nx = lane < 63 ? lut_s[4 * lane + 4] : INT_MAX;
+    const bool mono = __all(l4[0] <= l4[1] && l4[1] <= l4[2] && l4[2] <= l4[3] && l4[3] <= nx);
     const double Sd = (double)S;                         // S >= lut[255] >= 1: the row maximum maps to d = 255
     const double qa0 = (double)a.one / Sd;
     const double qb0 = (double)(S >> 1) / Sd + 0x1p-40 - 0.5;   // the - 0.5 is exact (Sterbenz, or S = 1)
@@ -247,29 +259,26 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   const double qa = qab[l32], qb = qab[32 + l32];
   // The tables sit in the partial-O space, 256 bytes a row: the entry of score s in row r is at column
   // (s & 255) ^ 4 r, so a lookup address is the row base with its low byte replaced by the swizzled score byte
-  // (one v_perm), and the 32 rows' entries for one s fall in 32 different banks.
+  // (one v_perm), and the 32 rows' entries for one s fall in 32 different banks. The XOR keeps each dword whole, so
+  // the table is written a dword at a time: dword c holds scores 4 c .. 4 c + 3 (c = -32 .. 31), d = 4 c + e - max + 255.
   // An entry is y = fma(lut[d], A, B - 1/2), within 2^-45 of n / S - 1/2 + 2^-40 and never a half-integer, so
   // adding 1.5 2^52 rounds it to n // S, which is then the low dword of the sum: two full-rate float64 operations.
-  // The four entries of a pass are written whatever dlow is (d clamped at 0): an entry with d < dlow either has
-  // d < d0, whose quotient is exactly 0, or d < 127 - max, whose score s < -128 wraps to the column of s + 256, a
-  // score above the row maximum that no kept key reads.
+  // A row writes the dwords from the one holding its max down to the one holding score dlow + max - 255 (>= -128, as
+  // dlow >= 127 - max, so every d >= 0): each byte of them with a score up to the max gets its exact quotient (0 below
+  // d0), and a byte above the max (d up to 258, the zero pad of lutd_s) gets 0 or less, read by no kept key.
   constexpr int PT = 256;
   const int cx = 4 * l32;
   {
-    const int part = 2 * w + half;                       // this lane's eighth of its row's table
+    const int part = 2 * w + half;                       // this lane's eighth of its row's dwords
     int8_t* trow = ptab + l32 * PT;
     const int dlow = dlow_s[l32];
-    for (int d = 255 - part; d >= dlow; d -= 32) {      // four independent entries per pass, reads issued together
-      int du[4];
-      double lv[4];
+    const int ctop = mx >> 2, cbot = (dlow + mx - 255) >> 2;   // arithmetic shifts: floor
+    for (int c = ctop - part; c >= cbot; c -= 8) {
+      const double* lp = lutd_s + (4 * c - mx + 255);
+      int v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        du[u] = max(d - 8 * u, 0);
-        lv[u] = lutd_s[du[u]];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        trow[((du[u] + mx - 255) & 255) ^ cx] = (int8_t)__double2loint(__builtin_fma(lv[u], qa, qb) + 0x1.8p52);
+      for (int e = 0; e < 4; ++e) v[e] = __double2loint(__builtin_fma(lp[e], qa, qb) + 0x1.8p52);
+      *reinterpret_cast<unsigned*>(trow + ((4 * c & 255) ^ cx)) = pack4(v[0], v[1], v[2], v[3]);
     }
     __syncthreads();
   }
@@ -427,6 +436,13 @@ extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t*
   a.one = one, a.causal = causal ? 1 : 0;
   a.mo = m_o, a.so = s_o, a.rndo = s_o ? 1 << (s_o - 1) : 0;
   a.nqt = T / 32;
+  auto magic = [](int d, unsigned long long& m, int& k) {
+    k = 0;
+    while ((1 << k) < d) ++k;
+    m = ((1ull << (32 + k)) + d - 1) / d;
+  };
+  magic(a.nqt, a.mq, a.kq);
+  magic(batch1, a.mb, a.kb);
   const unsigned grid = (unsigned)((long long)batch0 * batch1 * a.nqt);
   if (flags & ANVIL_ATTN_S24)
     launch_attention_nt<true>(a, D, grid, ctx->stream);
