@@ -150,6 +150,8 @@ class CompiledModel:
         self._embed_dev = None
         self._const_views = {}
         self._const_bt = {}
+        self._const_kb = {}
+        self._const_bt_host = {}
         self._plans = {}
         self.group_gemms = True           # independent consecutive GEMMs as one anvil_gemm_i8_group call
 
@@ -458,8 +460,49 @@ class CompiledModel:
             mem = self.dev.upload(bt)
             b = Buf(mem.nbytes, f"{op.sym_str}.Bt")
             b.mem = mem
+            self._const_bt_host[id(b)] = bt
             self._const_bt[key] = View(b, "i8", bt.shape, contig_strides(bt.shape))
         return self._const_bt[key]
+
+    def _bt_kblocked(self, op):
+        """The same transposed const (N, K), K-blocked for the fast GEMM kernels: (ceil(K / 64), N, 64), row n's K block j
+        at j N 64 + n 64. Returns (view of the buffer, block stride in bytes)."""
+        key = op.b
+        if key not in self._const_kb:
+            bt = self._bt_const(op)
+            N, K = bt.dims
+            host = np.zeros((N, -(-K // 64) * 64), np.int8)
+            host[:, :K] = self.dev_download_const(bt)
+            kb = np.ascontiguousarray(host.reshape(N, -1, 64).transpose(1, 0, 2))
+            mem = self.dev.upload(kb)
+            b = Buf(mem.nbytes, f"{op.sym_str}.Bt.kblocked")
+            b.mem = mem
+            self._const_kb[key] = (View(b, "i8", (N, K), (64, 1)), N * 64)
+        return self._const_kb[key]
+
+    def dev_download_const(self, bt):
+        """Host copy of a const operand view made by _bt_const (kept on the host when it was uploaded)."""
+        return self._const_bt_host[id(bt.buf)]
+
+    def _kblock_weight(self, op, rows1, rows2, strides, flags, K, swapped):
+        """Proven 2-D products whose const right operand is read through _bt_const take its K-blocked copy: the
+        operand's loads then fetch whole 64-byte blocks of consecutive rows, where row-major rows give 64-byte pieces
+        of separate lines. Only for the fast kernels (proven, K and the other operand's row stride multiples of 16);
+        returns (rows1, rows2, strides, flags) for the call."""
+        if not (flags & rt.GEMM_UNCHECKED) or K % 16 or op.b not in self._const_bt:
+            return rows1, rows2, strides, flags
+        if (rows1 if swapped else rows2).buf is not self._const_bt[op.b].buf:
+            return rows1, rows2, strides, flags
+        other = rows2 if swapped else rows1
+        if any(v % 16 for v in (strides[3:6] if swapped else strides[0:3])) or (other.offset * other.itemsize) % 16:
+            return rows1, rows2, strides, flags
+        kv, kb = self._bt_kblocked(op)
+        strides = list(strides)
+        if swapped:
+            strides[2] = kb
+            return kv, rows2, strides, flags | rt.GEMM_A_KBLOCK
+        strides[5] = kb
+        return rows1, kv, strides, flags | rt.GEMM_B_KBLOCK
 
     def _host_const(self, value):
         op = value.owner
@@ -540,6 +583,7 @@ class CompiledModel:
                 if add is not None and self._plan_fused_add(P, op, add, views, r1, rows2, c2, strides, lut, flags,
                                                             label, step, keep):
                     return out
+                r1, rows2, strides, flags = self._kblock_weight(op, r1, rows2, strides, flags, K, swapped)
                 step(label, _call_gemm, self.dev, r1, rows2, c2, 1, 1, r1.dims[0], Nx, K, strides, op, lut, t.dtype,
                      flags)
                 return out
@@ -559,6 +603,7 @@ class CompiledModel:
             merged.insert(0, (1, 0, 0, 0))
         (b0, sa0, sb0, sc0), (b1, sa1, sb1, sc1) = merged
         strides = [sa0, sa1, rows1.strides[-2], sb0, sb1, rows2.strides[-2], sc0, sc1, c.strides[-2]]
+        rows1, rows2, strides, flags = self._kblock_weight(op, rows1, rows2, strides, flags, K, swapped)
         step(label, _call_gemm, self.dev, rows1, rows2, c, b0, b1, Mx, Nx, K, strides, op, lut, t.dtype, flags)
         return out
 
@@ -578,6 +623,7 @@ class CompiledModel:
         store_y = keep == "all" or op.result in self.output_values or len(self.users.get(op.result, [])) > 1
         ma, mb = (int(add.Mb), int(add.Ma)) if y_first else (int(add.Ma), int(add.Mb))   # (residual, y)
         rstrides = [0, 0, rv.strides[0], 0, 0, d.strides[0]]
+        a2, bt, strides, flags = self._kblock_weight(op, a2, bt, strides, flags, K, False)
         step(label, _call_gemm_add, self.dev, a2, bt, c2 if store_y else None, rows, N, K, strides, op, lut, rv, ma,
              mb, int(add.s), d, rstrides, flags)
         views[add.result] = d.reshape(tuple(views[other].dims))

@@ -29,6 +29,7 @@ _ERRORS = {1: ValueError, 2: OverflowError, 3: ZeroDivisionError, 4: RuntimeErro
 
 # anvil_gemm_i8_ex flags (include/anvil_mi355x.h)
 GEMM_UNCHECKED, GEMM_CAUSAL_SKIP, GEMM_CAUSAL_K, GEMM_MUL24, GEMM_SPLITK = 1, 2, 4, 8, 16
+GEMM_A_KBLOCK, GEMM_B_KBLOCK = 32, 64
 # anvil_rmsnorm_int_ex / anvil_softmax_lut_ex / anvil_attention_i8 flags
 OP_UNCHECKED, ATTN_S24, RMS_S24 = 1, 2, 2
 

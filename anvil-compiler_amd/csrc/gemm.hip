@@ -44,6 +44,9 @@ struct GemmArgs {
   int batch1;
   int tiles_m, tiles_n;
   long long sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc;
+  // bytes from one 64-byte K block of an operand row to the next: 64 for row-major operands; for K-blocked ones
+  // (fast kernels only) the block stride, with lda / ldb then 64 (row r's block j at r 64 + j kba)
+  long long kba, kbb;
   int mult, shift, rnd;
   const int8_t* lut;
   unsigned* flags;
@@ -64,6 +67,12 @@ struct GemmArgs {
 
 constexpr int G_THREADS = 256;
 constexpr int GROUP_M = 4;
+
+// Bytes of a tile's operand rows that its buffer descriptor covers: rows whole rows of a row-major operand (kb = 64),
+// or, K-blocked, those rows in every K block; anything past reads as zero.
+__device__ __forceinline__ int operand_bytes(int rows, long long ld, long long kb, int K) {
+  return kb == 64 ? (int)(rows * ld) : (int)(rows * 64 + ((K + 63) / 64 - 1) * kb);
+}
 
 // Physical 16-byte chunk of logical chunk `chunk` in LDS row `row`. gfx950's LDS serves a ds_read_b128 from 64
 // banks (256 bytes a cycle) to 16 lanes at a time, taken as four blocks of four consecutive lanes whose block
@@ -481,12 +490,12 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
   // split-K: bz is the K chunk (the batch is 1), and the chunk's first byte becomes the operands' K origin
   const int b0 = SPLIT ? 0 : bz / g.batch1, b1 = SPLIT ? 0 : bz % g.batch1;
   const int kbeg = SPLIT ? bz * g.kchunk : 0;
-  const int8_t* Ab = g.A + b0 * g.sa0 + b1 * g.sa1 + (long long)m0 * g.lda + kbeg;
-  const int8_t* Bb = g.B + b0 * g.sb0 + b1 * g.sb1 + (long long)n0 * g.ldb + kbeg;
+  const int8_t* Ab = g.A + b0 * g.sa0 + b1 * g.sa1 + (long long)m0 * g.lda + (kbeg >> 6) * g.kba;
+  const int8_t* Bb = g.B + b0 * g.sb0 + b1 * g.sb1 + (long long)n0 * g.ldb + (kbeg >> 6) * g.kbb;
   const int rows_a = min(g.M - m0, BM), rows_b = min(g.N - n0, BN);
   const int K = SPLIT ? min(g.K - kbeg, g.kchunk) : (g.causal == 2 ? min(g.K, m0 + BM) : g.K);
-  const __amdgpu_buffer_rsrc_t ra = uniform_rsrc(Ab, (int)(rows_a * g.lda));
-  const __amdgpu_buffer_rsrc_t rb = uniform_rsrc(Bb, (int)(rows_b * g.ldb));
+  const __amdgpu_buffer_rsrc_t ra = uniform_rsrc(Ab, operand_bytes(rows_a, g.lda, g.kba, K));
+  const __amdgpu_buffer_rsrc_t rb = uniform_rsrc(Bb, operand_bytes(rows_b, g.ldb, g.kbb, K));
 
   if (g.lut) lut_s[t] = g.lut[t];
 
@@ -496,22 +505,23 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
 #pragma unroll
   for (int j = 0; j < JA; ++j) {
     const int P = (wave + 4 * j) * 64 + lane, row = P / CPR, c = swz<BK>(row, P % CPR);
-    offa[j] = (unsigned)(row * g.lda + c * 16);
+    offa[j] = (unsigned)(row * g.lda + (c >> 2) * g.kba + (c & 3) * 16);
     ka[j] = c * 16;
   }
 #pragma unroll
   for (int j = 0; j < JB; ++j) {
     const int P = (wave + 4 * j) * 64 + lane, row = P / CPR, c = swz<BK>(row, P % CPR);
-    offb[j] = (unsigned)(row * g.ldb + c * 16);
+    offb[j] = (unsigned)(row * g.ldb + (c >> 2) * g.kbb + (c & 3) * 16);
     kb[j] = c * 16;
   }
   // a stage at or past K loads zeros (every offset out of range): issuing is unconditional, so the compiler's
   // per-array tracking of outstanding LDS writes stays exact (a branch around the loads would make it wait for all)
   auto issue = [&](int8_t* arr, int k0) {
+    const unsigned oa = (unsigned)((k0 >> 6) * g.kba), ob = (unsigned)((k0 >> 6) * g.kbb);
 #pragma unroll
-    for (int j = 0; j < JA; ++j) dma16(ra, arr + (wave + 4 * j) * 1024, k0 + ka[j] < K ? offa[j] + k0 : OOB);
+    for (int j = 0; j < JA; ++j) dma16(ra, arr + (wave + 4 * j) * 1024, k0 + ka[j] < K ? offa[j] + oa : OOB);
 #pragma unroll
-    for (int j = 0; j < JB; ++j) dma16(rb, arr + BM * BK + (wave + 4 * j) * 1024, k0 + kb[j] < K ? offb[j] + k0 : OOB);
+    for (int j = 0; j < JB; ++j) dma16(rb, arr + BM * BK + (wave + 4 * j) * 1024, k0 + kb[j] < K ? offb[j] + ob : OOB);
   };
 
   v16i acc[TN][TM];
@@ -946,11 +956,11 @@ __global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) voi
   // an invalid tile gets empty descriptors: its loads read zeros and are never used
   auto rsrc_a = [&](const Tile& T) {
     return uniform_rsrc(g.A + T.b0 * g.sa0 + T.b1 * g.sa1 + (long long)T.m0 * g.lda,
-                        T.valid ? (int)(min(g.M - T.m0, BM) * g.lda) : 0);
+                        T.valid ? operand_bytes(min(g.M - T.m0, BM), g.lda, g.kba, g.K) : 0);
   };
   auto rsrc_b = [&](const Tile& T) {
     return uniform_rsrc(g.B + T.b0 * g.sb0 + T.b1 * g.sb1 + (long long)T.n0 * g.ldb,
-                        T.valid ? (int)(min(g.N - T.n0, BN) * g.ldb) : 0);
+                        T.valid ? operand_bytes(min(g.N - T.n0, BN), g.ldb, g.kbb, g.K) : 0);
   };
 
   Tile cur = tile_of(0);
@@ -962,21 +972,22 @@ __global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) voi
 #pragma unroll
   for (int j = 0; j < JA; ++j) {
     const int P = (wave + NW * j) * 64 + lane, row = P / CPR, c = swz<BK>(row, P % CPR);
-    offa[j] = (unsigned)(row * g.lda + c * 16);
+    offa[j] = (unsigned)(row * g.lda + (c >> 2) * g.kba + (c & 3) * 16);
     ka[j] = c * 16;
   }
 #pragma unroll
   for (int j = 0; j < JB; ++j) {
     const int P = (wave + NW * j) * 64 + lane, row = P / CPR, c = swz<BK>(row, P % CPR);
-    offb[j] = (unsigned)(((row & ~31) | bperm(row & 31)) * g.ldb + c * 16);
+    offb[j] = (unsigned)(((row & ~31) | bperm(row & 31)) * g.ldb + (c >> 2) * g.kbb + (c & 3) * 16);
     kb[j] = c * 16;
   }
   const int K = g.K;
   auto issue = [&](int8_t* arr, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int k0) {
+    const unsigned oa = (unsigned)((k0 >> 6) * g.kba), ob = (unsigned)((k0 >> 6) * g.kbb);
 #pragma unroll
-    for (int j = 0; j < JA; ++j) dma16(ra, arr + (wave + NW * j) * 1024, k0 + ka[j] < K ? offa[j] + k0 : OOB);
+    for (int j = 0; j < JA; ++j) dma16(ra, arr + (wave + NW * j) * 1024, k0 + ka[j] < K ? offa[j] + oa : OOB);
 #pragma unroll
-    for (int j = 0; j < JB; ++j) dma16(rb, arr + BM * BK + (wave + NW * j) * 1024, k0 + kb[j] < K ? offb[j] + k0 : OOB);
+    for (int j = 0; j < JB; ++j) dma16(rb, arr + BM * BK + (wave + NW * j) * 1024, k0 + kb[j] < K ? offb[j] + ob : OOB);
   };
 
   v16i acc[TN][TM];
@@ -1283,8 +1294,16 @@ static int gemm_validate(const int8_t* A, const int8_t* Bt, const void* C, int b
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: result dtype must be i8 or i16");
   if (lut && out_dtype != ANVIL_I8) return set_error(ANVIL_E_VALUE, "a LUT epilogue needs an i8 result");
   if (flags & ~(ANVIL_GEMM_UNCHECKED | ANVIL_GEMM_CAUSAL_SKIP | ANVIL_GEMM_CAUSAL_K | ANVIL_GEMM_MUL24 |
-                ANVIL_GEMM_SPLITK))
+                ANVIL_GEMM_SPLITK | ANVIL_GEMM_A_KBLOCK | ANVIL_GEMM_B_KBLOCK))
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: unknown flags %d", flags);
+  for (int o = 0; o < 2; ++o) {                          // K-blocked operands: block stride and reach
+    if (!(flags & (o ? ANVIL_GEMM_B_KBLOCK : ANVIL_GEMM_A_KBLOCK))) continue;
+    const long long kb = strides[o ? 5 : 2];
+    if (!(flags & ANVIL_GEMM_UNCHECKED))
+      return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: K-blocked operands need ANVIL_GEMM_UNCHECKED");
+    if (kb < 64 || kb % 16 || (long long)((K + 63) / 64) * kb + 256ll * 64 >= (1ll << 31))
+      return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: K-block stride %lld of %s out of range", kb, o ? "Bt" : "A");
+  }
   if ((flags & ANVIL_GEMM_SPLITK) && (!(flags & ANVIL_GEMM_UNCHECKED) ||
                                       (flags & (ANVIL_GEMM_CAUSAL_SKIP | ANVIL_GEMM_CAUSAL_K)) || add ||
                                       (long long)batch0 * batch1 != 1))
@@ -1320,9 +1339,13 @@ static int gemm_prepare(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void*
   g.sa0 = strides[0];
   g.sa1 = strides[1];
   g.lda = strides[2];
+  g.kba = 64;
+  if (flags & ANVIL_GEMM_A_KBLOCK) g.kba = g.lda, g.lda = 64;
   g.sb0 = strides[3];
   g.sb1 = strides[4];
   g.ldb = strides[5];
+  g.kbb = 64;
+  if (flags & ANVIL_GEMM_B_KBLOCK) g.kbb = g.ldb, g.ldb = 64;
   g.sc0 = strides[6];
   g.sc1 = strides[7];
   g.ldc = strides[8];
@@ -1365,6 +1388,9 @@ static int gemm_prepare(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void*
   p.fast = fast;
   p.mul24 = (flags & ANVIL_GEMM_MUL24) != 0;
   p.force_split = (flags & ANVIL_GEMM_SPLITK) != 0;
+  if ((flags & (ANVIL_GEMM_A_KBLOCK | ANVIL_GEMM_B_KBLOCK)) && !fast)
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: K-blocked operands need 16-byte aligned operands with K a multiple "
+                                    "of 16 (and no benchmarking override)");
   if (p.force_split && !fast)
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: SPLITK needs 16-byte aligned operands with K a multiple of 16");
   return ANVIL_OK;

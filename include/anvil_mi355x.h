@@ -95,13 +95,21 @@ int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, in
  *                           up and requantizes. Integer addition is exact, so the result is the same; the library picks
  *                           it by itself for products with few output tiles (M = 256), the flag forces it. The
  *                           workspace (one 128 x 128 int32 partial tile per output tile and chunk) belongs to the
- *                           context, allocated on first use. */
+ *                           context, allocated on first use.
+ *   ANVIL_GEMM_A_KBLOCK     (with UNCHECKED) A is K-blocked: the 64-byte K block j of row r (its K bytes 64 j ..
+ *                           64 j + 63) sits at A + r * 64 + j * strides[2] (plus the batch strides), so one block of
+ *                           consecutive rows is contiguous and a tile's operand loads read whole cache lines.
+ *   ANVIL_GEMM_B_KBLOCK     (with UNCHECKED) the same for Bt, with strides[5] the block stride.
+ *                           Both need 16-byte aligned operands, K a multiple of 16 and a block stride that is a
+ *                           multiple of 16; the results are those of the row-major operands. */
 enum anvil_gemm_flags {
   ANVIL_GEMM_UNCHECKED = 1,
   ANVIL_GEMM_CAUSAL_SKIP = 2,
   ANVIL_GEMM_CAUSAL_K = 4,
   ANVIL_GEMM_MUL24 = 8,
-  ANVIL_GEMM_SPLITK = 16
+  ANVIL_GEMM_SPLITK = 16,
+  ANVIL_GEMM_A_KBLOCK = 32,
+  ANVIL_GEMM_B_KBLOCK = 64
 };
 int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,

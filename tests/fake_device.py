@@ -10,6 +10,7 @@ import threading
 
 import numpy as np
 
+from anvil_mi355x import runtime as rt
 from oracle import semantics as sem
 
 NP = {"i8": np.int8, "i16": np.int16, "i32": np.int32}
@@ -100,13 +101,31 @@ class FakeDevice:
         """Every output is computed, also under the causal flags (a superset of what the kernel writes)."""
         self.calls.append(("gemm", b0, b1, M, N, K, tuple(strides), flags))
         sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc = strides
-        a = self.view(A, "i8", (b0, b1, M, K), (sa0, sa1, lda, 1)).astype(np.int64)
-        bt = self.view(Bt, "i8", (b0, b1, N, K), (sb0, sb1, ldb, 1)).astype(np.int64)
+        a = self._operand(A, b0, b1, M, K, sa0, sa1, lda, flags & rt.GEMM_A_KBLOCK)
+        bt = self._operand(Bt, b0, b1, N, K, sb0, sb1, ldb, flags & rt.GEMM_B_KBLOCK)
         lt = None if lut is None else self.view(lut, "i8", (256,), (1,)).astype(np.int64)
         out = self._guard(lambda: sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, out_dtype,
                                                       fast=self.fast))
         if out is not None:
             self.store(Cp, out_dtype, (b0, b1, M, N), (sc0, sc1, ldc, 1), out)
+
+    def _operand(self, ptr, b0, b1, rows, K, s0, s1, ld, kblocked):
+        """A GEMM operand (b0, b1, rows, K): row-major rows of stride ld, or K-blocked (row r's 64-byte K block j at
+        r 64 + j ld, as ANVIL_GEMM_A_KBLOCK / B_KBLOCK describe)."""
+        if not kblocked:
+            return self.view(ptr, "i8", (b0, b1, rows, K), (s0, s1, ld, 1)).astype(np.int64)
+        nb = -(-K // 64)
+        v = self.view(ptr, "i8", (b0, b1, rows, nb, 64), (s0, s1, 64, ld, 1)).astype(np.int64)
+        return v.reshape(b0, b1, rows, nb * 64)[..., :K]
+
+    @staticmethod
+    def _operand_end(dims, strides, kblocked, K):
+        """Offset of the last byte an operand (b0, b1, rows, K) covers."""
+        b0, b1, rows = dims
+        s0, s1, ld = strides
+        if not kblocked:
+            return (b0 - 1) * s0 + (b1 - 1) * s1 + (rows - 1) * ld + K - 1
+        return (b0 - 1) * s0 + (b1 - 1) * s1 + (rows - 1) * 64 + (-(-K // 64) - 1) * ld + 63
 
     def gemm_i8_group(self, calls):
         """Members run one after another; none may write bytes another member reads or writes."""
@@ -119,9 +138,10 @@ class FakeDevice:
             return p, p + (last + 1) * SIZE[dtype]
 
         reads, writes = [], []
-        for A, Bt, Cp, b0, b1, M, N, K, st, _, _, lut, dt, _ in calls:
-            r = [span(A, "i8", (b0, b1, M, K), (st[0], st[1], st[2], 1)),
-                 span(Bt, "i8", (b0, b1, N, K), (st[3], st[4], st[5], 1))]
+        for A, Bt, Cp, b0, b1, M, N, K, st, _, _, lut, dt, fl in calls:
+            pa, pb = (x.ptr if hasattr(x, "ptr") else int(x) for x in (A, Bt))
+            r = [(pa, pa + 1 + self._operand_end((b0, b1, M), st[0:3], fl & rt.GEMM_A_KBLOCK, K)),
+                 (pb, pb + 1 + self._operand_end((b0, b1, N), st[3:6], fl & rt.GEMM_B_KBLOCK, K))]
             if lut is not None:
                 r.append(span(lut, "i8", (256,), (1,)))
             reads.append(r)
@@ -140,8 +160,8 @@ class FakeDevice:
         self.calls.append(("gemm_add", b0, b1, M, N, K, tuple(strides), flags, Cp is not None))
         sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc = strides
         sr0, sr1, ldr, sd0, sd1, ldd = rstrides
-        a = self.view(A, "i8", (b0, b1, M, K), (sa0, sa1, lda, 1)).astype(np.int64)
-        bt = self.view(Bt, "i8", (b0, b1, N, K), (sb0, sb1, ldb, 1)).astype(np.int64)
+        a = self._operand(A, b0, b1, M, K, sa0, sa1, lda, flags & rt.GEMM_A_KBLOCK)
+        bt = self._operand(Bt, b0, b1, N, K, sb0, sb1, ldb, flags & rt.GEMM_B_KBLOCK)
         lt = None if lut is None else self.view(lut, "i8", (256,), (1,)).astype(np.int64)
         r = self.view(R, "i8", (b0, b1, M, N), (sr0, sr1, ldr, 1)).astype(np.int64)
 

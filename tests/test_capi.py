@@ -62,7 +62,11 @@ def test_gemm_argument_validation_precedes_the_device():
     with pytest.raises(ValueError, match="SPLITK needs UNCHECKED"):
         gemm(2, 1, 16, 16, 16, st, 1, 3, None, 1, 17)
     with pytest.raises(ValueError, match="unknown flags"):
-        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 64)
+        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 128)
+    with pytest.raises(ValueError, match="K-blocked operands need ANVIL_GEMM_UNCHECKED"):
+        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 32)
+    with pytest.raises(ValueError, match="K-block stride 16 of Bt out of range"):
+        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 1 | 64)
     with pytest.raises(ValueError, match="exclude each other"):
         gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 6)
     with pytest.raises(ValueError, match="null context"):
