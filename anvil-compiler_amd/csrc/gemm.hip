@@ -47,6 +47,7 @@ struct GemmArgs {
   // bytes from one 64-byte K block of an operand row to the next: 64 for row-major operands; for K-blocked ones
   // (fast kernels only) the block stride, with lda / ldb then 64 (row r's block j at r 64 + j kba)
   long long kba, kbb;
+  long long kbc;        // the same for the result's 64-column blocks (64: row-major; fast kernels only otherwise)
   int mult, shift, rnd;
   const int8_t* lut;
   unsigned* flags;
@@ -67,6 +68,12 @@ struct GemmArgs {
 
 constexpr int G_THREADS = 256;
 constexpr int GROUP_M = 4;
+
+// Element offset of result (m, n) from the batch entry's base: row-major (kbc = 64) or K-blocked (ldc = 64, column
+// block n / 64 at kbc). A 16-byte store chunk never crosses a 64-column block.
+__device__ __forceinline__ long long cpos(const GemmArgs& g, int m, int n) {
+  return (long long)m * g.ldc + (long long)(n >> 6) * g.kbc + (n & 63);
+}
 
 // Bytes of a tile's operand rows that its buffer descriptor covers: rows whole rows of a row-major operand (kb = 64),
 // or, K-blocked, those rows in every K block; anything past reads as zero.
@@ -268,7 +275,7 @@ __global__ __launch_bounds__(G_THREADS) void gemm_i8_kernel(GemmArgs g) {
     const int m = m0 + rr;
     if (m >= g.M) break;
     const int8_t* src = smem + rr * SROW + cc * 16;
-    char* dst = Cb + ((long long)m * g.ldc + n0 + cfirst) * OSZ;
+    char* dst = Cb + cpos(g, m, n0 + cfirst) * OSZ;
     if (g.vec_store && cfirst + 16 / OSZ <= cols_valid) {
       *reinterpret_cast<v4i*>(dst) = *reinterpret_cast<const v4i*>(src);
     } else {
@@ -406,7 +413,7 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
             v4i w;
 #pragma unroll
             for (int q = 0; q < 4; ++q) w[q] = (int)pack4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-            *reinterpret_cast<v4i*>(Cb + (long long)m * g.ldc + n) = w;
+            *reinterpret_cast<v4i*>(Cb + cpos(g, m, n)) = w;
           } else {
             v4i w0, w1;
 #pragma unroll
@@ -414,7 +421,7 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
               w0[q] = (int)__builtin_amdgcn_perm((unsigned)v[2 * q + 1], (unsigned)v[2 * q], 0x05040100u);
               w1[q] = (int)__builtin_amdgcn_perm((unsigned)v[2 * q + 9], (unsigned)v[2 * q + 8], 0x05040100u);
             }
-            char* d = Cb + ((long long)m * g.ldc + n) * 2;
+            char* d = Cb + cpos(g, m, n) * 2;
             *reinterpret_cast<v4i*>(d) = w0;
             *reinterpret_cast<v4i*>(d + 16) = w1;
           }
@@ -429,9 +436,9 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
               if (!g.store_y) continue;
             }
             if (OSZ == 1)
-              Cb[(long long)m * g.ldc + n + e] = (int8_t)v[e];
+              Cb[cpos(g, m, n) + e] = (int8_t)v[e];
             else
-              reinterpret_cast<int16_t*>(Cb)[(long long)m * g.ldc + n + e] = (int16_t)v[e];
+              reinterpret_cast<int16_t*>(Cb)[cpos(g, m, n) + e] = (int16_t)v[e];
           }
         }
       }
@@ -734,10 +741,9 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
       }
       if (!g.store_y) return;
     }
-    char* Cr = Cb + ((long long)m0 * g.ldc + n0) * OSZ;
 #pragma unroll
     for (int pass = 0; pass < PASSES; ++pass)
-      *reinterpret_cast<v4i*>(Cr + ((long long)rr_of(pass) * g.ldc + cf_of(pass)) * OSZ) = ch[pass];
+      *reinterpret_cast<v4i*>(Cb + cpos(g, m0 + rr_of(pass), n0 + cf_of(pass)) * OSZ) = ch[pass];
     return;
   }
 #pragma unroll
@@ -773,7 +779,7 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
       }
       if (!g.store_y) continue;
     }
-    char* dst = Cb + ((long long)m * g.ldc + n0 + cfirst) * OSZ;
+    char* dst = Cb + cpos(g, m, n0 + cfirst) * OSZ;
     if (g.vec_store && cfirst + 16 / OSZ <= cols_valid) {
       *reinterpret_cast<v4i*>(dst) = *reinterpret_cast<const v4i*>(src);
     } else {
@@ -837,7 +843,7 @@ __global__ __launch_bounds__(G_THREADS) void splitk_reduce(GemmArgs g) {
       v[e] = min(max(x >> g.shift, lo), hi);
       if (lut) v[e] = lut_s[v[e] + 128];
     }
-    char* c = Cb + ((long long)m * g.ldc + n) * OSZ;
+    char* c = Cb + cpos(g, m, n) * OSZ;
     if (OSZ == 1 && g.vec_store && n + 3 < g.N) {
       *reinterpret_cast<unsigned*>(c) = pack4(v[0], v[1], v[2], v[3]);
     } else {
@@ -1294,15 +1300,18 @@ static int gemm_validate(const int8_t* A, const int8_t* Bt, const void* C, int b
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: result dtype must be i8 or i16");
   if (lut && out_dtype != ANVIL_I8) return set_error(ANVIL_E_VALUE, "a LUT epilogue needs an i8 result");
   if (flags & ~(ANVIL_GEMM_UNCHECKED | ANVIL_GEMM_CAUSAL_SKIP | ANVIL_GEMM_CAUSAL_K | ANVIL_GEMM_MUL24 |
-                ANVIL_GEMM_SPLITK | ANVIL_GEMM_A_KBLOCK | ANVIL_GEMM_B_KBLOCK))
+                ANVIL_GEMM_SPLITK | ANVIL_GEMM_A_KBLOCK | ANVIL_GEMM_B_KBLOCK | ANVIL_GEMM_C_KBLOCK))
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: unknown flags %d", flags);
-  for (int o = 0; o < 2; ++o) {                          // K-blocked operands: block stride and reach
-    if (!(flags & (o ? ANVIL_GEMM_B_KBLOCK : ANVIL_GEMM_A_KBLOCK))) continue;
-    const long long kb = strides[o ? 5 : 2];
+  for (int o = 0; o < 3; ++o) {                          // K-blocked operands and result: block stride and reach
+    const int flag = o == 0 ? ANVIL_GEMM_A_KBLOCK : (o == 1 ? ANVIL_GEMM_B_KBLOCK : ANVIL_GEMM_C_KBLOCK);
+    if (!(flags & flag)) continue;
+    const long long kb = strides[2 + 3 * o];
+    const int blocks = ((o == 2 ? N : K) + 63) / 64;
     if (!(flags & ANVIL_GEMM_UNCHECKED))
       return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: K-blocked operands need ANVIL_GEMM_UNCHECKED");
-    if (kb < 64 || kb % 16 || (long long)((K + 63) / 64) * kb + 256ll * 64 >= (1ll << 31))
-      return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: K-block stride %lld of %s out of range", kb, o ? "Bt" : "A");
+    if (kb < 64 || kb % 16 || (long long)blocks * kb + 256ll * 64 >= (1ll << 31))
+      return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: K-block stride %lld of %s out of range", kb,
+                       o == 0 ? "A" : (o == 1 ? "Bt" : "C"));
   }
   if ((flags & ANVIL_GEMM_SPLITK) && (!(flags & ANVIL_GEMM_UNCHECKED) ||
                                       (flags & (ANVIL_GEMM_CAUSAL_SKIP | ANVIL_GEMM_CAUSAL_K)) || add ||
@@ -1349,6 +1358,8 @@ static int gemm_prepare(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void*
   g.sc0 = strides[6];
   g.sc1 = strides[7];
   g.ldc = strides[8];
+  g.kbc = 64;
+  if (flags & ANVIL_GEMM_C_KBLOCK) g.kbc = g.ldc, g.ldc = 64;
   g.mult = mult;
   g.shift = shift;
   g.rnd = shift ? (int)(1u << (shift - 1)) : 0;
@@ -1388,7 +1399,7 @@ static int gemm_prepare(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void*
   p.fast = fast;
   p.mul24 = (flags & ANVIL_GEMM_MUL24) != 0;
   p.force_split = (flags & ANVIL_GEMM_SPLITK) != 0;
-  if ((flags & (ANVIL_GEMM_A_KBLOCK | ANVIL_GEMM_B_KBLOCK)) && !fast)
+  if ((flags & (ANVIL_GEMM_A_KBLOCK | ANVIL_GEMM_B_KBLOCK | ANVIL_GEMM_C_KBLOCK)) && !fast)
     return set_error(ANVIL_E_VALUE, "anvil_gemm_i8: K-blocked operands need 16-byte aligned operands with K a multiple "
                                     "of 16 (and no benchmarking override)");
   if (p.force_split && !fast)

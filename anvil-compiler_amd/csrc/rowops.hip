@@ -189,9 +189,13 @@ template <bool S24>
 __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
                                                            const int* __restrict__ lut, int lut_len, int mult,
                                                            int shift, long long rows, int cols,
-                                                           int8_t* __restrict__ out) {
+                                                           int8_t* __restrict__ out, int kbo) {
   const int lane = threadIdx.x & 63;
   const bool active = lane < (cols >> 4);
+  // kbo: the output K-blocked (64-byte blocks of consecutive rows, block stride kbo bytes), stored through one buffer
+  // over the whole output with rows past the end sent out of range
+  const __amdgpu_buffer_rsrc_t wall = uniform_rsrc(out, kbo ? (int)(rows * cols) : 0);
+  const unsigned kcol = (unsigned)((lane >> 2) * kbo + 16 * (lane & 3));
   v4i wv = {0, 0, 0, 0};
   if (active) wv = *reinterpret_cast<const v4i*>(w + 16 * lane);
   // this lane's 16 weights, sign-extended once
@@ -256,8 +260,9 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
         }
         o[q] = (int)sra_pack4(y[0], y[1], y[2], y[3], s);
       }
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o), ws,
-                                             off[j], 0, 0);
+      const unsigned ko = active && r0 + j < rows ? kcol + (unsigned)((r0 + j) * 64) : OOB;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o),
+                                             kbo ? wall : ws, kbo ? ko : off[j], 0, 0);
     }
   };
   // two row-group buffers in turn (the loop unrolled by two), so a group's rows are never copied between registers
@@ -311,9 +316,13 @@ __device__ __forceinline__ int mad_i24v(int a, int b, int c) {
 template <int CH>
 __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
                                                              const int* __restrict__ lut, int lut_len, int mult,
-                                                             int shift, long long rows, int8_t* __restrict__ out) {
+                                                             int shift, long long rows, int8_t* __restrict__ out,
+                                                             int kbo) {
   constexpr int COLS = 256 * CH;
   const int lane = threadIdx.x & 63, rr = lane >> 4, sub = lane & 15;
+  // kbo: the output K-blocked, as in rmsnorm_fast; chunk 16 c + sub of a row is in block 4 c + sub / 4
+  const __amdgpu_buffer_rsrc_t wall = uniform_rsrc(out, kbo ? (int)(rows * COLS) : 0);
+  const unsigned kcol = (unsigned)((sub >> 2) * kbo + 16 * (sub & 3));
   v4i wv[CH];                                                   // this lane's weights, packed (each multiply
 #pragma unroll                                                  // selects and sign-extends its byte)
   for (int c = 0; c < CH; ++c) wv[c] = *reinterpret_cast<const v4i*>(w + 16 * (16 * c + sub));
@@ -371,8 +380,9 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
         const int y3 = med3i(mad_i24v(mul_sbytes<3>(xd, wd), rm, rnd), lo, hi);
         o[q] = (int)sra_pack4v(y0, y1, y2, y3, sh);
       }
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o), ws,
-                                             off[c], 0, 0);
+      const unsigned ko = r0 + rr < rows ? kcol + (unsigned)(4 * c * kbo + (r0 + rr) * 64) : OOB;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o),
+                                             kbo ? wall : ws, kbo ? ko : off[c], 0, 0);
     }
   };
   long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * 4;
@@ -449,7 +459,7 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_wide_fast(const int16_t* __
                                                                 const int8_t* __restrict__ w,
                                                                 const int* __restrict__ lut, int lut_len, int mult,
                                                                 int shift, int c, int e, int s24, long long rows,
-                                                                int cols, int8_t* __restrict__ out) {
+                                                                int cols, int8_t* __restrict__ out, int kbo) {
   static_assert(CH == 1 || L == 64, "several chunks a lane only with a whole wave a row");
   constexpr int RW = 64 / L;                                     // rows a wave holds at once
   extern __shared__ int wide_lut[];
@@ -465,7 +475,8 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_wide_fast(const int16_t* __
   const int lane = threadIdx.x & 63, rr = lane / L, sub = lane % L;
   const int n = cols >> 3;                                       // 16-byte chunks of x a row
   v2i wv[CH];
-  unsigned xoff[CH], ooff[CH];
+  unsigned xoff[CH], ooff[CH], kcol[CH];
+  const __amdgpu_buffer_rsrc_t wall = uniform_rsrc(out, kbo ? (int)(rows * cols) : 0);
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
     const int ch = k * L + sub;
@@ -473,6 +484,7 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_wide_fast(const int16_t* __
     wv[k] = on ? *reinterpret_cast<const v2i*>(w + 8 * ch) : v2i{0, 0};
     xoff[k] = on ? (unsigned)(rr * 2 * cols + 16 * ch) : OOB;
     ooff[k] = on ? (unsigned)(rr * cols + 8 * ch) : OOB;
+    kcol[k] = on ? (unsigned)((ch >> 3) * kbo + 8 * (ch & 7)) : OOB;   // K-blocked output: 8 chunks a block
   }
   const int rc = c ? 1 << (c - 1) : 0;
   const long long step = (long long)gridDim.x * R_WAVES * RW;
@@ -530,8 +542,9 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_wide_fast(const int16_t* __
         for (int j = 0; j < 8; ++j) y[j] = med3i((int)((unsigned)xw[j] * (unsigned)rm + (unsigned)rnd), lo, hi);
       }
       const v2i o = {(int)sra_pack4v(y[0], y[1], y[2], y[3], sh), (int)sra_pack4v(y[4], y[5], y[6], y[7], sh)};
-      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, o), ws,
-                                            ooff[k], 0, 0);
+      const unsigned ko = kcol[k] != OOB && r0 + rr < rows ? kcol[k] + (unsigned)((r0 + rr) * 64) : OOB;
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, o),
+                                            kbo ? wall : ws, kbo ? ko : ooff[k], 0, 0);
     }
   };
   long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * RW;
@@ -561,7 +574,7 @@ template <typename T>
 __global__ __launch_bounds__(R_THREADS) void rmsnorm_kernel(const T* __restrict__ x, const int8_t* __restrict__ w,
                                                              const int* __restrict__ lut, int lut_len, int mult,
                                                              int shift, int c, int e, long long rows, int cols,
-                                                             int8_t* __restrict__ out, unsigned* flags) {
+                                                             int8_t* __restrict__ out, unsigned* flags, int kbo) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -593,7 +606,11 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_kernel(const T* __restrict_
   for (int j = lane; j < cols; j += 64) {
     const long long xwr = (long long)xr[j] * w[j] * r;
     bad |= (xwr < I32_MIN) | (xwr > I32_MAX);
-    o[j] = (int8_t)requant_checked((int)xwr, mult, sh, rnd, -128, 127, bad);
+    const int8_t y = (int8_t)requant_checked((int)xwr, mult, sh, rnd, -128, 127, bad);
+    if (kbo)
+      out[(long long)(j >> 6) * kbo + row * 64 + (j & 63)] = y;   // K-blocked output
+    else
+      o[j] = y;
   }
   if (bad) raise_flag(flags, FLAG_OVERFLOW);
 }
@@ -668,8 +685,12 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
   if (shift < 0 || shift > 31) return set_error(ANVIL_E_VALUE, "shift %d outside [0, 31]", shift);
   if (ss_shift < 0 || ss_shift > 30) return set_error(ANVIL_E_VALUE, "ss_shift %d outside [0, 30]", ss_shift);
   if (ss_init < 0) return set_error(ANVIL_E_VALUE, "ss_init %d negative", ss_init);
-  if (flags & ~(ANVIL_OP_UNCHECKED | ANVIL_RMS_S24))
+  if (flags & ~(ANVIL_OP_UNCHECKED | ANVIL_RMS_S24 | ANVIL_RMS_OUT_KBLOCK))
     return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: unknown flags %d", flags);
+  if ((flags & ANVIL_RMS_OUT_KBLOCK) && (cols % 64 || rows * cols >= (1ll << 31)))
+    return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: a K-blocked result needs cols %% 64 == 0 and rows x cols "
+                                    "below 2^31 (cols %d)", cols);
+  const int kbo = (flags & ANVIL_RMS_OUT_KBLOCK) ? (int)(rows * 64) : 0;   // block stride of a K-blocked result
   if ((flags & ANVIL_RMS_S24) && !(flags & ANVIL_OP_UNCHECKED))
     return set_error(ANVIL_E_VALUE, "anvil_rmsnorm_int: ANVIL_RMS_S24 needs ANVIL_OP_UNCHECKED");
   if (int r = check_ctx(ctx)) return r;
@@ -686,7 +707,7 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
     if ((flags & ANVIL_RMS_S24) && cols % 256 == 0 && ch <= 4) {      // rows of 256, 512, 768 or 1024 bytes
       auto launch = [&](auto kernel) {
         ANVIL_LAUNCH(kernel, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len, mult,
-                           shift, (long long)rows, out);
+                           shift, (long long)rows, out, kbo);
       };
       if (ch == 1) launch(rmsnorm_rows16<1>);
       else if (ch == 2) launch(rmsnorm_rows16<2>);
@@ -694,10 +715,10 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
       else launch(rmsnorm_rows16<4>);
     } else if (flags & ANVIL_RMS_S24)
       ANVIL_LAUNCH(rmsnorm_fast<true>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
-                         mult, shift, (long long)rows, cols, out);
+                         mult, shift, (long long)rows, cols, out, kbo);
     else
       ANVIL_LAUNCH(rmsnorm_fast<false>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
-                         mult, shift, (long long)rows, cols, out);
+                         mult, shift, (long long)rows, cols, out, kbo);
   } else if ((flags & ANVIL_OP_UNCHECKED) && x_dtype == ANVIL_I16 && cols % 8 == 0 && cols <= 2048 &&
              lut_len <= WIDE_LUT_MAX && al16(x) && al8(w) && al8(out)) {
     const int n = cols / 8;                                     // 16-byte chunks a row
@@ -708,7 +729,7 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
     const int s24 = (flags & ANVIL_RMS_S24) ? 1 : 0;
     auto launch = [&](auto kernel) {
       ANVIL_LAUNCH(kernel, grid, dim3(R_THREADS), 4 * lut_len, ctx->stream, (const int16_t*)x, w, lut, lut_len, mult,
-                   shift, ss_shift, ss_init, s24, (long long)rows, cols, out);
+                   shift, ss_shift, ss_init, s24, (long long)rows, cols, out, kbo);
     };
     switch (n > 64 ? 64 * ((n + 63) / 64) : L) {
       case 1: launch(rmsnorm_wide_fast<1, 1>); break;
@@ -725,11 +746,11 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
   } else if (x_dtype == ANVIL_I8) {
     ANVIL_LAUNCH(rmsnorm_kernel<int8_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
                        (const int8_t*)x, w, lut, lut_len, mult, shift, ss_shift, ss_init, (long long)rows, cols, out,
-                       ctx->flags);
+                       ctx->flags, kbo);
   } else {
     ANVIL_LAUNCH(rmsnorm_kernel<int16_t>, dim3((unsigned)blocks), dim3(R_THREADS), 0, ctx->stream,
                        (const int16_t*)x, w, lut, lut_len, mult, shift, ss_shift, ss_init, (long long)rows, cols,
-                       out, ctx->flags);
+                       out, ctx->flags, kbo);
   }
   ANVIL_LAUNCHED();
   return ANVIL_OK;

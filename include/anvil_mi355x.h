@@ -100,6 +100,8 @@ int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, in
  *                           64 j + 63) sits at A + r * 64 + j * strides[2] (plus the batch strides), so one block of
  *                           consecutive rows is contiguous and a tile's operand loads read whole cache lines.
  *   ANVIL_GEMM_B_KBLOCK     (with UNCHECKED) the same for Bt, with strides[5] the block stride.
+ *   ANVIL_GEMM_C_KBLOCK     (with UNCHECKED) the result is written K-blocked, for a product that reads it as its A
+ *                           operand: result (m, n) at C + (m * 64 + (n / 64) * strides[8] + n % 64) * itemsize.
  *                           Both need 16-byte aligned operands, K a multiple of 16 and a block stride that is a
  *                           multiple of 16; the results are those of the row-major operands. */
 enum anvil_gemm_flags {
@@ -109,7 +111,8 @@ enum anvil_gemm_flags {
   ANVIL_GEMM_MUL24 = 8,
   ANVIL_GEMM_SPLITK = 16,
   ANVIL_GEMM_A_KBLOCK = 32,
-  ANVIL_GEMM_B_KBLOCK = 64
+  ANVIL_GEMM_B_KBLOCK = 64,
+  ANVIL_GEMM_C_KBLOCK = 128
 };
 int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
@@ -171,8 +174,10 @@ enum anvil_op_flags { ANVIL_OP_UNCHECKED = 1 };
 
 /* anvil_rmsnorm_int with flags (same reference op, anvil/semantics.py:158-182). ANVIL_RMS_S24 (with
  * ANVIL_OP_UNCHECKED) adds that every |lut[i] * mult| is below 2^23: each element's x w lut[i] mult + rnd is then one
- * 24-bit multiply-add. */
-enum anvil_rms_flags { ANVIL_RMS_S24 = 2 };
+ * 24-bit multiply-add. ANVIL_RMS_OUT_KBLOCK writes the result K-blocked for a GEMM that reads it as a K-blocked
+ * operand (ANVIL_GEMM_A_KBLOCK / B_KBLOCK with block stride rows * 64): out_j of row r at out + (j / 64) * rows * 64 +
+ * r * 64 + j % 64; cols must be a multiple of 64. */
+enum anvil_rms_flags { ANVIL_RMS_S24 = 2, ANVIL_RMS_OUT_KBLOCK = 4 };
 int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, const int8_t* w, const int32_t* lut,
                          int lut_len, int32_t mult, int shift, int ss_shift, int32_t ss_init, int64_t rows, int cols,
                          int8_t* out, int flags);

@@ -62,7 +62,7 @@ def test_gemm_argument_validation_precedes_the_device():
     with pytest.raises(ValueError, match="SPLITK needs UNCHECKED"):
         gemm(2, 1, 16, 16, 16, st, 1, 3, None, 1, 17)
     with pytest.raises(ValueError, match="unknown flags"):
-        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 128)
+        gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 256)
     with pytest.raises(ValueError, match="K-blocked operands need ANVIL_GEMM_UNCHECKED"):
         gemm(1, 1, 16, 16, 16, st, 1, 3, None, 1, 32)
     with pytest.raises(ValueError, match="K-block stride 16 of Bt out of range"):
@@ -114,9 +114,12 @@ def test_attention_argument_validation_precedes_the_device():
 def test_rmsnorm_flag_validation_precedes_the_device():
     lib = rt.library()
     p = C.c_void_p(4096)
-    rms = lambda flags: lib.call("anvil_rmsnorm_int_ex", None, p, 1, p, p, 1024, 1, 14, 0, 0, 4, 768, p, flags)  # noqa: E731
+    rms = lambda flags, cols=768: lib.call("anvil_rmsnorm_int_ex", None, p, 1, p, p, 1024, 1, 14, 0, 0, 4, cols, p,  # noqa: E731
+                                           flags)
     with pytest.raises(ValueError, match="unknown flags"):
-        rms(4)
+        rms(8)
+    with pytest.raises(ValueError, match="K-blocked result needs cols % 64"):
+        rms(rt.OP_UNCHECKED | rt.RMS_OUT_KBLOCK, 80)
     with pytest.raises(ValueError, match="needs ANVIL_OP_UNCHECKED"):
         rms(rt.RMS_S24)
     with pytest.raises(ValueError, match="null context"):

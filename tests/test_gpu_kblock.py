@@ -1,4 +1,5 @@
-"""K-blocked GEMM operands (ANVIL_GEMM_A_KBLOCK / ANVIL_GEMM_B_KBLOCK): row r's 64-byte K block j at r * 64 + j * stride.
+"""K-blocked GEMM operands and results (ANVIL_GEMM_A_KBLOCK / B_KBLOCK / C_KBLOCK): row r's 64-element block j at
+r * 64 + j * stride.
 Every fast kernel family reads them (256 x 128 and 128 x 128 tiles, 256 x 192, the three persistent forms, split-K, the
 fused residual add, batched and grouped products), with a last K block that is partial and padding rows between
 blocks; the results equal the oracle's (reference op: anvil/semantics.py:95-103) on sampled rows."""
@@ -49,6 +50,17 @@ def _operands(dev, a, wt, mode, rng):
     return A, B, lda, ldb, flags
 
 
+def _result(dev, M, N, dtype, mode):
+    """The result buffer (K-blocked with two pad rows when "C" is in the mode), strides[8], its flag, and a reader."""
+    if "C" not in mode:
+        c = dev.alloc(M * N * rt.ITEMSIZE[dtype])
+        return c, N, 0, lambda: c.download((M, N), rt.NP_DTYPE[dtype])
+    nb, rows = -(-N // 64), M + 2
+    c = dev.alloc(nb * rows * 64 * rt.ITEMSIZE[dtype])
+    read = lambda: c.download((nb, rows, 64), rt.NP_DTYPE[dtype])[:, :M].transpose(1, 0, 2).reshape(M, -1)[:, :N]  # noqa
+    return c, rows * 64, rt.GEMM_C_KBLOCK, read
+
+
 def _check(dev, M, N, K, mode, seed, lut=False, dtype="i8", add=False):
     rng = np.random.default_rng([71, M, N, K, seed])
     a, w = rng.integers(-128, 128, (M, K), dtype=np.int8), rng.integers(-128, 128, (K, N), dtype=np.int8)
@@ -58,9 +70,9 @@ def _check(dev, M, N, K, mode, seed, lut=False, dtype="i8", add=False):
     m = int(min(((1 << 31) - 1 - (1 << (s - 1))) // int(np.abs(acc).max() * 2 + 1), (1 << 23) - 1))
     L = rng.integers(-128, 128, 256) if lut else None
     A, B, lda, ldb, flags = _operands(dev, a, np.ascontiguousarray(w.T), mode, rng)
-    flags |= rt.GEMM_UNCHECKED | rt.GEMM_MUL24
-    c = dev.alloc(M * N * rt.ITEMSIZE[dtype])
-    st = [0, 0, lda, 0, 0, ldb, 0, 0, N]
+    c, ldc, cflag, read = _result(dev, M, N, dtype, mode)
+    flags |= rt.GEMM_UNCHECKED | rt.GEMM_MUL24 | cflag
+    st = [0, 0, lda, 0, 0, ldb, 0, 0, ldc]
     y = sem.qmatmul(a[rows].astype(np.int64), w.astype(np.int64), m, s, L, dtype=dtype, fast=True)
     if add:
         r = rng.integers(-128, 128, (M, N), dtype=np.int8)
@@ -69,7 +81,7 @@ def _check(dev, M, N, K, mode, seed, lut=False, dtype="i8", add=False):
     else:
         dev.gemm_i8(A, B, c, 1, 1, M, N, K, st, m, s, None if L is None else up(dev, L), dtype, flags)
     dev.sync()
-    got = c.download((M, N), rt.NP_DTYPE[dtype])[rows].astype(np.int64)
+    got = read()[rows].astype(np.int64)
     assert np.array_equal(got, y), (mode, np.argwhere(got != y)[:5])
     if add:
         want = sem.add_requant(r[rows].astype(np.int64), y, 300, -200, 9)
@@ -83,7 +95,7 @@ SHAPES = [(300, 200, 80), (32768, 768, 768), (32768, 3072, 768), (32768 + 37, 76
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
-@pytest.mark.parametrize("mode", ["A", "B", "AB"])
+@pytest.mark.parametrize("mode", ["A", "B", "AB", "C", "ABC"])
 def test_kblocked_operands_match_the_oracle(dev, M, N, K, mode):
     _check(dev, M, N, K, mode, 0)
 
@@ -92,11 +104,14 @@ def test_kblocked_operands_match_the_oracle(dev, M, N, K, mode):
 def test_kblocked_operands_with_the_fused_add(dev, M, N, K):
     """The block's y and proj shapes with their residual add in the epilogue, both operands K-blocked."""
     _check(dev, M, N, K, "AB", 1, add=True)
+    _check(dev, M, N, K, "ABC", 4, add=True)          # y stored K-blocked beside the row-major sum
 
 
 def test_kblocked_operands_lut_and_i16(dev):
     _check(dev, 4096 + 9, 640, 1024 + 16, "AB", 2, lut=True)
     _check(dev, 4096 + 9, 640, 1024 + 16, "AB", 3, dtype="i16")
+    _check(dev, 4096 + 9, 640 + 16, 1024 + 16, "ABC", 5, lut=True)
+    _check(dev, 4096 + 9, 640 + 16, 1024 + 16, "ABC", 6, dtype="i16")
 
 
 def test_kblocked_batched_and_grouped(dev):
@@ -138,3 +153,32 @@ def test_kblocked_batched_and_grouped(dev):
     for o, wi in zip(outs, ws):
         want = sem.qmatmul(x[rows].astype(np.int64), wi.astype(np.int64), 5, 18, fast=True)
         assert np.array_equal(o.download((M2, 768), np.int8)[rows].astype(np.int64), want)
+
+
+@pytest.mark.parametrize("xdt,d,flags", [("i8", 768, rt.OP_UNCHECKED | rt.RMS_S24), ("i8", 256, rt.OP_UNCHECKED | rt.RMS_S24),
+                                         ("i8", 320, rt.OP_UNCHECKED | rt.RMS_S24), ("i8", 768, rt.OP_UNCHECKED),
+                                         ("i8", 192, 0), ("i16", 64, rt.OP_UNCHECKED), ("i16", 768, rt.OP_UNCHECKED),
+                                         ("i16", 128, 0)])
+@pytest.mark.parametrize("rows", [203, 8 * 4 * 256 * 4 * 2 + 3])
+def test_rmsnorm_kblocked_result(dev, xdt, d, flags, rows):
+    """ANVIL_RMS_OUT_KBLOCK on every rmsnorm kernel (16 lanes a row, four rows a wave, the wide int16 form and the
+    checked one): the result K-blocked, block stride rows * 64, equal to the oracle's rows; ragged row counts, and
+    more row groups than the grid has waves."""
+    from anvil_mi355x import quantize as Q
+    rng = np.random.default_rng([73, d, rows, flags])
+    w = rng.integers(-127, 128, d)
+    if xdt == "i8":
+        lut, s = Q.rsqrt_table(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
+        c = e = 0
+        x = rng.integers(-128, 128, (rows, d))
+        want = sem.rmsnorm_int(x, w, lut, 1, s)
+    else:
+        lut, s, c, e = Q.wide_rsqrt_table(4e-4, 0.01, 0.02, int(np.abs(w).max()), d, 1e-6, 1 << 15)
+        x = rng.integers(-(1 << 15), 1 << 15, (rows, d))
+        want = sem.rmsnorm_wide(x, w, lut, 1, s, c, e, "i16")
+    out = dev.alloc(rows * d)
+    dev.rmsnorm_int(up(dev, x, xdt), xdt, up(dev, w), up(dev, lut, "i32"), len(lut), 1, s, c, e, rows, d, out,
+                    flags | rt.RMS_OUT_KBLOCK)
+    dev.sync()
+    got = out.download((d // 64, rows, 64), np.int8).transpose(1, 0, 2).reshape(rows, d).astype(np.int64)
+    assert np.array_equal(got, want)
