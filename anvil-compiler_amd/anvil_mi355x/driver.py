@@ -113,6 +113,14 @@ class _Plan:
         b = self.buf(math.prod(dims) * rt.ITEMSIZE[dtype], name)
         return View(b, dtype, dims, contig_strides(dims))
 
+    def kblocked(self, dims, dtype, name=""):
+        """Storage for a value read only as a GEMM operand: the last dim in 64-element blocks, each block holding
+        all rows consecutively (block stride rows * 64)."""
+        dims = tuple(int(d) for d in dims)
+        b = self.buf(math.prod(dims) * rt.ITEMSIZE[dtype], name)
+        lead = contig_strides(dims[:-1])
+        return View(b, dtype, dims, tuple(64 * x for x in lead) + (1,), kb=64 * math.prod(dims[:-1]))
+
 
 class CompiledModel:
     """A graph compiled for the mi355x backend: consts resident on the device, plans per batch size."""
@@ -151,6 +159,7 @@ class CompiledModel:
         self._const_views = {}
         self._const_bt = {}
         self._const_kb = {}
+        self._kb_values = set()
         self._const_bt_host = {}
         self._plans = {}
         self.group_gemms = True           # independent consecutive GEMMs as one anvil_gemm_i8_group call
@@ -269,6 +278,7 @@ class CompiledModel:
         fused = self._attention_chains(keep)
         skip = {o for s_op, sm in fused.values() for o in (s_op, sm)}
         adds = self._residual_fusions(keep)
+        self._kb_values = self._kblocked_values(keep, fused, skip, adds)
         for op in self.ops:
             if op in skip or op in P.fused_adds:
                 continue
@@ -304,7 +314,7 @@ class CompiledModel:
             if isinstance(op, g.SoftmaxLutOp):
                 views[r] = self._plan_softmax(P, op, views, out_dims, label, dense, step)
                 continue
-            out = P.dense(out_dims, t.dtype, label)
+            out = P.kblocked(out_dims, t.dtype, label) if r in self._kb_values else P.dense(out_dims, t.dtype, label)
             views[r] = out
             if isinstance(op, g.RmsNormIntOp):
                 x = dense(views[op.x], label + ".x")
@@ -315,6 +325,8 @@ class CompiledModel:
                 lut_vals = self._const_array(op.lut)
                 if flags and lut_vals is not None and int(np.abs(lut_vals).max()) * abs(int(op.M)) < (1 << 23):
                     flags |= rt.RMS_S24                          # x w (lut M) + rnd as one 24-bit multiply-add
+                if out.kb:
+                    flags |= rt.RMS_OUT_KBLOCK
                 step(label, _call_ptrs, dev.rmsnorm_int, [x, g.qt(op.x).dtype, w, lut, lut.size, int(op.M),
                                                           int(op.s), op.ss_shift_int, op.ss_init_int, rows,
                                                           x.dims[-1], out, flags])
@@ -436,6 +448,8 @@ class CompiledModel:
         """Dense storage of a matmul result in its chosen physical order, viewed in the logical order."""
         t = g.qt(op.result)
         perm = self.phys.get(op.result)
+        if op.result in self._kb_values:
+            return P.kblocked(out_dims, t.dtype, label)
         if perm is None:
             return P.dense(out_dims, t.dtype, label)
         k = 0 if op.result in self.is_const else 1
@@ -466,7 +480,7 @@ class CompiledModel:
 
     def _bt_kblocked(self, op):
         """The same transposed const (N, K), K-blocked for the fast GEMM kernels: (ceil(K / 64), N, 64), row n's K block j
-        at j N 64 + n 64. Returns (view of the buffer, block stride in bytes)."""
+        at j N 64 + n 64, as a K-blocked view."""
         key = op.b
         if key not in self._const_kb:
             bt = self._bt_const(op)
@@ -477,32 +491,64 @@ class CompiledModel:
             mem = self.dev.upload(kb)
             b = Buf(mem.nbytes, f"{op.sym_str}.Bt.kblocked")
             b.mem = mem
-            self._const_kb[key] = (View(b, "i8", (N, K), (64, 1)), N * 64)
+            self._const_kb[key] = View(b, "i8", (N, K), (64, 1), kb=N * 64)
         return self._const_kb[key]
 
     def dev_download_const(self, bt):
         """Host copy of a const operand view made by _bt_const (kept on the host when it was uploaded)."""
         return self._const_bt_host[id(bt.buf)]
 
-    def _kblock_weight(self, op, rows1, rows2, strides, flags, K, swapped):
+    def _kblock_weight(self, op, rows1, rows2, strides, K, swapped):
         """Proven 2-D products whose const right operand is read through _bt_const take its K-blocked copy: the
         operand's loads then fetch whole 64-byte blocks of consecutive rows, where row-major rows give 64-byte pieces
-        of separate lines. Only for the fast kernels (proven, K and the other operand's row stride multiples of 16);
-        returns (rows1, rows2, strides, flags) for the call."""
-        if not (flags & rt.GEMM_UNCHECKED) or K % 16 or op.b not in self._const_bt:
-            return rows1, rows2, strides, flags
+        of separate lines. Only for the fast kernels (proven, K and the other operand's strides multiples of 16);
+        returns (rows1, rows2) for the call (_kb_call then sets the strides and flags)."""
+        if not self.proven or K % 16 or op.b not in self._const_bt:
+            return rows1, rows2
         if (rows1 if swapped else rows2).buf is not self._const_bt[op.b].buf:
-            return rows1, rows2, strides, flags
+            return rows1, rows2
         other = rows2 if swapped else rows1
         if any(v % 16 for v in (strides[3:6] if swapped else strides[0:3])) or (other.offset * other.itemsize) % 16:
-            return rows1, rows2, strides, flags
-        kv, kb = self._bt_kblocked(op)
+            return rows1, rows2
+        kv = self._bt_kblocked(op)
+        return (kv, rows2) if swapped else (rows1, kv)
+
+    @staticmethod
+    def _kb_call(rows1, rows2, c, strides, flags):
+        """Strides and flags of a GEMM call for its operands' and result's layouts: a K-blocked view passes its block
+        stride in place of its row stride, with the ANVIL_GEMM_*_KBLOCK flag."""
         strides = list(strides)
-        if swapped:
-            strides[2] = kb
-            return kv, rows2, strides, flags | rt.GEMM_A_KBLOCK
-        strides[5] = kb
-        return rows1, kv, strides, flags | rt.GEMM_B_KBLOCK
+        if rows1.kb:
+            strides[2], flags = rows1.kb, flags | rt.GEMM_A_KBLOCK
+        if rows2.kb:
+            strides[5], flags = rows2.kb, flags | rt.GEMM_B_KBLOCK
+        if c is not None and c.kb:
+            strides[8], flags = c.kb, flags | rt.GEMM_C_KBLOCK
+        return strides, flags
+
+    def _kblocked_values(self, keep, fused, skip, adds) -> set:
+        """Values stored K-blocked in this plan: int8 results of an rmsnorm or of a plain linear product (a 2-D const
+        right operand, stored unpermuted, no fused add) that are read only as the left operand of plain linear
+        products and not returned (keep="outputs"), in a proven graph, with a last dim that is a multiple of 64.
+        Their readers then load whole 64-byte blocks of consecutive rows (ANVIL_GEMM_*_KBLOCK)."""
+        if keep != "outputs" or not self.proven:
+            return set()
+        fused_ops = set(fused) | skip
+
+        def linear(op):
+            return (isinstance(op, (g.QMatmulOp, g.QLinearOp)) and op.b in self.is_const
+                    and len(g.qt(op.b).dims) == 2 and op not in fused_ops)
+        out = set()
+        for op in self.ops:
+            r = op.results[0] if op.results else None
+            if r is None or r in self.output_values or r in self.is_const or g.qt(r).dtype != "i8":
+                continue
+            producer = isinstance(op, g.RmsNormIntOp) or (linear(op) and op not in adds and r not in self.phys)
+            users = self.users.get(r, [])
+            if (producer and g.qt(r).dims[-1] % 64 == 0 and users
+                    and all(linear(u) and u.a is r and u.b is not r for u in users)):
+                out.add(r)
+        return out
 
     def _host_const(self, value):
         op = value.owner
@@ -583,7 +629,8 @@ class CompiledModel:
                 if add is not None and self._plan_fused_add(P, op, add, views, r1, rows2, c2, strides, lut, flags,
                                                             label, step, keep):
                     return out
-                r1, rows2, strides, flags = self._kblock_weight(op, r1, rows2, strides, flags, K, swapped)
+                r1, rows2 = self._kblock_weight(op, r1, rows2, strides, K, swapped)
+                strides, flags = self._kb_call(r1, rows2, c2, strides, flags)
                 step(label, _call_gemm, self.dev, r1, rows2, c2, 1, 1, r1.dims[0], Nx, K, strides, op, lut, t.dtype,
                      flags)
                 return out
@@ -603,7 +650,8 @@ class CompiledModel:
             merged.insert(0, (1, 0, 0, 0))
         (b0, sa0, sb0, sc0), (b1, sa1, sb1, sc1) = merged
         strides = [sa0, sa1, rows1.strides[-2], sb0, sb1, rows2.strides[-2], sc0, sc1, c.strides[-2]]
-        rows1, rows2, strides, flags = self._kblock_weight(op, rows1, rows2, strides, flags, K, swapped)
+        rows1, rows2 = self._kblock_weight(op, rows1, rows2, strides, K, swapped)
+        strides, flags = self._kb_call(rows1, rows2, c, strides, flags)
         step(label, _call_gemm, self.dev, rows1, rows2, c, b0, b1, Mx, Nx, K, strides, op, lut, t.dtype, flags)
         return out
 
@@ -623,7 +671,8 @@ class CompiledModel:
         store_y = keep == "all" or op.result in self.output_values or len(self.users.get(op.result, [])) > 1
         ma, mb = (int(add.Mb), int(add.Ma)) if y_first else (int(add.Ma), int(add.Mb))   # (residual, y)
         rstrides = [0, 0, rv.strides[0], 0, 0, d.strides[0]]
-        a2, bt, strides, flags = self._kblock_weight(op, a2, bt, strides, flags, K, False)
+        a2, bt = self._kblock_weight(op, a2, bt, strides, K, False)
+        strides, flags = self._kb_call(a2, bt, c2 if store_y else None, strides, flags)
         step(label, _call_gemm_add, self.dev, a2, bt, c2 if store_y else None, rows, N, K, strides, op, lut, rv, ma,
              mb, int(add.s), d, rstrides, flags)
         views[add.result] = d.reshape(tuple(views[other].dims))
@@ -887,6 +936,8 @@ def _copy_view(dev, src: View, dst: View):
 
 
 def _dense_copy_into(P, step, dev, src: View, label):
+    if src.kb:
+        raise RuntimeError(f"{label}: a K-blocked value has no strided copy (it is planned for GEMM readers only)")
     dst = P.dense(src.dims, src.dtype, label + ".dense")
     step(label + ".copy", _copy_view, dev, src, dst)
     return dst

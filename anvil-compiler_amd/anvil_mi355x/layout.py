@@ -41,6 +41,9 @@ class View:
     dims: tuple
     strides: tuple
     offset: int = 0
+    # K-blocked storage of the last dim (0: none): element (..., r, k) at the lead offset + (k // 64) * kb + k % 64,
+    # the row stride (strides[-2]) being 64 -- the layout of ANVIL_GEMM_*_KBLOCK operands, read only by GEMMs
+    kb: int = 0
 
     @property
     def itemsize(self) -> int:
@@ -55,23 +58,34 @@ class View:
         return self.buf.ptr + self.offset * self.itemsize
 
     def is_contiguous(self) -> bool:
+        if self.kb:
+            return False
         return all(s == c for d, s, c in zip(self.dims, self.strides, contig_strides(self.dims)) if d != 1)
 
     def permute(self, perm) -> "View":
+        if self.kb and list(perm)[-1] != len(self.dims) - 1:
+            raise ValueError("a K-blocked view keeps its last dim last")
         return View(self.buf, self.dtype, tuple(self.dims[p] for p in perm), tuple(self.strides[p] for p in perm),
-                    self.offset)
+                    self.offset, self.kb)
 
     def reshape(self, newdims):
         """The same elements as `newdims` in row-major order, or None when that needs a copy."""
+        if self.kb:                                   # lead dims only: the blocked last dim stays as it is
+            if not newdims or newdims[-1] != self.dims[-1]:
+                return None
+            st = nocopy_strides(self.dims[:-1], self.strides[:-1], newdims[:-1])
+            return None if st is None else View(self.buf, self.dtype, tuple(newdims), (*st, 1), self.offset, self.kb)
         st = nocopy_strides(self.dims, self.strides, newdims)
         return None if st is None else View(self.buf, self.dtype, tuple(newdims), st, self.offset)
 
     def prepend(self, n: int) -> "View":
         """Broadcast over a new leading dim of size n (stride 0)."""
-        return View(self.buf, self.dtype, (n,) + self.dims, (0,) + self.strides, self.offset)
+        return View(self.buf, self.dtype, (n,) + self.dims, (0,) + self.strides, self.offset, self.kb)
 
     def read(self, base: np.ndarray) -> np.ndarray:
         """This view of `base` (the whole buffer downloaded as self.dtype) as an int64 array."""
+        if self.kb:
+            raise ValueError("K-blocked storage is planned only for values that are not read back")
         a = np.lib.stride_tricks.as_strided(base[self.offset:], shape=self.dims,
                                             strides=tuple(s * self.itemsize for s in self.strides))
         return a.astype(np.int64)

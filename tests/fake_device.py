@@ -107,7 +107,7 @@ class FakeDevice:
         out = self._guard(lambda: sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, out_dtype,
                                                       fast=self.fast))
         if out is not None:
-            self.store(Cp, out_dtype, (b0, b1, M, N), (sc0, sc1, ldc, 1), out)
+            self._store_result(Cp, out_dtype, b0, b1, M, N, (sc0, sc1, ldc), flags & rt.GEMM_C_KBLOCK, out)
 
     def _operand(self, ptr, b0, b1, rows, K, s0, s1, ld, kblocked):
         """A GEMM operand (b0, b1, rows, K): row-major rows of stride ld, or K-blocked (row r's 64-byte K block j at
@@ -117,6 +117,17 @@ class FakeDevice:
         nb = -(-K // 64)
         v = self.view(ptr, "i8", (b0, b1, rows, nb, 64), (s0, s1, 64, ld, 1)).astype(np.int64)
         return v.reshape(b0, b1, rows, nb * 64)[..., :K]
+
+    def _store_result(self, ptr, dtype, b0, b1, M, N, strides, kblocked, values):
+        """A GEMM result (b0, b1, M, N): row-major, or K-blocked (ANVIL_GEMM_C_KBLOCK: (m, n) at m 64 + (n // 64) ld +
+        n % 64; N a multiple of 64 here)."""
+        s0, s1, ld = strides
+        if not kblocked:
+            self.store(ptr, dtype, (b0, b1, M, N), (s0, s1, ld, 1), values)
+            return
+        assert N % 64 == 0
+        self.store(ptr, dtype, (b0, b1, M, N // 64, 64), (s0, s1, 64, ld, 1),
+                   np.asarray(values).reshape(b0, b1, M, N // 64, 64))
 
     @staticmethod
     def _operand_end(dims, strides, kblocked, K):
@@ -171,7 +182,7 @@ class FakeDevice:
         out = self._guard(both)
         if out is not None:
             if Cp is not None:
-                self.store(Cp, "i8", (b0, b1, M, N), (sc0, sc1, ldc, 1), out[0])
+                self._store_result(Cp, "i8", b0, b1, M, N, (sc0, sc1, ldc), flags & rt.GEMM_C_KBLOCK, out[0])
             self.store(D, "i8", (b0, b1, M, N), (sd0, sd1, ldd, 1), out[1])
 
     def attention_i8(self, Q, K, Vt, O, b0, b1, T, D, strides, ms, ss, lut, one, causal, mo, so, flags):
@@ -197,7 +208,9 @@ class FakeDevice:
         wv = self.view(w, "i8", (cols,), (1,)).astype(np.int64)
         lv = self.view(lut, "i32", (lut_len,), (1,)).astype(np.int64)
         r = self._guard(lambda: sem.rmsnorm_wide(xv, wv, lv, mult, shift, ss_shift, ss_init, x_dtype))
-        if r is not None:
+        if r is not None and flags & rt.RMS_OUT_KBLOCK:        # K-blocked: [cols // 64][rows][64]
+            self.store(out, "i8", (rows, cols // 64, 64), (64, rows * 64, 1), r.reshape(rows, cols // 64, 64))
+        elif r is not None:
             self.store(out, "i8", (rows, cols), (cols, 1), r)
 
     def softmax_lut(self, x, lut, one, causal, batch, t1, t2, out, out_dtype, flags=0):

@@ -277,3 +277,29 @@ def test_wide_frozen_model_selects_the_fast_wide_rmsnorm(fake):
     rms = [c for c in fake.calls if c[0] == "rmsnorm"]
     assert len(rms) == 4 and all(c[1:3] == (32, 32) and c[3] & rt.OP_UNCHECKED for c in rms)
     assert all(c[3] & rt.RMS_S24 for c in rms)
+
+
+def test_gemm_operands_are_planned_kblocked(fake, cfg1):
+    """keep="outputs" on a proven block: values read only as the left operand of linear products (h1, h2 and the fc
+    result) are stored K-blocked by their producers (RMS_OUT_KBLOCK, GEMM_C_KBLOCK) and read K-blocked (A_KBLOCK, or
+    B_KBLOCK where the v product runs transposed); every constant weight is read K-blocked. keep="all" stores every
+    returned value row-major. Results equal the oracle's either way."""
+    cm = anvil_mi355x.compile(cfg1)
+    x = models.eval_inputs(cfg1.spec, 2, 7)
+    want = interp.run(cfg1.module, {"x": cm.quantize_input(x)}, cfg1.consts, batch=True)
+    res = cm.run(x, "mi355x", batch=True, keep="outputs")
+    assert np.array_equal(res.ints["out"], want.values["out"])
+    rms = [c[3] for c in fake.calls if c[0] == "rmsnorm"]
+    assert rms == [rt.OP_UNCHECKED | rt.RMS_S24 | rt.RMS_OUT_KBLOCK] * 2
+    kb = rt.GEMM_A_KBLOCK | rt.GEMM_B_KBLOCK
+    gemm_flags = [c[7] for c in fake.calls if c[0] in ("gemm", "gemm_add")]
+    assert all(f & rt.GEMM_B_KBLOCK or f & rt.GEMM_A_KBLOCK for f in gemm_flags)
+    assert sum(f & kb == kb for f in gemm_flags) == 5                  # q, k, v, fc, proj
+    assert sum(bool(f & rt.GEMM_C_KBLOCK) for f in gemm_flags) == 1     # fc
+    fake.calls.clear()
+    res = cm.run(x, "mi355x", batch=True, keep="all")
+    assert all(c[3] & rt.RMS_OUT_KBLOCK == 0 for c in fake.calls if c[0] == "rmsnorm")
+    assert all(c[7] & rt.GEMM_C_KBLOCK == 0 for c in fake.calls if c[0] == "gemm")
+    for k, v in want.values.items():
+        if k not in cfg1.consts:
+            assert np.array_equal(res.ints[k], v), k
