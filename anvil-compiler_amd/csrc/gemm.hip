@@ -1179,10 +1179,13 @@ static int fast_choice(const GemmArgs& g, int batch, int cfg, int num_cu) {
   // 82.5 us alone, about 5 us a step with its fused residual add. Short K (q, y) gains nothing and fc loses on it.
   // Otherwise, N a multiple of 192 without a fused add: 256 x 192 tiles, one workgroup per CU with whole tiles
   // (with the fused add its heavier epilogue has no second workgroup beside it and loses to 256 x 128).
+  // Both rules serve a row-major A, whose 64-byte row pieces are the slow pattern: with A K-blocked (64-byte blocks
+  // of consecutive rows contiguous) the 256 x 128 tile with K blocks of 64 is faster (proj 72 against 80 us).
+  const bool a_rows = g.kba == 64;
   const long long tiles128 = (long long)((g.M + 255) / 256) * ((g.N + 127) / 128) * batch;
-  if (g.K >= 2048 && g.N < 2048 && persist128_ok && tiles128 >= 2ll * num_cu) return 40;
+  if (a_rows && g.K >= 2048 && g.N < 2048 && persist128_ok && tiles128 >= 2ll * num_cu) return 40;
   const long long tiles192 = (long long)((g.M + 255) / 256) * (g.N / 192) * batch;
-  if (g.K >= 2048 && g.N % 192 == 0 && g.N < 2048 && !g.res && tiles192 >= 2ll * num_cu) return 19;
+  if (a_rows && g.K >= 2048 && g.N % 192 == 0 && g.N < 2048 && !g.res && tiles192 >= 2ll * num_cu) return 19;
   if ((long long)g.M * g.N * batch >= 256ll * 128 * 512 && g.M >= 256 && g.N >= 128) return 16;
   return 13;
 }
