@@ -530,7 +530,9 @@ class CompiledModel:
         """Values stored K-blocked in this plan: int8 results of an rmsnorm or of a plain linear product (a 2-D const
         right operand, stored unpermuted, no fused add) that are read only as the left operand of plain linear
         products and not returned (keep="outputs"), in a proven graph, with a last dim that is a multiple of 64.
-        Their readers then load whole 64-byte blocks of consecutive rows (ANVIL_GEMM_*_KBLOCK)."""
+        Their readers then load whole 64-byte blocks of consecutive rows (ANVIL_GEMM_*_KBLOCK). Linear results read
+        only by fused attention chains through a split into heads of 64 (q and k) are stored head-blocked too: each
+        head's rows are then one contiguous block, read as a plain strided view."""
         if keep != "outputs" or not self.proven:
             return set()
         fused_ops = set(fused) | skip
@@ -538,6 +540,19 @@ class CompiledModel:
         def linear(op):
             return (isinstance(op, (g.QMatmulOp, g.QLinearOp)) and op.b in self.is_const
                     and len(g.qt(op.b).dims) == 2 and op not in fused_ops)
+        scores_ops = {s_op for s_op, _ in fused.values()}
+
+        def to_attention(v):
+            """v reaches only fused attention chains' score products, through transposes."""
+            us = self.users.get(v, [])
+            return bool(us) and v not in self.output_values and all(
+                (isinstance(u, g.TransposeOp) and to_attention(u.result)) or u in scores_ops for u in us)
+
+        def head_split(u, r):
+            """u splits r's last dim into heads of 64 (a view of head-blocked storage) and feeds attention only."""
+            d = g.qt(u.result).dims
+            return (isinstance(u, g.ReshapeOp) and len(d) >= 2 and d[-1] == 64 and d[-2] * 64 == g.qt(r).dims[-1]
+                    and to_attention(u.result))
         out = set()
         for op in self.ops:
             r = op.results[0] if op.results else None
@@ -545,8 +560,9 @@ class CompiledModel:
                 continue
             producer = isinstance(op, g.RmsNormIntOp) or (linear(op) and op not in adds and r not in self.phys)
             users = self.users.get(r, [])
-            if (producer and g.qt(r).dims[-1] % 64 == 0 and users
-                    and all(linear(u) and u.a is r and u.b is not r for u in users)):
+            if producer and g.qt(r).dims[-1] % 64 == 0 and users and (
+                    all(linear(u) and u.a is r and u.b is not r for u in users)
+                    or (linear(op) and all(head_split(u, r) for u in users))):
                 out.add(r)
         return out
 

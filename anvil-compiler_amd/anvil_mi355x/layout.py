@@ -70,7 +70,11 @@ class View:
 
     def reshape(self, newdims):
         """The same elements as `newdims` in row-major order, or None when that needs a copy."""
-        if self.kb:                                   # lead dims only: the blocked last dim stays as it is
+        if self.kb:                                   # lead dims only: the blocked last dim stays as it is,
+            newdims = tuple(int(d) for d in newdims)  # or splits into its 64-element blocks (a plain view)
+            if len(newdims) >= 2 and newdims[-1] == 64 and newdims[-2] * 64 == self.dims[-1]:
+                st = nocopy_strides(self.dims[:-1], self.strides[:-1], newdims[:-2])
+                return None if st is None else View(self.buf, self.dtype, newdims, (*st, self.kb, 1), self.offset)
             if not newdims or newdims[-1] != self.dims[-1]:
                 return None
             st = nocopy_strides(self.dims[:-1], self.strides[:-1], newdims[:-1])

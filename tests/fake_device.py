@@ -156,7 +156,9 @@ class FakeDevice:
             if lut is not None:
                 r.append(span(lut, "i8", (256,), (1,)))
             reads.append(r)
-            writes.append(span(Cp, dt, (b0, b1, M, N), (st[6], st[7], st[8], 1)))
+            pc = Cp.ptr if hasattr(Cp, "ptr") else int(Cp)
+            end = self._operand_end((b0, b1, M), st[6:9], fl & rt.GEMM_C_KBLOCK, N)
+            writes.append((pc, pc + (end + 1) * SIZE[dt]))
         hit = lambda x, y: x[0] < y[1] and y[0] < x[1]                       # noqa: E731
         for i, w in enumerate(writes):
             for j in range(len(calls)):

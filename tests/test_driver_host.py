@@ -303,3 +303,23 @@ def test_gemm_operands_are_planned_kblocked(fake, cfg1):
     for k, v in want.values.items():
         if k not in cfg1.consts:
             assert np.array_equal(res.ints[k], v), k
+
+
+def test_attention_inputs_are_planned_head_blocked(fake):
+    """Head dim 64: q and k, read only by the fused attention through their split into heads, are written
+    head-blocked by their products (GEMM_C_KBLOCK, block = head), and the attention reads each head's rows as one
+    contiguous block (q / k strides: sequence T * 64, head B * T * 64, row 64). Results equal the oracle's."""
+    spec = models.BlockSpec(n_embd=128, n_head=2, seq=64, calib_batches=2, calib_batch=2)
+    built = models.build(spec, 9, stored=False)
+    cm = anvil_mi355x.compile(built)
+    nb = 3
+    x = models.eval_inputs(built.spec, nb, 9)
+    res = cm.run(x, "mi355x", batch=True, keep="outputs")
+    want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
+    assert np.array_equal(res.ints["out"], want.values["out"])
+    att = [c for c in fake.calls if c[0] == "attention"][0]
+    T = spec.seq
+    assert att[1:5] == (nb, 2, T, 64)
+    assert att[5][0:3] == (T * 64, nb * T * 64, 64) and att[5][3:6] == (T * 64, nb * T * 64, 64)
+    members = [c for c in fake.calls if c[0] == "gemm"][:2]
+    assert all(c[7] & rt.GEMM_C_KBLOCK and c[6][8] == nb * T * 64 for c in members)
