@@ -18,6 +18,7 @@ from pathlib import Path
 
 import numpy as np
 
+from anvil_mi355x import quantize as Q
 from anvil_mi355x.ir import GraphBuilder
 from oracle import interp
 from oracle import semantics as sem
@@ -289,3 +290,23 @@ def reference_model(name):
     consts = {k: np.asarray(v, dtype=np.int64).reshape(body["shapes"][k]) for k, v in body["consts"].items()}
     x = np.asarray(body["x"], dtype=np.int64) if "x" in body else None
     return body["ir"], consts, x
+
+
+def kblock_graph():
+    """x (16, 128) -> rmsnorm h -> qlinear a, qlinear b; h also feeds an add (so h stays row-major); a feeds two
+    qlinears (K-blocked); b is returned (row-major); c = qlinear(a) feeds a lut (row-major)."""
+    rng = np.random.default_rng(31)
+    bld = GraphBuilder("kb")
+    x = bld.input("x", [16, 128])
+    w = bld.const("w", [128], value=rng.integers(-100, 100, 128))
+    lut, s = Q.rsqrt_table(0.03, 0.01, 0.02, 100, 128, 1e-5)
+    h = bld.rmsnorm_int("h", x, w, bld.const("r", [len(lut)], dtype="i32", value=lut), 1, s)
+    wt = lambda n, k: bld.const(n, [k, 128], value=rng.integers(-128, 128, (k, 128)))      # noqa: E731
+    a = bld.qlinear("a", h, wt("wa", 128), 3, 16)
+    b = bld.qlinear("b", h, wt("wb", 128), 3, 16)
+    r = bld.add_requant("r1", h, x, 1, 1, 1)
+    c = bld.qlinear("c", a, wt("wc", 128), 3, 16)
+    d = bld.qlinear("d", a, wt("wd", 128), 3, 16)
+    e = bld.lut("e", c, bld.const("t", [256], value=rng.integers(-128, 128, 256)))
+    bld.output(b, r, d, e)
+    return bld.module()

@@ -325,31 +325,11 @@ def test_attention_inputs_are_planned_head_blocked(fake):
     assert all(c[7] & rt.GEMM_C_KBLOCK and c[6][8] == nb * T * 64 for c in members)
 
 
-def _kb_graph():
-    """x (16, 128) -> rmsnorm h -> qlinear a, qlinear b; h also feeds an add (so h stays row-major); a feeds two
-    qlinears (K-blocked); b is returned (row-major); c = qlinear(a) feeds a lut (row-major)."""
-    rng = np.random.default_rng(31)
-    bld = GraphBuilder("kb")
-    x = bld.input("x", [16, 128])
-    w = bld.const("w", [128], value=rng.integers(-100, 100, 128))
-    lut, s = anvil_mi355x.quantize.rsqrt_table(0.03, 0.01, 0.02, 100, 128, 1e-5)
-    h = bld.rmsnorm_int("h", x, w, bld.const("r", [len(lut)], dtype="i32", value=lut), 1, s)
-    wt = lambda n, k: bld.const(n, [k, 128], value=rng.integers(-128, 128, (k, 128)))      # noqa: E731
-    a = bld.qlinear("a", h, wt("wa", 128), 3, 16)
-    b = bld.qlinear("b", h, wt("wb", 128), 3, 16)
-    r = bld.add_requant("r1", h, x, 1, 1, 1)
-    c = bld.qlinear("c", a, wt("wc", 128), 3, 16)
-    d = bld.qlinear("d", a, wt("wd", 128), 3, 16)
-    e = bld.lut("e", c, bld.const("t", [256], value=rng.integers(-128, 128, 256)))
-    bld.output(b, r, d, e)
-    return bld.module()
-
-
 def test_kblocked_planning_only_for_values_read_by_linear_products(fake):
     """Of the candidates, only `a` (an rmsnorm-fed linear result read by two linear products and nothing else) is
     stored K-blocked; `h` (also read by an add), `b` (returned) and `c` (read by a lut) stay row-major. Every
     output equals the oracle's."""
-    mod = _kb_graph()
+    mod = helpers.kblock_graph()
     cm = anvil_mi355x.compile(mod)
     assert cm.proven
     xs = np.random.default_rng(32).integers(-128, 128, (2, 16, 128))

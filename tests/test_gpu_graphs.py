@@ -148,3 +148,17 @@ def test_config4_from_token_ids():
         cm.run(bad, "mi355x", tokens=True, batch=True)
     again = cm.run(ids, "mi355x", tokens=True, batch=True)          # the context is usable after the error
     assert np.array_equal(again.ints[cm.outputs[0]], res.ints[cm.outputs[0]])
+
+
+def test_kblocked_intermediates_on_the_device():
+    """A graph where one linear result is read only by two linear products (stored K-blocked: the GEMM writes it with
+    C_KBLOCK, its readers take it with A_KBLOCK) beside candidates that stay row-major (an rmsnorm output also read
+    by an add, a returned result, a result read by a lut): every output equals the oracle's."""
+    mod = helpers.kblock_graph()
+    cm = anvil_mi355x.compile(mod)
+    xs = np.random.default_rng(33).integers(-128, 128, (5, 16, 128))
+    res = cm.run(xs, "mi355x", quantized=True, batch=True)
+    want = interp.run(mod, {"x": xs}, cm.consts, batch=True)
+    assert sorted(v.owner.sym_str for v in cm._kb_values) == ["a"]
+    for k in ("b", "r1", "d", "e"):
+        assert np.array_equal(res.ints[k], want.values[k]), k
