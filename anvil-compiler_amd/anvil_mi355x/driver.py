@@ -102,6 +102,7 @@ class _Plan:
         self.works: list = []          # per step: (kind, algorithmic int ops, algorithmic HBM bytes)
         self.fused_adds: set = set()   # add_requant ops computed in a GEMM epilogue
         self.stage: dict = {}          # device staging buffers of float inputs and token ids
+        self.kb_values: set = set()    # values stored K-blocked (read only by GEMMs)
 
     def buf(self, nbytes, name=""):
         b = Buf(nbytes, name)
@@ -159,7 +160,6 @@ class CompiledModel:
         self._const_views = {}
         self._const_bt = {}
         self._const_kb = {}
-        self._kb_values = set()
         self._const_bt_host = {}
         self._plans = {}
         self.group_gemms = True           # independent consecutive GEMMs as one anvil_gemm_i8_group call
@@ -278,7 +278,7 @@ class CompiledModel:
         fused = self._attention_chains(keep)
         skip = {o for s_op, sm in fused.values() for o in (s_op, sm)}
         adds = self._residual_fusions(keep)
-        self._kb_values = self._kblocked_values(keep, fused, skip, adds)
+        P.kb_values = self._kblocked_values(keep, fused, skip, adds)
         for op in self.ops:
             if op in skip or op in P.fused_adds:
                 continue
@@ -314,7 +314,7 @@ class CompiledModel:
             if isinstance(op, g.SoftmaxLutOp):
                 views[r] = self._plan_softmax(P, op, views, out_dims, label, dense, step)
                 continue
-            out = P.kblocked(out_dims, t.dtype, label) if r in self._kb_values else P.dense(out_dims, t.dtype, label)
+            out = P.kblocked(out_dims, t.dtype, label) if r in P.kb_values else P.dense(out_dims, t.dtype, label)
             views[r] = out
             if isinstance(op, g.RmsNormIntOp):
                 x = dense(views[op.x], label + ".x")
@@ -448,7 +448,7 @@ class CompiledModel:
         """Dense storage of a matmul result in its chosen physical order, viewed in the logical order."""
         t = g.qt(op.result)
         perm = self.phys.get(op.result)
-        if op.result in self._kb_values:
+        if op.result in P.kb_values:
             return P.kblocked(out_dims, t.dtype, label)
         if perm is None:
             return P.dense(out_dims, t.dtype, label)
@@ -486,7 +486,7 @@ class CompiledModel:
             bt = self._bt_const(op)
             N, K = bt.dims
             host = np.zeros((N, -(-K // 64) * 64), np.int8)
-            host[:, :K] = self.dev_download_const(bt)
+            host[:, :K] = self._bt_host(bt)
             kb = np.ascontiguousarray(host.reshape(N, -1, 64).transpose(1, 0, 2))
             mem = self.dev.upload(kb)
             b = Buf(mem.nbytes, f"{op.sym_str}.Bt.kblocked")
@@ -494,7 +494,7 @@ class CompiledModel:
             self._const_kb[key] = View(b, "i8", (N, K), (64, 1), kb=N * 64)
         return self._const_kb[key]
 
-    def dev_download_const(self, bt):
+    def _bt_host(self, bt):
         """Host copy of a const operand view made by _bt_const (kept on the host when it was uploaded)."""
         return self._const_bt_host[id(bt.buf)]
 

@@ -337,7 +337,7 @@ def test_kblocked_planning_only_for_values_read_by_linear_products(fake):
     want = interp.run(mod, {"x": xs}, cm.consts, batch=True)
     for k in ("b", "r1", "d", "e"):
         assert np.array_equal(res.ints[k], want.values[k]), k
-    assert sorted(v.owner.sym_str for v in cm._kb_values) == ["a"]
+    assert sorted(v.owner.sym_str for v in cm.plan(2).kb_values) == ["a"]
     rms = [c for c in fake.calls if c[0] == "rmsnorm"]
     assert rms and not rms[0][3] & rt.RMS_OUT_KBLOCK
     gemms = [c[7] for c in fake.calls if c[0] == "gemm"]

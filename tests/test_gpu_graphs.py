@@ -159,6 +159,6 @@ def test_kblocked_intermediates_on_the_device():
     xs = np.random.default_rng(33).integers(-128, 128, (5, 16, 128))
     res = cm.run(xs, "mi355x", quantized=True, batch=True)
     want = interp.run(mod, {"x": xs}, cm.consts, batch=True)
-    assert sorted(v.owner.sym_str for v in cm._kb_values) == ["a"]
+    assert sorted(v.owner.sym_str for v in cm.plan(5).kb_values) == ["a"]
     for k in ("b", "r1", "d", "e"):
         assert np.array_equal(res.ints[k], want.values[k]), k
