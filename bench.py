@@ -71,9 +71,8 @@ SLOTS = 240
 
 def kernel_times(dev, steps, passes=3):
     """Average device microseconds of each launch: passes * len(steps) steps back to back, launch k % len(steps)
-    carrying events in step k, so each launch is measured among neighbours that run as in the timed region (a kernel
-    with events attached releases its caches on completion, which slows the next one) and no synchronisation idles
-    the device in between."""
+    carrying events in step k, so each launch is measured among neighbours that run as in the timed region and no
+    synchronisation idles the device in between."""
     n = len(steps)
     per = [0.0] * n
     for k in range(passes * n):
@@ -145,11 +144,11 @@ def bench_block(args):
     for _ in range(args.warmup):
         cm.launch(plan)
     dev.sync()
-    per = kernel_times(dev, steps)
-    dom = max(range(len(steps)), key=lambda i: per[i])
+    dom = max(range(len(steps)), key=lambda i: kernel_times(dev, steps, 1)[i])
     K = args.steps
     wall_s, device_ms, dom_us, n = timed_steps(dev, steps, K, dom)
     value = nb * spec.seq * K / wall_s
+    per = kernel_times(dev, steps)           # after the timed steps: the clock has settled
 
     kind, ops, nbytes = plan.works[dom]
     roof = roofline(kind, ops, nbytes, dom_us, steps[dom][0], n)
@@ -202,8 +201,8 @@ def bench_block(args):
         "kernels": kernels,
         "kernels_us_sum": round(sum(per), 2),
         "kernels_note": "per launch, device time of each launch's kernels alone (events bound to the kernels' dispatch, "
-                        "hipExtLaunchKernel), mean of 3 untimed back-to-back steps in which only that launch carries "
-                        "events; ms_per_step adds the launch gaps",
+                        "hipExtLaunchKernel), mean of 3 untimed back-to-back steps run after the timed ones, in which "
+                        "only that launch carries events; ms_per_step adds the launch gaps",
         "cpu_baseline": cpu,
     }
 
@@ -233,10 +232,10 @@ def bench_linear(args):
         for _, fn, a in steps:
             fn(*a)
     dev.sync()
-    per = kernel_times(dev, steps)
     dom = max(range(len(steps)), key=lambda i: works[i][1])
     K_ = args.steps
     wall_s, device_ms, dom_us, n = timed_steps(dev, steps, K_, dom)
+    per = kernel_times(dev, steps)           # after the timed steps: the clock has settled
     total_ops = sum(w[1] for w in works)
     value = total_ops * K_ / wall_s / 1e12
     shapes = {}
@@ -264,7 +263,7 @@ def bench_linear(args):
         "roofline": roof,
         "shapes": shapes,
         "kernels_note": "per shape, device time of its kernel alone (events bound to the kernel's dispatch), mean of "
-                        "3 untimed passes; M = 256 sits below the ridge (about 630 ops/byte), so frac_hbm is its "
+                        "3 untimed passes after the timed ones; M = 256 sits below the ridge (about 630 ops/byte), so frac_hbm is its "
                         "second bound",
         "cpu_baseline": cpu,
     }

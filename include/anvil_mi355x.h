@@ -58,7 +58,9 @@ int anvil_download(anvil_ctx* ctx, void* dst, const void* src, size_t bytes);
 int anvil_zero(anvil_ctx* ctx, void* dst, size_t bytes);
 
 /* -------------------------------------------------------------------------------------------- timing */
-/* Events on the context's stream, in 512 slots: record two, then read the elapsed milliseconds between them. */
+/* Events on the context's stream, in 512 slots: record two, then read the elapsed milliseconds between them. They
+ * time work only: they are created without the system-scope fence (hipEventDisableSystemFence), so waiting on one
+ * does not make device memory visible to the host (anvil_sync and the copies do). */
 int anvil_event_record(anvil_ctx* ctx, int slot);
 int anvil_event_elapsed(anvil_ctx* ctx, int slot0, int slot1, float* ms);
 /* Kernel-bound timing (no reference counterpart: the reference times ops in simulator cycles, anvil/driver.py:
