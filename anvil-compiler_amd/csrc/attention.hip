@@ -79,13 +79,14 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   constexpr int KS = (D + 31) / 32;         // 32-wide MFMA k-steps over the head dim
   constexpr int CT = (D + 31) / 32;         // 32-wide output column tiles
   constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
-  static_assert(2 * 32 * OROW * 4 >= 32 * 256, "the per-row p tables fit in the partial-O space");
+  // the partial-O space (two slots of 32 rows) also holds the p tables (32 rows of 256 bytes) and the tile maxima
+  constexpr int OSLOT = std::max(32 * OROW, (32 * 256 + A_THREADS * NTW) / 8);
   __shared__ __attribute__((aligned(16))) int lut_s[256];
   __shared__ double lutd_s[260];                            // the LUT as doubles, for the p tables (+ 4 zeros)
   __shared__ __attribute__((aligned(16))) int red_m[4][32];   // after the max: the rows' (A, B) as doubles
   __shared__ int red_s[4][32];
   __shared__ int dlow_s[32];
-  __shared__ __attribute__((aligned(256))) int opart[2][32 * OROW];   // 256: the p-table rows
+  __shared__ __attribute__((aligned(256))) int opart[2][OSLOT];   // 256: the p-table rows
 
   const int t = threadIdx.x;
   const int lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -117,6 +118,9 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   // The requant clamps before its shift (clamp(x >> s) = clamp'(x) >> s with the bounds scaled by 2^s), so the
   // max runs on the clamped values and each score byte is one shift written into its byte lane.
   unsigned sc[NTW][4];
+  // tile i's largest kept score of the lane (an int8 score) at tmx_s[NTW t + i], past the p tables in the partial-O
+  // space (untouched until the partial O tiles)
+  int8_t* tmx_s = reinterpret_cast<int8_t*>(&opart[0][0]) + 32 * 256 + NTW * t;
   int mxc = a.clo;
   // K and V^T tiles come through raw buffer loads; a tile past the causal diagonal (or a chunk past the head dim)
   // gets an offset beyond the descriptor, which loads zeros without touching memory, so every pass can issue its
@@ -151,14 +155,17 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
       const int y = S24 ? __mul24(acc[r], a.ms) + a.rnds : acc[r] * a.ms + a.rnds;
       x[r] = med3i(y, a.clo, a.chi);
     }
+    int tm = a.clo;                                   // the largest kept score of the lane's 16
     if (a.causal && nt == ntiles - 1) {               // the diagonal tile: keys past the row are masked
       const int lim = qrow - nt * 32 - 16 * half;     // key r of this lane is kept iff r <= lim
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mxc = max(mxc, r <= lim ? x[r] : a.clo);
+      for (int r = 0; r < 16; ++r) tm = max(tm, r <= lim ? x[r] : a.clo);
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mxc = max(mxc, x[r]);
+      for (int r = 0; r < 16; ++r) tm = max(tm, x[r]);
     }
+    mxc = max(mxc, tm);
+    tmx_s[i] = (int8_t)(tm >> a.ss);
 #pragma unroll
     for (int g = 0; g < 4; ++g) sc[i][g] = sra_pack4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3], a.ss);
 #pragma unroll
@@ -268,10 +275,12 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   // d0), and a byte above the max (d up to 258, the zero pad of lutd_s) gets 0 or less, read by no kept key.
   constexpr int PT = 256;
   const int cx = 4 * l32;
+  int sthr;                                              // the row's scores below it have p = 0
   {
     const int part = 2 * w + half;                       // this lane's eighth of its row's dwords
     int8_t* trow = ptab + l32 * PT;
     const int dlow = dlow_s[l32];
+    sthr = dlow + mx - 255;
     const int ctop = mx >> 2, cbot = (dlow + mx - 255) >> 2;   // arithmetic shifts: floor
     for (int c = ctop - part; c >= cbot; c -= 8) {
       const double* lp = lutd_s + (4 * c - mx + 255);
@@ -287,10 +296,19 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   v16i oacc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) oacc[ct] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  // A tile whose largest kept score is below its row's threshold in every lane holds p = 0 only (with a
+  // non-decreasing LUT; 45 % of the causal tiles of the GPT-2 block's scores): its lookups and its product are
+  // skipped. Its V^T load is still issued (made conditional too, it costs the kernel spilled registers).
+  unsigned live = 0;
+  static_for<NTW>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    live |= (__any(tmx_s[i] >= sthr) ? 1u : 0u) << i;
+  });
   auto pass3 = [&](auto self, auto ic) __attribute__((always_inline)) -> void {   // nested passes, as for K
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
     if (i + 1 < NTW) vload(nt + 4, vn);                 // one tile ahead (two cost 8 registers)
+    if ((live >> i) & 1) {
     int p[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -310,6 +328,7 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
     for (int g = 0; g < 4; ++g) pf[g] = (int)pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) oacc[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf[ct], pf, oacc[ct], 0, 0, 0);
+    }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) vf[ct] = vn[ct];
     if constexpr (i + 1 < NTW) {

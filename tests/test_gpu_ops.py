@@ -318,8 +318,10 @@ def test_quantize_input(dev, f64):
 def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127):
     """Random q, k, v (B, T, H D) i8 with scores and output requants that spread over int8, the reference chain
     qmatmul -> softmax_lut -> qmatmul evaluated by the oracle, and the head-split views the fused kernel reads.
-    lut_kind: "exp" (the quantizer's table), "steep" (an exp table with a run of zeros at the low end) or "random"
-    (positive and not monotone, so no threshold shortcut applies)."""
+    lut_kind: "exp" (the quantizer's table), "steep" (an exp table with a run of zeros at the low end), "random"
+    (positive and not monotone, so no threshold shortcut applies) or "self" (every key equal to its own query and the
+    self score near the clamp: each row peaks on the diagonal, and from T = 64 most 32 x 32 tiles hold p = 0 only,
+    beside live ones in the same wave)."""
     rng = np.random.default_rng([21, B, H, T, D, int(causal), seed])
     C = H * D
     q, k, v = (rng.integers(-128, 128, (B, T, C)) for _ in range(3))
@@ -330,6 +332,10 @@ def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127
     ss, mo, so = 16, 1, 7
     if lut_kind == "random":
         lut = rng.integers(1, 1 << 20, 256)
+    elif lut_kind == "self":
+        k[:] = q
+        ms = round(1.2 * 127 / (D * 5461) * (1 << 16))      # E[q^2] = 5461: the self score just past 127
+        lut = Q.exp_table(0.3, T, one)
     else:
         lut = Q.exp_table(0.5 if lut_kind == "steep" else 0.05, T, one)
     split = lambda a: a.reshape(B, T, H, D).transpose(0, 2, 1, 3)       # noqa: E731
@@ -344,9 +350,11 @@ def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127
 @pytest.mark.parametrize("causal", [True, False])
 def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
     """anvil_attention_i8 over q, k (B, T, H D), v^T (B, H D, T) and o (B, T, H D), as the planner lays them out,
-    bit-exact with the oracle's scores -> softmax -> P.V chain, for the quantizer's exp table, a table with a zero run
-    and a non-monotone one, and one = 127 or 100."""
-    for seed, sign, kind, one in ((0, 1, "exp", 127), (1, -1, "exp", 127), (2, 1, "random", 127), (3, 1, "steep", 100)):
+    bit-exact with the oracle's scores -> softmax -> P.V chain, for the quantizer's exp table, a table with a zero run,
+    a non-monotone one and rows peaked on the diagonal (tiles whose p are all zero are skipped), and one = 127 or
+    100."""
+    for seed, sign, kind, one in ((0, 1, "exp", 127), (1, -1, "exp", 127), (2, 1, "random", 127), (3, 1, "steep", 100),
+                                  (4, 1, "self", 127)):
         q, k, v, (ms, ss, mo, so), lut, want = _attention_case(B, H, T, D, causal, seed, sign, kind, one)
         if kind == "steep":
             assert (lut == 0).any() and np.all(np.diff(lut) >= 0)
