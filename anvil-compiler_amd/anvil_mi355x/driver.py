@@ -299,7 +299,7 @@ class CompiledModel:
             if isinstance(op, g.ReshapeOp):
                 src = views[op.x]
                 nd = (*lead(op.x), *t.dims)
-                v = src.reshape(nd)
+                v = src.merge_kblocked(nd) if r in P.kb_values else src.reshape(nd)
                 if v is None:
                     v = dense_copy(src, label).reshape(nd)
                 views[r] = v
@@ -410,7 +410,16 @@ class CompiledModel:
         qa = views[s_op.a]
         kb = views[s_op.b].permute(_swap_last2(n))           # key rows (..., T, d)
         vb = views[o_op.b].permute(_swap_last2(n))           # V^T rows (..., d, T)
-        out = self._alloc_result(P, o_op, (nb, *g.qt(o_op.result).dims), label)
+        om = self._merged_heads(o_op)
+        if om is not None and om in P.kb_values:
+            # o written head-blocked: om's K-blocked storage (block = head), split into heads and permuted back to
+            # o's order, is a plain strided view (sequence T * 64, head rows * 64, row 64)
+            omd = (nb, *g.qt(om).dims)
+            split = P.kblocked(omd, "i8", label).reshape((*omd[:-1], omd[-1] // 64, 64))
+            pfull = [0] + [p + 1 for p in self.users[o_op.result][0].perm_list]
+            out = split.permute([pfull.index(i) for i in range(len(pfull))])
+        else:
+            out = self._alloc_result(P, o_op, (nb, *g.qt(o_op.result).dims), label)
         vs = [qa, kb, vb, out]
         lead = out.dims[:-2]
         idx = [i for i, d in enumerate(lead) if d != 1]
@@ -532,7 +541,8 @@ class CompiledModel:
         products and not returned (keep="outputs"), in a proven graph, with a last dim that is a multiple of 64.
         Their readers then load whole 64-byte blocks of consecutive rows (ANVIL_GEMM_*_KBLOCK). Linear results read
         only by fused attention chains through a split into heads of 64 (q and k) are stored head-blocked too: each
-        head's rows are then one contiguous block, read as a plain strided view."""
+        head's rows are then one contiguous block, read as a plain strided view. So is a fused attention's output
+        merged back from its heads of 64 when only linear products read the merged value (om)."""
         if keep != "outputs" or not self.proven:
             return set()
         fused_ops = set(fused) | skip
@@ -564,7 +574,34 @@ class CompiledModel:
                     all(linear(u) and u.a is r and u.b is not r for u in users)
                     or (linear(op) and all(head_split(u, r) for u in users))):
                 out.add(r)
+        for o_op in fused:                     # attention outputs merged back from heads of 64 for linear readers
+            om = self._merged_heads(o_op)
+            users = self.users.get(om, []) if om is not None else []
+            if users and g.qt(om).dtype == "i8" and all(linear(u) and u.a is om and u.b is not om for u in users):
+                out.add(om)
         return out
+
+    def _merged_heads(self, o_op):
+        """om when a fused attention's output o (..., H, T, 64) reaches the graph only as om = reshape(transpose(o))
+        of dims (..., T, H * 64), the transpose swapping the head and sequence dims; none of the three returned. o can
+        then be written straight into om's K-blocked storage, one block per head."""
+        o = o_op.result
+        us = self.users.get(o, [])
+        d = g.qt(o).dims
+        n = len(d)
+        if len(us) != 1 or not isinstance(us[0], g.TransposeOp) or o in self.output_values or n < 3 or d[-1] != 64:
+            return None
+        t = us[0]
+        if list(t.perm_list) != list(range(n - 3)) + [n - 2, n - 3, n - 1]:
+            return None
+        us2 = self.users.get(t.result, [])
+        if len(us2) != 1 or not isinstance(us2[0], g.ReshapeOp) or t.result in self.output_values:
+            return None
+        om = us2[0].result
+        rd = g.qt(om).dims
+        if om in self.output_values or tuple(rd) != (*d[:-3], d[-2], d[-3] * 64):
+            return None
+        return om
 
     def _host_const(self, value):
         op = value.owner

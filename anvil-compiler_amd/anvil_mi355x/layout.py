@@ -82,6 +82,17 @@ class View:
         st = nocopy_strides(self.dims, self.strides, newdims)
         return None if st is None else View(self.buf, self.dtype, tuple(newdims), st, self.offset)
 
+    def merge_kblocked(self, newdims):
+        """A plain view whose last two dims are (n, 64) with strides (kb, 1), presented as newdims (..., n * 64) in
+        K-blocked storage of block stride kb: the inverse of splitting a K-blocked last dim into its blocks. None when
+        the view is not of that form or its lead dims do not reshape without a copy."""
+        newdims = tuple(int(d) for d in newdims)
+        if (self.kb or len(self.dims) < 2 or self.dims[-1] != 64 or self.strides[-1] != 1 or not newdims
+                or newdims[-1] != self.dims[-2] * 64):
+            return None
+        st = nocopy_strides(self.dims[:-2], self.strides[:-2], newdims[:-1])
+        return None if st is None else View(self.buf, self.dtype, newdims, (*st, 1), self.offset, self.strides[-2])
+
     def prepend(self, n: int) -> "View":
         """Broadcast over a new leading dim of size n (stride 0)."""
         return View(self.buf, self.dtype, (n,) + self.dims, (0,) + self.strides, self.offset, self.kb)

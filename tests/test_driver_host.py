@@ -308,7 +308,9 @@ def test_gemm_operands_are_planned_kblocked(fake, cfg1):
 def test_attention_inputs_are_planned_head_blocked(fake):
     """Head dim 64: q and k, read only by the fused attention through their split into heads, are written
     head-blocked by their products (GEMM_C_KBLOCK, block = head), and the attention reads each head's rows as one
-    contiguous block (q / k strides: sequence T * 64, head B * T * 64, row 64). Results equal the oracle's."""
+    contiguous block (q / k strides: sequence T * 64, head B * T * 64, row 64). Its output o, read only by the y
+    product through its merge back into rows (om), is written the same way and y reads om K-blocked
+    (GEMM_A_KBLOCK, block stride B * T * 64). Results equal the oracle's."""
     spec = models.BlockSpec(n_embd=128, n_head=2, seq=64, calib_batches=2, calib_batch=2)
     built = models.build(spec, 9, stored=False)
     cm = anvil_mi355x.compile(built)
@@ -323,6 +325,10 @@ def test_attention_inputs_are_planned_head_blocked(fake):
     assert att[5][0:3] == (T * 64, nb * T * 64, 64) and att[5][3:6] == (T * 64, nb * T * 64, 64)
     members = [c for c in fake.calls if c[0] == "gemm"][:2]
     assert all(c[7] & rt.GEMM_C_KBLOCK and c[6][8] == nb * T * 64 for c in members)
+    assert att[5][9:12] == (T * 64, nb * T * 64, 64)
+    y = [c for c in fake.calls if c[0] == "gemm_add"][0]
+    assert y[7] & rt.GEMM_A_KBLOCK and y[6][2] == nb * T * 64
+    assert "om" in {v.owner.sym_str for v in cm.plan(nb).kb_values}
 
 
 def test_kblocked_planning_only_for_values_read_by_linear_products(fake):
