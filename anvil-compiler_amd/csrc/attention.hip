@@ -49,6 +49,7 @@ struct AttnArgs {
   const int* lut;
   int one, causal;
   int mo, so, rndo;    // output requant
+  int mo24;            // |mo| < 2^23: the output requant multiply fits 24 bits
   int nqt;             // query tiles of 32 rows per head
   unsigned long long mq, mb;   // n / nqt and n / batch1 as (n m) >> (32 + k): m = ceil(2^(32+k) / d), 2^k >= d
   int kq, kb;
@@ -155,15 +156,16 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
       const int y = S24 ? __mul24(acc[r], a.ms) + a.rnds : acc[r] * a.ms + a.rnds;
       x[r] = med3i(y, a.clo, a.chi);
     }
-    int tm = a.clo;                                   // the largest kept score of the lane's 16
-    if (a.causal && nt == ntiles - 1) {               // the diagonal tile: keys past the row are masked
+    // the diagonal tile: a key past the row takes the lowest score (clo >> ss), which leaves the row max as it is;
+    // the sums subtract its LUT term and the probabilities mask it
+    if (a.causal && nt == ntiles - 1) {
       const int lim = qrow - nt * 32 - 16 * half;     // key r of this lane is kept iff r <= lim
 #pragma unroll
-      for (int r = 0; r < 16; ++r) tm = max(tm, r <= lim ? x[r] : a.clo);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) tm = max(tm, x[r]);
+      for (int r = 0; r < 16; ++r) x[r] = r <= lim ? x[r] : a.clo;
     }
+    int tm = a.clo;                                   // the largest kept score of the lane's 16
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tm = max(tm, x[r]);
     mxc = max(mxc, tm);
     tmx_s[i] = (int8_t)(tm >> a.ss);
 #pragma unroll
@@ -208,23 +210,15 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   int S = 0;
   static_for<NTW>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
-    const int nt = w + 4 * i;
-    if (nt < ntiles) {
-      if (a.causal && nt == ntiles - 1) {
-        const int lim = qrow - nt * 32 - 16 * half;
+    if (w + 4 * i < ntiles) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int s = sbyte(sc[i][r >> 2], r & 3);
-          const bool kept = r <= lim;
-          const int e = erow[kept ? s : mx];              // a masked score may exceed the max: read inside the table
-          S += kept ? e : 0;
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) S += erow[sbyte(sc[i][r >> 2], r & 3)];
-      }
+      for (int r = 0; r < 16; ++r) S += erow[sbyte(sc[i][r >> 2], r & 3)];
     }
   });
+  if (a.causal && ((ntiles - 1 - w) & 3) == 0 && w < ntiles) {   // this wave holds the diagonal tile: its masked
+    const int lim = l32 - 16 * half;                              // keys (those past r = lim) added lut terms of
+    S -= (15 - max(-1, min(lim, 15))) * erow[a.clo >> a.ss];      // the lowest score
+  }
   S += __shfl_xor(S, 32, 64);
   if (half == 0) red_s[w][l32] = S;
   __syncthreads();
@@ -317,15 +311,15 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
       for (int e = 0; e < 4; ++e)
         p[4 * g + e] = *reinterpret_cast<lds_u8*>(__builtin_amdgcn_perm(rbase, sw, 0x07060500u | e));
     }
-    if (a.causal && nt == ntiles - 1) {
-      asm volatile("");                                  // keeps the masking on the diagonal tile's own path
-      const int lim = qrow - nt * 32 - 16 * half;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = r <= lim ? p[r] : 0;
-    }
     v4i pf;
 #pragma unroll
     for (int g = 0; g < 4; ++g) pf[g] = (int)pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
+    if (a.causal && nt == ntiles - 1) {
+      asm volatile("");                                  // keeps the masking on the diagonal tile's own path
+      const int lim = qrow - nt * 32 - 16 * half;        // bytes r <= lim kept: n of dword g's four
+#pragma unroll
+      for (int g = 0; g < 4; ++g) pf[g] &= (int)(0xFFFFFFFFull >> (32 - 8 * min(max(lim + 1 - 4 * g, 0), 4)));
+    }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) oacc[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf[ct], pf, oacc[ct], 0, 0, 0);
     }
@@ -365,17 +359,28 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
     put();
   }
   __syncthreads();
+  // |O| <= 128 (one + T / 2) < 2^17 (p >= 0 sums to at most one + T / 2 over a row), so with |m_o| < 2^23 the
+  // output requant multiply is one 24-bit multiply-add
   constexpr int C4 = D / 4;                              // 4-column groups per row
   int8_t* Ob = a.O + b0 * a.so0 + b1 * a.so1 + (long long)q0 * a.ldo;
-  for (int idx = t; idx < 32 * C4; idx += A_THREADS) {
-    const int row = idx / C4, c = 4 * (idx % C4);
-    v4i sum = *reinterpret_cast<const v4i*>(opart[0] + row * OROW + c);
-    sum += *reinterpret_cast<const v4i*>(opart[1] + row * OROW + c);
-    int o[4];
+  auto store = [&](auto m24) {
+    for (int idx = t; idx < 32 * C4; idx += A_THREADS) {
+      const int row = idx / C4, c = 4 * (idx % C4);
+      v4i sum = *reinterpret_cast<const v4i*>(opart[0] + row * OROW + c);
+      sum += *reinterpret_cast<const v4i*>(opart[1] + row * OROW + c);
+      int o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = min(max((sum[e] * a.mo + a.rndo) >> a.so, -128), 127);
-    *reinterpret_cast<unsigned*>(Ob + (long long)row * a.ldo + c) = pack4(o[0], o[1], o[2], o[3]);
-  }
+      for (int e = 0; e < 4; ++e) {
+        const int y = decltype(m24)::value ? __mul24(sum[e], a.mo) + a.rndo : sum[e] * a.mo + a.rndo;
+        o[e] = min(max(y >> a.so, -128), 127);
+      }
+      *reinterpret_cast<unsigned*>(Ob + (long long)row * a.ldo + c) = pack4(o[0], o[1], o[2], o[3]);
+    }
+  };
+  if (a.mo24)
+    store(std::true_type{});
+  else
+    store(std::false_type{});
 }
 
 template <int NTW, bool S24>
@@ -454,6 +459,7 @@ extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t*
   a.lut = lut;
   a.one = one, a.causal = causal ? 1 : 0;
   a.mo = m_o, a.so = s_o, a.rndo = s_o ? 1 << (s_o - 1) : 0;
+  a.mo24 = m_o > -(1 << 23) && m_o < (1 << 23);
   a.nqt = T / 32;
   auto magic = [](int d, unsigned long long& m, int& k) {
     k = 0;
