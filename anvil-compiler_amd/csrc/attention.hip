@@ -76,7 +76,7 @@ __device__ __forceinline__ v4i chunk16(const int8_t* row, int chunk) {
 }
 
 template <int NTW, int D, bool S24>
-__global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(AttnArgs a) {
+__global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(AttnArgs a) {
   constexpr int KS = (D + 31) / 32;         // 32-wide MFMA k-steps over the head dim
   constexpr int CT = (D + 31) / 32;         // 32-wide output column tiles
   constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
@@ -135,21 +135,21 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
       kf[ks] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(krs, o, 0, 0));
     }
   };
-  // K tiles are loaded two tiles ahead of their MFMAs. The wave's tiles are a prefix of its passes, and pass i + 1
-  // is entered from the end of pass i only (nested, not sequential, branches), each pass issuing its prefetch
-  // unconditionally: each wait then covers exactly the loads two tiles back, where a join of a path that loaded
-  // with one that did not would make it cover every load issued so far. The buffers rotate in registers.
-  v4i kf[KS], kn[KS];
+  // The next K tile loads into kf as soon as this pass's score MFMAs have read it, so its latency overlaps the
+  // requant of this tile; one buffer (not two, loaded two tiles ahead) keeps the kernel at 80 registers, six waves a
+  // SIMD. The wave's tiles are a prefix of its passes, and pass i + 1 is entered from the end of pass i only
+  // (nested, not sequential, branches), each pass issuing its load unconditionally: each wait then covers exactly
+  // the load one tile back, where a join of a path that loaded with one that did not would make it cover every load
+  // issued so far.
+  v4i kf[KS];
   kload(w, kf);
-  if (NTW > 1) kload(w + 4, kn);
   auto pass1 = [&](auto self, auto ic) __attribute__((always_inline)) -> void {
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
-    v4i kn2[KS];
-    if (i + 2 < NTW) kload(nt + 8, kn2);
     v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[ks], qf[ks], acc, 0, 0, 0);
+    if (i + 1 < NTW) kload(nt + 4, kf);
     int x[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -170,11 +170,7 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
     tmx_s[i] = (int8_t)(tm >> a.ss);
 #pragma unroll
     for (int g = 0; g < 4; ++g) sc[i][g] = sra_pack4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3], a.ss);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = kn[ks];
-      kn[ks] = kn2[ks];
-    }
+
     if constexpr (i + 1 < NTW) {
       if (nt + 4 < ntiles) self(self, std::integral_constant<int, i + 1>{});
     }
@@ -302,17 +298,17 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
     if ((live >> i) & 1) {
-    int p[16];
+    v4i pf;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const unsigned sw = sc[i][g] ^ swz;
+      int p[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        p[4 * g + e] = *reinterpret_cast<lds_u8*>(__builtin_amdgcn_perm(rbase, sw, 0x07060500u | e));
+        p[e] = *reinterpret_cast<lds_u8*>(__builtin_amdgcn_perm(rbase, sw, 0x07060500u | e));
+      pf[g] = (int)pack4(p[0], p[1], p[2], p[3]);
+      if (g == 1) __builtin_amdgcn_sched_barrier(0);  // two halves of eight lookups: 8 registers fewer at the peak
     }
-    v4i pf;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) pf[g] = (int)pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
     if (a.causal && nt == ntiles - 1) {
       asm volatile("");                                  // keeps the masking on the diagonal tile's own path
       const int lim = qrow - nt * 32 - 16 * half;        // bytes r <= lim kept: n of dword g's four
@@ -333,7 +329,7 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 5 : 1)) void attention_i8(Att
   if (w < ntiles) pass3(pass3, std::integral_constant<int, 0>{});
 
   // ---- 4. sum the four partial O tiles, requant, store. Lane l holds O_w[row l % 32][32 ct + 8 g + 4 (l / 32) + e].
-  // Two LDS slots (half the partial-O space of one slot a wave, which lets five workgroups share a CU): waves 2 and 3
+  // Two LDS slots (half the partial-O space of one slot a wave, which lets six workgroups share a CU): waves 2 and 3
   // store theirs, waves 0 and 1 add them in and store the pair sums, and every thread adds the two slots. A lane
   // reads and then rewrites only its own chunks of a slot.
   __syncthreads();                                       // every wave is done with the p tables
