@@ -319,12 +319,16 @@ def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127
     """Random q, k, v (B, T, H D) i8 with scores and output requants that spread over int8, the reference chain
     qmatmul -> softmax_lut -> qmatmul evaluated by the oracle, and the head-split views the fused kernel reads.
     lut_kind: "exp" (the quantizer's table), "steep" (an exp table with a run of zeros at the low end), "random"
-    (positive and not monotone, so no threshold shortcut applies) or "self" (every key equal to its own query and the
+    (positive and not monotone, so no threshold shortcut applies), "self" (every key equal to its own query and the
     self score near the clamp: each row peaks on the diagonal, and from T = 64 most 32 x 32 tiles hold p = 0 only,
-    beside live ones in the same wave)."""
+    beside live ones in the same wave) or "shift25" (score shift 25: the int32 pre-shift range reaches scores in
+    [-64, 63] only, so the lowest score, which masked keys of the diagonal tile take, is -64 rather than -128;
+    q, k in [-40, 40] keep acc M_s inside int32 as a proven graph's would be)."""
     rng = np.random.default_rng([21, B, H, T, D, int(causal), seed])
     C = H * D
     q, k, v = (rng.integers(-128, 128, (B, T, C)) for _ in range(3))
+    if lut_kind == "shift25":
+        q, k = rng.integers(-40, 41, (B, T, C)), rng.integers(-40, 41, (B, T, C))
     if seed == 1:
         q[0, :, :D] = 0                                      # a head of all-zero scores: uniform rows
         q[-1, :, -D:], k[-1, :, -D:] = 127, -128             # a head of scores clamped to -128: max = -128
@@ -332,6 +336,9 @@ def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127
     ss, mo, so = 16, 1, 7
     if lut_kind == "random":
         lut = rng.integers(1, 1 << 20, 256)
+    elif lut_kind == "shift25":
+        ms, ss = ((1 << 31) - (1 << 25)) // (D * 40 * 40), 25    # |acc M_s| + 2^24 < 2^31 for any q, k in range
+        lut = Q.exp_table(0.05, T, one)
     elif lut_kind == "self":
         k[:] = q
         ms = round(1.2 * 127 / (D * 5461) * (1 << 16))      # E[q^2] = 5461: the self score just past 127
@@ -354,7 +361,7 @@ def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
     a non-monotone one and rows peaked on the diagonal (tiles whose p are all zero are skipped), and one = 127 or
     100."""
     for seed, sign, kind, one in ((0, 1, "exp", 127), (1, -1, "exp", 127), (2, 1, "random", 127), (3, 1, "steep", 100),
-                                  (4, 1, "self", 127)):
+                                  (4, 1, "self", 127), (5, 1, "shift25", 127)):
         q, k, v, (ms, ss, mo, so), lut, want = _attention_case(B, H, T, D, causal, seed, sign, kind, one)
         if kind == "steep":
             assert (lut == 0).any() and np.all(np.diff(lut) >= 0)
