@@ -210,6 +210,38 @@ def test_nocopy_strides_agree_with_numpy():
             assert got is not None
 
 
+def test_merge_kblocked_inverts_the_head_split():
+    """View.merge_kblocked: the plain (B, T, H, 64) view of K-blocked (B, T, H * 64) storage (the attention output o,
+    permuted from (B, H, T, 64)) merges back into the K-blocked view, element for element; views of any other form
+    are refused."""
+    B, T, H = 3, 5, 4
+    kb = B * T * 64
+    buf = layout.Buf(B * T * H * 64)
+    om = layout.View(buf, "i8", (B, T, H * 64), (T * 64, 64, 1), 0, kb)
+    split = om.reshape((B, T, H, 64))
+    assert split.kb == 0 and split.strides == (T * 64, 64, kb, 1)
+    o = split.permute([0, 2, 1, 3])                      # the attention writes o as (B, H, T, 64)
+    back = o.permute([0, 2, 1, 3]).merge_kblocked((B, T, H * 64))
+    assert (back.dims, back.strides, back.kb, back.offset) == (om.dims, om.strides, om.kb, om.offset)
+
+    def addr_kb(v, idx):                                 # element address under the K-blocked layout
+        *lead, k = idx
+        return v.offset + sum(i * s for i, s in zip(lead, v.strides[:-1])) + (k // 64) * v.kb + k % 64
+
+    def addr(v, idx):
+        return v.offset + sum(i * s for i, s in zip(idx, v.strides))
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        b, t, h, d = (int(rng.integers(0, n)) for n in (B, T, H, 64))
+        assert addr_kb(back, (b, t, h * 64 + d)) == addr(o, (b, h, t, d))
+    assert om.merge_kblocked((B, T, H * 64)) is None                        # already K-blocked
+    assert split.merge_kblocked((B, T, H * 32)) is None                     # sizes differ
+    half = layout.View(buf, "i8", (B, T, 2 * H, 32), (T * 32, 32, kb // 2, 1))
+    assert half.merge_kblocked((B, T, H * 64)) is None                      # blocks of 32
+    crossed = split.permute([1, 0, 2, 3])                                   # lead dims that do not fold into (T, B)
+    assert crossed.merge_kblocked((T * B, H * 64)) is None
+
+
 def test_layout_choice_makes_head_merge_free(cfg1):
     cm = anvil_mi355x.driver.CompiledModel(cfg1.module, cfg1.consts)
     phys = {v.owner.sym_str: p for v, p in cm.phys.items()}
