@@ -21,6 +21,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
+from . import hostpar
 from . import ir as g
 from . import quantize as Q
 from . import runtime as rt
@@ -783,7 +784,7 @@ class CompiledModel:
 
     def dequantize(self, sym, ints):
         s = self.scale(sym)
-        return np.asarray(ints, dtype=np.float64) * (1.0 if s is None else s)
+        return hostpar.scaled_f64(ints, 1.0 if s is None else s)
 
     def set_embedding(self, wte, wpe):
         """Token and position tables of a token model (float32 (vocab, C), (>= T, C)); the graph's single input is
@@ -837,7 +838,7 @@ class CompiledModel:
             else:
                 if self.scale(sym) is None:
                     raise ValueError(f"input {sym!r} has no scale: pass integer inputs with quantized=True")
-                if v.dtype.kind == "f" and not np.all(np.isfinite(v)):
+                if v.dtype.kind == "f" and not hostpar.all_finite(v):
                     raise ValueError(f"input {sym!r} has NaN or infinite values")
                 # quantized on the device (clamp(rint(x / scale)) in float64, as quantize_input does on the host)
                 out[sym] = _FloatInput(np.ascontiguousarray(v, dtype=np.float32 if v.dtype == np.float32

@@ -11,6 +11,8 @@ from dataclasses import dataclass
 
 import numpy as np
 
+from . import hostpar
+
 ITEMSIZE = {"i8": 1, "i16": 2, "i32": 4}
 
 
@@ -103,7 +105,7 @@ class View:
             raise ValueError("K-blocked storage is planned only for values that are not read back")
         a = np.lib.stride_tricks.as_strided(base[self.offset:], shape=self.dims,
                                             strides=tuple(s * self.itemsize for s in self.strides))
-        return a.astype(np.int64)
+        return hostpar.astype(a, np.int64)
 
 
 def nocopy_strides(dims, strides, newdims):
