@@ -12,9 +12,10 @@
 // Workgroup: 4 waves on 32 query rows q0 .. q0 + 31; wave w takes the 32-key tiles w, w + 4, w + 8, ... up to the
 // causal diagonal, so the waves share the row's keys evenly and each holds at most T / 128 tiles of scores.
 //   1. S = Q K^T per tile on v_mfma_i32_32x32x32_i8, requantised to int8 and kept packed in registers: lane l holds
-//      row q0 + l % 32 and, of each tile, the keys 16 (l / 32) + 4 g + e (g, e = 0..3) in dword g, byte e. Partial
-//      row maxima (init -128, kept keys only) meet in LDS.
-//   2. Partial sums of lut[s - max + 255] (lut staged in LDS) meet in LDS.
+//      row q0 + l % 32 and, of each tile, the keys 16 (l / 32) + 4 g + e (g, e = 0..3) in dword g, byte e. A key
+//      past the causal diagonal takes the lowest score. Partial row maxima meet in LDS.
+//   2. Partial sums of lut[s - max + 255] (lut staged in LDS) meet in LDS; the diagonal tile's masked keys are
+//      subtracted once per lane.
 //   3. p = (lut[d] one + S // 2) // S, d = s - max + 255, exactly, in float64 (full rate on CDNA4): with per-row
 //      A = fl(one / S) and B = fl((S // 2) / S + 2^-40), y = fma(lut[d], A, B) is within 2^-45 of n / S + 2^-40
 //      (n = lut[d] one + S // 2 < 2^31, n / S < 128, three roundings of 2^-53 relative), and n / S is either an
@@ -22,9 +23,11 @@
 //      1.5 2^52). The LUT (>= 0) is staged in LDS as doubles, and each row's p values go into a byte table indexed
 //      by score. O_w = P V over the wave's tiles on MFMA, P packed in registers: lane l's 16 probabilities of a tile
 //      are keys 16 (l / 32) .. + 15 (the key rows entered the score MFMA in bperm order), so its V^T fragment is one
-//      contiguous 16-byte load.
+//      contiguous 16-byte load. With a non-decreasing LUT, p = 0 below a per-row score threshold: a tile whose
+//      largest kept score is below it in every lane skips its lookups and its product.
 //   4. The four partial O tiles (int32) are summed through two LDS slots; o = clamp((O M_o + rnd(s_o)) >> s_o),
 //      4-byte stores.
+// At D = 64 the kernel fits 80 registers and 21.7 KB of LDS: six workgroups (six waves a SIMD) share a CU.
 // Every product is proven to fit int32 (prove_no_overflow), so the requants run in 32 bits; with S24 the score
 // requant multiply is one 24-bit multiply-add (|acc|, |M_s| < 2^23).
 #include <algorithm>
