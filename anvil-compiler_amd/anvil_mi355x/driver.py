@@ -433,10 +433,12 @@ class CompiledModel:
                 strides += [0 if i is None else v.strides[i] for i in idx] + [v.strides[-2]]
             offs = [v.offset for v in vs]
             T, D = qa.dims[-2], qa.dims[-1]
-            # K and V^T go through 32-bit buffer offsets over one head: rows at least D (keys) / T (V^T) apart
+            # K and V^T go through 32-bit buffer offsets over one head: rows at least D (keys) / T (V^T) apart; O's
+            # 32-row tiles through 32-bit offsets too
             fits = (all(st % 16 == 0 for st in strides[:9]) and all(st % 4 == 0 for st in strides[9:])
                     and all(o % 16 == 0 for o in offs[:3]) and offs[3] % 4 == 0
-                    and strides[5] >= D and strides[8] >= T and T * strides[5] < 1 << 31 and D * strides[8] < 1 << 31)
+                    and strides[5] >= D and strides[8] >= T and T * strides[5] < 1 << 31 and D * strides[8] < 1 << 31
+                    and strides[11] >= D and 32 * strides[11] < 1 << 31)
         if not fits:
             sv = self._plan_matmul(P, s_op, views, (nb, *g.qt(s_op.result).dims), label + ".scores", dense, step,
                                    keep)

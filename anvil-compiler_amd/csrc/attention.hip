@@ -53,6 +53,10 @@ struct AttnArgs {
   int one, causal;
   int mo, so, rndo;    // output requant
   int mo24;            // |mo| < 2^23: the output requant multiply fits 24 bits
+  int clo_o, chi_o;    // the output requant's clamp in the pre-shift domain, as clo / chi
+  int ldo32, obytes;   // O's row stride, and the bytes of one 32-row tile (31 ldo + D), both below 2^31
+  unsigned long long mone;   // n / one as (n mone) >> (32 + kone)
+  int kone;
   int nqt;             // query tiles of 32 rows per head
   unsigned long long mq, mb;   // n / nqt and n / batch1 as (n m) >> (32 + k): m = ceil(2^(32+k) / d), 2^k >= d
   int kq, kb;
@@ -243,7 +247,7 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
     if (mono) {
       // lut[d] one + S // 2 >= S  <=>  lut[d] >= e0 = ceil((S - S // 2) / one); d0 = #{d : lut[d] < e0}, by binary
       // search over the non-decreasing table (256 when even lut[255] is below e0)
-      const int e0 = (S - (S >> 1) + a.one - 1) / a.one;
+      const int e0 = (int)udiv_magic((unsigned)(S - (S >> 1) + a.one - 1), a.mone, a.kone);
       int pos = 0;
 #pragma unroll
       for (int step = 128; step >= 1; step >>= 1) pos += lut_s[pos + step - 1] < e0 ? step : 0;
@@ -360,21 +364,22 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
   }
   __syncthreads();
   // |O| <= 128 (one + T / 2) < 2^17 (p >= 0 sums to at most one + T / 2 over a row), so with |m_o| < 2^23 the
-  // output requant multiply is one 24-bit multiply-add
+  // output requant multiply is one 24-bit multiply-add. The clamp runs before the shift, as for the scores, so each
+  // output byte is one shift written into its byte lane; the tile's 32 rows are stored through a buffer descriptor
+  // with 32-bit offsets.
   constexpr int C4 = D / 4;                              // 4-column groups per row
-  int8_t* Ob = a.O + b0 * a.so0 + b1 * a.so1 + (long long)q0 * a.ldo;
+  const __amdgpu_buffer_rsrc_t ors = uniform_rsrc(a.O + b0 * a.so0 + b1 * a.so1 + (long long)q0 * a.ldo, a.obytes);
   auto store = [&](auto m24) {
     for (int idx = t; idx < 32 * C4; idx += A_THREADS) {
       const int row = idx / C4, c = 4 * (idx % C4);
       v4i sum = *reinterpret_cast<const v4i*>(opart[0] + row * OROW + c);
       sum += *reinterpret_cast<const v4i*>(opart[1] + row * OROW + c);
-      int o[4];
+      int x[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int y = decltype(m24)::value ? __mul24(sum[e], a.mo) + a.rndo : sum[e] * a.mo + a.rndo;
-        o[e] = min(max(y >> a.so, -128), 127);
-      }
-      *reinterpret_cast<unsigned*>(Ob + (long long)row * a.ldo + c) = pack4(o[0], o[1], o[2], o[3]);
+      for (int e = 0; e < 4; ++e)
+        x[e] = med3i(decltype(m24)::value ? __mul24(sum[e], a.mo) + a.rndo : sum[e] * a.mo + a.rndo, a.clo_o, a.chi_o);
+      __builtin_amdgcn_raw_buffer_store_b32(sra_pack4(x[0], x[1], x[2], x[3], a.so), ors, (unsigned)(row * a.ldo32 + c),
+                                            0, 0);
     }
   };
   if (a.mo24)
@@ -440,6 +445,8 @@ extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t*
   if (st[5] < D || st[8] < T || (long long)T * st[5] >= (1ll << 31) || (long long)D * st[8] >= (1ll << 31))
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: K row stride %lld / V^T row stride %lld out of range",
                      (long long)st[5], (long long)st[8]);
+  if (st[11] < D || 32 * st[11] >= (1ll << 31))   // a 32-row output tile is stored through 32-bit offsets
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: O row stride %lld out of range", (long long)st[11]);
   if (int r = check_ctx(ctx)) return r;
   AttnArgs a;
   a.Q = Q;
@@ -460,6 +467,10 @@ extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t*
   a.one = one, a.causal = causal ? 1 : 0;
   a.mo = m_o, a.so = s_o, a.rndo = s_o ? 1 << (s_o - 1) : 0;
   a.mo24 = m_o > -(1 << 23) && m_o < (1 << 23);
+  a.clo_o = (int)std::max(-128ll * (1ll << s_o), I32_MIN);
+  a.chi_o = (int)std::min(128ll * (1ll << s_o) - 1, I32_MAX);
+  a.ldo32 = (int)st[11];
+  a.obytes = (int)(31 * st[11] + D);
   a.nqt = T / 32;
   auto magic = [](int d, unsigned long long& m, int& k) {
     k = 0;
@@ -468,6 +479,7 @@ extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t*
   };
   magic(a.nqt, a.mq, a.kq);
   magic(batch1, a.mb, a.kb);
+  magic(one, a.mone, a.kone);
   const unsigned grid = (unsigned)((long long)batch0 * batch1 * a.nqt);
   if (flags & ANVIL_ATTN_S24)
     launch_attention_nt<true>(a, D, grid, ctx->stream);

@@ -202,8 +202,9 @@ int anvil_softmax_lut_ex(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, in
  *   O      = clamp_i8((p V * m_o + 2^(s_o-1)) >> s_o)
  * bit-exact with the three ops, without writing scores or p. Q, K: (T, D) rows; Vt: V transposed, (D, T) rows;
  * O: (T, D) rows. strides = {sq0, sq1, ldq, sk0, sk1, ldk, sv0, sv1, ldv, so0, so1, ldo} in elements (bytes): the
- * first nine and Q, K, Vt multiples of 16, the O strides and O multiples of 4; ldk >= D, ldv >= T, and T * ldk,
- * D * ldv below 2^31 (one head of K and of Vt is read through 32-bit offsets). T a multiple of 32 in [32, 1024];
+ * first nine and Q, K, Vt multiples of 16, the O strides and O multiples of 4; ldk >= D, ldv >= T, ldo >= D, and
+ * T * ldk, D * ldv, 32 * ldo below 2^31 (one head of K and of Vt is read, and 32 rows of O are written, through
+ * 32-bit offsets). T a multiple of 32 in [32, 1024];
  * D in {16, 32, 64, 128}; 1 <= one <= 127; lut int32[256] with every entry >= 0 and lut[255] >= 1.
  * flags must hold ANVIL_OP_UNCHECKED: the caller has proven every int32 intermediate of the three ops in range;
  * ANVIL_ATTN_S24 adds that every |Q K^T| and |m_s| is below 2^23 (the score requant multiply is then 24-bit). */

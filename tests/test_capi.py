@@ -107,6 +107,10 @@ def test_attention_argument_validation_precedes_the_device():
         s = (C.c_int64 * 12)(*[64 * 64, 64, 64] + [64 * 64, 64, ldk] + [64 * 64, 64, ldv] + [64 * 64, 64, 64])
         with pytest.raises(ValueError, match="K row stride"):
             att(64, 64, 127, 1, s)
+    for ldo in (32, 1 << 26):                                       # O rows < D apart, 32 rows past 2^31
+        s = (C.c_int64 * 12)(*[64 * 64, 64, 64] * 3 + [64 * 64, 64, ldo])
+        with pytest.raises(ValueError, match="O row stride"):
+            att(64, 64, 127, 1, s)
     with pytest.raises(ValueError, match="null context"):
         att(64, 64, 127, 1)
 
