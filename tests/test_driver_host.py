@@ -363,6 +363,27 @@ def test_attention_inputs_are_planned_head_blocked(fake):
     assert "om" in {v.owner.sym_str for v in cm.plan(nb).kb_values}
 
 
+def test_single_head_attention_output_is_head_blocked(fake):
+    """One head of 64: om is o itself, one 64-wide block. The attention batches over the sequences (one head, its
+    stride unused) and writes o as T * 64-byte blocks of rows, which the y product reads K-blocked; the output
+    equals the oracle's."""
+    spec = models.BlockSpec(n_embd=64, n_head=1, seq=64, calib_batches=2, calib_batch=2)
+    built = models.build(spec, 12, stored=False)
+    cm = anvil_mi355x.compile(built)
+    nb = 2
+    x = models.eval_inputs(built.spec, nb, 12)
+    res = cm.run(x, "mi355x", batch=True, keep="outputs")
+    want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
+    assert np.array_equal(res.ints["out"], want.values["out"])
+    assert "om" in {v.owner.sym_str for v in cm.plan(nb).kb_values}
+    att = [c for c in fake.calls if c[0] == "attention"][0]
+    T = spec.seq
+    assert att[1:5] == (1, nb, T, 64)                             # one head: the sequences are the batch
+    assert att[5][9:12] == (0, T * 64, 64)
+    y = [c for c in fake.calls if c[0] == "gemm_add"][0]
+    assert y[7] & rt.GEMM_A_KBLOCK
+
+
 def test_kblocked_planning_only_for_values_read_by_linear_products(fake):
     """Of the candidates, only `a` (an rmsnorm-fed linear result read by two linear products and nothing else) is
     stored K-blocked; `h` (also read by an add), `b` (returned) and `c` (read by a lut) stay row-major. Every

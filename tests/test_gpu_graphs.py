@@ -162,3 +162,20 @@ def test_kblocked_intermediates_on_the_device():
     assert sorted(v.owner.sym_str for v in cm.plan(5).kb_values) == ["a"]
     for k in ("b", "r1", "d", "e"):
         assert np.array_equal(res.ints[k], want.values[k]), k
+
+
+@pytest.mark.parametrize("n_embd,n_head,seq", [(64, 1, 96), (128, 2, 64), (256, 4, 128)])
+def test_head_blocked_attention_blocks(n_embd, n_head, seq):
+    """Blocks with head dim 64 and one, two or four heads, keep="outputs": q, k and the attention output o are
+    head-blocked (o written into the K-blocked storage the y product reads, om planned K-blocked), and the output
+    equals the oracle's for every sequence of the batch."""
+    spec = models.BlockSpec(n_embd=n_embd, n_head=n_head, seq=seq, calib_batches=2, calib_batch=2)
+    built = models.build(spec, 11, stored=False)
+    cm = anvil_mi355x.compile(built)
+    nb = 3
+    x = models.eval_inputs(built.spec, nb, 11)
+    res = cm.run(x, "mi355x", batch=True, keep="outputs")
+    want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
+    assert "om" in {v.owner.sym_str for v in cm.plan(nb).kb_values}
+    assert np.array_equal(res.ints[cm.outputs[0]], want.values[cm.outputs[0]])
+
