@@ -70,9 +70,23 @@ __device__ __forceinline__ unsigned udiv_magic(unsigned n, unsigned long long m,
 
 constexpr int A_THREADS = 256;
 
-__device__ __forceinline__ int sbyte(unsigned v, int e) { return (int)(int8_t)(v >> (8 * e)); }
 
 typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+
+// 4 * (byte e of v), zero-extended: one SDWA shift, the byte offset of entry e of an int table
+template <int E>
+__device__ __forceinline__ unsigned byte_x4(unsigned v) {
+  unsigned r;
+  if constexpr (E == 0)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(r) : "v"(v));
+  else if constexpr (E == 1)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(r) : "v"(v));
+  else if constexpr (E == 2)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(r) : "v"(v));
+  else
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(r) : "v"(v));
+  return r;
+}
 
 
 // One 16-byte chunk of a K-contiguous operand row; zero past the head dim.
@@ -90,7 +104,7 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
   // the partial-O space (two slots of 32 rows) also holds the p tables (32 rows of 256 bytes) and the tile maxima
   constexpr int OSLOT = std::max(32 * OROW, (32 * 256 + A_THREADS * NTW) / 8);
   __shared__ __attribute__((aligned(16))) int lut_s[256];
-  __shared__ double lutd_s[260];                            // the LUT as doubles, for the p tables (+ 4 zeros)
+  __shared__ double lutd_s[256];                            // the LUT as doubles, for the p tables
   __shared__ __attribute__((aligned(16))) int red_m[4][32];   // after the max: the rows' (A, B) as doubles
   __shared__ int red_s[4][32];
   __shared__ int dlow_s[32];
@@ -200,7 +214,6 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
   if (half == 0) red_m[w][l32] = mx;
   lut_s[t] = lutv;
   lutd_s[t] = (double)lutv;
-  if (t < 4) lutd_s[256 + t] = 0.0;                      // read by the top dword of a row table (scores above the max)
   // the p tables (8 KiB of the partial-O space, filled after the next barrier) start zeroed, 32 bytes a thread
   int8_t* ptab = reinterpret_cast<int8_t*>(&opart[0][0]);
   *reinterpret_cast<v4i*>(ptab + 32 * t) = v4i{0, 0, 0, 0};
@@ -209,18 +222,26 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
   mx = max(max(red_m[0][l32], red_m[1][l32]), max(red_m[2][l32], red_m[3][l32]));
 
   // ---- 2. partial exp sums over the kept keys
-  const int* erow = lut_s + (255 - mx);                   // erow[s] = lut[s - max + 255]
+  // Each score byte s becomes its LUT index d = s - max + 255, in [0, 255] for every score of the row (-128 <= s <=
+  // max): in unsigned form s + 128 plus 127 - max, which no byte carries out of, so one xor-add rewrites four
+  // bytes. A lookup is then one SDWA shift to the entry's byte offset, the table base folding into the LDS offset.
+  const unsigned dadd = 0x01010101u * (unsigned)(127 - mx);
+  const uint8_t* lutb = reinterpret_cast<const uint8_t*>(lut_s);
   int S = 0;
   static_for<NTW>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     if (w + 4 * i < ntiles) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) S += erow[sbyte(sc[i][r >> 2], r & 3)];
+      for (int g = 0; g < 4; ++g) sc[i][g] = (sc[i][g] ^ 0x80808080u) + dadd;
+      static_for<16>([&](auto rc) {
+        constexpr int r = decltype(rc)::value;
+        S += *reinterpret_cast<const int*>(lutb + byte_x4<r & 3>(sc[i][r >> 2]));
+      });
     }
   });
   if (a.causal && ((ntiles - 1 - w) & 3) == 0 && w < ntiles) {   // this wave holds the diagonal tile: its masked
     const int lim = l32 - 16 * half;                              // keys (those past r = lim) added lut terms of
-    S -= (15 - max(-1, min(lim, 15))) * erow[a.clo >> a.ss];      // the lowest score
+    S -= (15 - max(-1, min(lim, 15))) * lut_s[(a.clo >> a.ss) + 255 - mx];   // the lowest score
   }
   S += __shfl_xor(S, 32, 64);
   if (half == 0) red_s[w][l32] = S;
@@ -261,15 +282,14 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
   }
   __syncthreads();
   const double qa = qab[l32], qb = qab[32 + l32];
-  // The tables sit in the partial-O space, 256 bytes a row: the entry of score s in row r is at column
-  // (s & 255) ^ 4 r, so a lookup address is the row base with its low byte replaced by the swizzled score byte
-  // (one v_perm), and the 32 rows' entries for one s fall in 32 different banks. The XOR keeps each dword whole, so
-  // the table is written a dword at a time: dword c holds scores 4 c .. 4 c + 3 (c = -32 .. 31), d = 4 c + e - max + 255.
+  // The tables sit in the partial-O space, 256 bytes a row, indexed by d (the score bytes hold d since phase 2): the
+  // entry of d in row r is at column d ^ 4 r, so a lookup address is the row base with its low byte replaced by the
+  // swizzled byte (one v_perm), and the 32 rows' entries for one d fall in 32 different banks. The XOR keeps each
+  // dword whole, so the table is written a dword at a time: dword c holds d = 4 c .. 4 c + 3.
   // An entry is y = fma(lut[d], A, B - 1/2), within 2^-45 of n / S - 1/2 + 2^-40 and never a half-integer, so
   // adding 1.5 2^52 rounds it to n // S, which is then the low dword of the sum: two full-rate float64 operations.
-  // A row writes the dwords from the one holding its max down to the one holding score dlow + max - 255 (>= -128, as
-  // dlow >= 127 - max, so every d >= 0): each byte of them with a score up to the max gets its exact quotient (0 below
-  // d0), and a byte above the max (d up to 258, the zero pad of lutd_s) gets 0 or less, read by no kept key.
+  // A row writes the dwords from the top one (d = 255, its max) down to the one holding d = dlow; a byte of the
+  // bottom dword below dlow gets its exact quotient too (0 below d0) or belongs to a score below -128, read by no key.
   constexpr int PT = 256;
   const int cx = 4 * l32;
   int sthr;                                              // the row's scores below it have p = 0
@@ -278,13 +298,12 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
     int8_t* trow = ptab + l32 * PT;
     const int dlow = dlow_s[l32];
     sthr = dlow + mx - 255;
-    const int ctop = mx >> 2, cbot = (dlow + mx - 255) >> 2;   // arithmetic shifts: floor
-    for (int c = ctop - part; c >= cbot; c -= 8) {
-      const double* lp = lutd_s + (4 * c - mx + 255);
+    for (int c = 63 - part; c >= dlow >> 2; c -= 8) {
+      const double* lp = lutd_s + 4 * c;
       int v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = __double2loint(__builtin_fma(lp[e], qa, qb) + 0x1.8p52);
-      *reinterpret_cast<unsigned*>(trow + ((4 * c & 255) ^ cx)) = pack4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<unsigned*>(trow + ((4 * c) ^ cx)) = pack4(v[0], v[1], v[2], v[3]);
     }
     __syncthreads();
   }
