@@ -4,11 +4,13 @@ in parallel; each element goes through the same operation as in one whole-array 
 Arrays below PAR_MIN elements take the single call."""
 import concurrent.futures
 import os
+import threading
 
 import numpy as np
 
 PAR_MIN = 1 << 20
 _pool = None
+_pool_lock = threading.Lock()
 
 
 def _workers() -> int:
@@ -21,15 +23,18 @@ def _workers() -> int:
 
 def pool():
     global _pool
-    if _pool is None:
-        _pool = concurrent.futures.ThreadPoolExecutor(max_workers=_workers(), thread_name_prefix="anvil-host")
-    return _pool
+    with _pool_lock:                  # runs from several host threads at once create one pool between them
+        if _pool is None:
+            _pool = concurrent.futures.ThreadPoolExecutor(max_workers=_workers(), thread_name_prefix="anvil-host")
+        return _pool
 
 
 def _after_fork():
-    # a forked child has none of the parent's pool threads: it starts its own pool when it needs one
-    global _pool
+    # a forked child has none of the parent's pool threads (and a lock possibly taken by one of them): it starts its
+    # own pool when it needs one
+    global _pool, _pool_lock
     _pool = None
+    _pool_lock = threading.Lock()
 
 
 os.register_at_fork(after_in_child=_after_fork)

@@ -48,3 +48,25 @@ def test_all_finite(par_min, bad):
     x[-1, -1, -1] = bad                                           # in the last chunk
     assert not hostpar.all_finite(x)
     assert not hostpar.all_finite(x[:, ::2, :])                   # row 32 of 33 is kept by the stride
+
+
+def test_one_pool_for_concurrent_callers(monkeypatch):
+    """Host threads that start runs at the same moment share one pool, and their results are each the single call's."""
+    import threading
+    monkeypatch.setattr(hostpar, "PAR_MIN", 1)
+    monkeypatch.setattr(hostpar, "_pool", None)
+    a = np.arange(-5000, 5000, dtype=np.int16).reshape(100, 100)
+    pools, outs, go = [], [None] * 8, threading.Barrier(8)
+
+    def work(i):
+        go.wait()
+        pools.append(hostpar.pool())
+        outs[i] = hostpar.astype(a[i % 3:], np.int64)
+
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert len({id(p) for p in pools}) == 1
+    assert all(np.array_equal(o, a[i % 3:].astype(np.int64)) for i, o in enumerate(outs))
