@@ -157,7 +157,7 @@ __global__ __launch_bounds__(G_THREADS) void gemm_i8_kernel(GemmArgs g) {
   const int rows_a = g.M - m0, rows_b = g.N - n0;
   const int K = g.causal == 2 ? min(g.K, m0 + BM) : g.K;
 
-  if (g.lut) lut_s[t] = g.lut[t];
+  if (g.lut) lut_s[t ^ 128] = g.lut[t];               // rotated: the entry of v at index v & 255
 
   const int lc = t % CPR, lr = t / CPR;
   constexpr int RSTEP = G_THREADS / CPR;
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(G_THREADS) void gemm_i8_kernel(GemmArgs g) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           v[e] = rq<CHECKED>(acc[i][j][4 * q + e], g, lo, hi, bad);
-          if (OSZ == 1 && g.lut) v[e] = lut_s[v[e] + 128];
+          if (OSZ == 1 && g.lut) v[e] = lut_s[(uint8_t)v[e]];
         }
         int8_t* dst = smem + m_l * SROW + n_l * OSZ;
         if (OSZ == 1) {
@@ -346,15 +346,35 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 template <int BM, int BN>
 constexpr int fast_occupancy() { return BM * BN <= 128 * 128 ? 3 : (BM * BN <= 256 * 128 ? 2 : 1); }
 
-// requant (+ LUT) of one lane's 16 accumulators into 16 results
+// (x >> sh) & 255 by one SDWA shift (byte 0 written, the rest zeroed): the LUT index of a clamped int8 result
+__device__ __forceinline__ unsigned sra_byte(int x, int sh) {
+  unsigned d;
+  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+      : "=v"(d) : "s"(sh), "v"(x));
+  return d;
+}
+
+// requant (+ LUT) of one lane's 16 accumulators into 16 results. With a LUT (int8 results, the table staged rotated
+// so that the entry of v sits at index v & 255) the clamp runs before the shift, with bounds [-128, 127] << shift
+// saturated to int32, and one SDWA shift gives the lookup index.
 template <int OSZ, bool MUL24, bool LUT>
 __device__ __forceinline__ void requant16(const v16i& a, int mult, int rnd, int shift, const int8_t* lut_s, int v[16]) {
-  const int lo = OSZ == 1 ? -128 : -32768, hi = OSZ == 1 ? 127 : 32767;
+  if constexpr (LUT) {
+    static_assert(OSZ == 1, "a LUT epilogue has int8 results");
+    const int clo = (int)max(-128ll << shift, (long long)INT32_MIN);
+    const int chi = (int)min((128ll << shift) - 1, (long long)INT32_MAX);
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int x = MUL24 ? (__mul24(a[e], mult) + rnd) : (a[e] * mult + rnd);
-    v[e] = min(max(x >> shift, lo), hi);
-    if (LUT) v[e] = lut_s[v[e] + 128];
+    for (int e = 0; e < 16; ++e) {
+      const int x = MUL24 ? (__mul24(a[e], mult) + rnd) : (a[e] * mult + rnd);
+      v[e] = lut_s[sra_byte(med3i(x, clo, chi), shift)];
+    }
+  } else {
+    const int lo = OSZ == 1 ? -128 : -32768, hi = OSZ == 1 ? 127 : 32767;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int x = MUL24 ? (__mul24(a[e], mult) + rnd) : (a[e] * mult + rnd);
+      v[e] = min(max(x >> shift, lo), hi);
+    }
   }
 }
 
@@ -445,11 +465,13 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
     }
   };
   const bool lut = OSZ == 1 && g.lut;
-  if (interior) {
-    if (lut) run(std::true_type{}, std::true_type{}); else run(std::false_type{}, std::true_type{});
-  } else {
-    if (lut) run(std::true_type{}, std::false_type{}); else run(std::false_type{}, std::false_type{});
-  }
+  auto pick = [&](auto full_c) {
+    if constexpr (OSZ == 1) {
+      if (lut) return run(std::true_type{}, full_c);
+    }
+    run(std::false_type{}, full_c);
+  };
+  if (interior) pick(std::true_type{}); else pick(std::false_type{});
 }
 
 // One output tile of the fast kernel: logical tile pid of batch entry bz (the XCD remap below assumes pid and the
@@ -504,7 +526,7 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
   const __amdgpu_buffer_rsrc_t ra = uniform_rsrc(Ab, operand_bytes(rows_a, g.lda, g.kba, K));
   const __amdgpu_buffer_rsrc_t rb = uniform_rsrc(Bb, operand_bytes(rows_b, g.ldb, g.kbb, K));
 
-  if (g.lut) lut_s[t] = g.lut[t];
+  if (g.lut) lut_s[t ^ 128] = g.lut[t];               // rotated: the entry of v at index v & 255
 
   // per-lane global byte offsets (without k0) of the chunks this wave loads, and their K offsets
   unsigned offa[JA], offb[JB];
@@ -691,7 +713,7 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
             const int a = acc[i][j][4 * q + e];
             const int x = MUL24 ? (__mul24(a, mult) + rnd) : (a * mult + rnd);
             v[e] = min(max(x >> shift, lo), hi);
-            if (LUT) v[e] = lut_s[v[e] + 128];
+            if (LUT) v[e] = lut_s[(uint8_t)v[e]];
           }
           if (OSZ == 1) {
             const unsigned t01 = __builtin_amdgcn_perm((unsigned)v[1], (unsigned)v[0], 0x0c0c0400u);
@@ -822,7 +844,7 @@ __global__ __launch_bounds__(G_THREADS) void splitk_reduce(GemmArgs g) {
   const int tile = blockIdx.x / (T / BAND), band = blockIdx.x % (T / BAND);
   const int tm = tile / g.tiles_n, tn = tile % g.tiles_n;
   const bool lut = OSZ == 1 && g.lut;
-  if (lut) lut_s[threadIdx.x] = g.lut[threadIdx.x];
+  if (lut) lut_s[threadIdx.x ^ 128] = g.lut[threadIdx.x];   // rotated: the entry of v at index v & 255
   __syncthreads();
   const int rr = band * BAND + threadIdx.x / 32 * 2, c4 = threadIdx.x % 32 * 4;
   const int lo = OSZ == 1 ? -128 : -32768, hi = OSZ == 1 ? 127 : 32767;
@@ -841,7 +863,7 @@ __global__ __launch_bounds__(G_THREADS) void splitk_reduce(GemmArgs g) {
     for (int e = 0; e < 4; ++e) {
       const int x = MUL24 ? (__mul24(a[e], g.mult) + g.rnd) : (a[e] * g.mult + g.rnd);
       v[e] = min(max(x >> g.shift, lo), hi);
-      if (lut) v[e] = lut_s[v[e] + 128];
+      if (lut) v[e] = lut_s[(uint8_t)v[e]];
     }
     char* c = Cb + cpos(g, m, n) * OSZ;
     if (OSZ == 1 && g.vec_store && n + 3 < g.N) {
@@ -914,13 +936,14 @@ __global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) voi
   static_assert(IA % NW == 0 && IB % NW == 0, "each wave issues an equal share of a stage");
   constexpr int JA = IA / NW, JB = IB / NW, G = JA + JB;
   constexpr int STAGE = (BM + BN) * BK;
+  // the LUT first, at a low LDS address that a lookup's offset field can hold (past the stages it would not fit)
+  __shared__ __attribute__((aligned(2048))) int8_t lut_s[256];
   __shared__ __attribute__((aligned(1024))) int8_t L0[STAGE];
   __shared__ __attribute__((aligned(1024))) int8_t L1[STAGE];
   __shared__ __attribute__((aligned(1024))) int8_t L2[NS > 2 ? STAGE : 16];
   __shared__ __attribute__((aligned(1024))) int8_t L3[NS > 3 ? STAGE : 16];
   __shared__ __attribute__((aligned(1024))) int8_t L4[NS > 4 ? STAGE : 16];
   __shared__ __attribute__((aligned(1024))) int8_t L5[NS > 5 ? STAGE : 16];
-  __shared__ int8_t lut_s[256];
   // the array of pipeline stage u (mod NS), chosen at compile time so that every LDS access has a known array
   auto arr = [&](auto u) -> int8_t* {
     constexpr int U = decltype(u)::value % NS;
@@ -971,7 +994,7 @@ __global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) voi
 
   Tile cur = tile_of(0);
   if (!cur.valid) return;
-  if (g.lut && t < 256) lut_s[t] = g.lut[t];
+  if (g.lut && t < 256) lut_s[t ^ 128] = g.lut[t];   // rotated: the entry of v at index v & 255
 
   unsigned offa[JA], offb[JB];
   int ka[JA], kb[JB];
