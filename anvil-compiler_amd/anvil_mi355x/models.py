@@ -152,6 +152,91 @@ def float_forward_amax(spec: BlockSpec, params, x, amax: dict):
         rec("logits", hf @ params["wte"].T)
 
 
+def device_params(params, device):
+    """The float weights on a torch device as float32: (weights, transposed 2-D weights, contiguous)."""
+    import torch
+    W = {k: torch.as_tensor(np.ascontiguousarray(v), dtype=torch.float32, device=device) for k, v in params.items()}
+    return W, {k: v.t().contiguous() for k, v in W.items() if v.dim() == 2}      # x @ w.T as x @ (w.T, contiguous)
+
+
+def float_forward_amax_torch(spec: BlockSpec, W, Wt, x, amax: dict, device):
+    """float_forward_amax with the forward on a torch device (weights from device_params): float32 throughout, GELU
+    in float64 as on the host. The same max-abs values up to float32 rounding of the products and reductions."""
+    import torch
+    C, H, T = spec.n_embd, spec.n_head, spec.seq
+    d = C // H
+    f32 = dict(dtype=torch.float32, device=device)
+    keep = torch.ones((T, T), dtype=torch.bool, device=device).tril()
+    eps = torch.tensor(np.float32(EPS), **f32)
+
+    def rec(k, v):
+        amax[k] = max(amax.get(k, 0.0), float(v.abs().max()))
+
+    def rms(v, w):
+        return v / torch.sqrt((v * v).mean(-1, keepdim=True) + eps) * w
+
+    def heads(v):                                   # (N, T, C) -> (N, H, T, d), contiguous
+        return v.reshape(v.shape[0], T, H, d).transpose(1, 2).contiguous()
+
+    x = torch.as_tensor(np.asarray(x, dtype=np.float32), **f32)
+    for L in _prefixes(spec):
+        h1 = rms(x, W[L + "ln1"])
+        rec(L + "h1", h1)
+        q, k, v = (h1 @ Wt[L + n] for n in ("q", "k", "v"))
+        for n, t in (("q", q), ("k", k), ("v", v)):
+            rec(L + n, t)
+        N = x.shape[0]
+        qh, kh, vh = heads(q), heads(k), heads(v)
+        sc = (qh @ kh.transpose(-1, -2).contiguous()) * np.float32(1.0 / math.sqrt(d))
+        if spec.causal:
+            rec(L + "scores", torch.where(keep, sc, torch.zeros((), **f32)))
+            sc = sc.masked_fill(~keep, float("-inf"))
+        else:
+            rec(L + "scores", sc)
+        sc = sc - sc.amax(-1, keepdim=True)
+        e = torch.exp(sc)
+        p = e / e.sum(-1, keepdim=True)
+        o = p @ vh
+        rec(L + "o", o)
+        om = o.transpose(1, 2).reshape(N, T, C)
+        y = om @ Wt[L + "y"]
+        rec(L + "y", y)
+        r1 = x + y
+        rec(L + "r1", r1)
+        h2 = rms(r1, W[L + "ln2"])
+        rec(L + "h2", h2)
+        fc = h2 @ Wt[L + "fc"]
+        rec(L + "fc", fc)
+        f64 = fc.double()
+        ge = (0.5 * f64 * (1 + torch.erf(f64 / math.sqrt(2)))).float()
+        rec(L + "gelu", ge)
+        proj = ge @ Wt[L + "proj"]
+        rec(L + "proj", proj)
+        x = r1 + proj
+        rec(L + "out", x)
+    if spec.vocab:
+        hf = rms(x, W["lnf"])
+        rec("hf", hf)
+        rec("logits", hf @ Wt["wte"])
+
+
+def calibrate_on_device(spec: BlockSpec, params, tag: int, device="cuda"):
+    """calibrate() with the float forward on a torch device (reference quantize.py:276-300 runs it in torch). The
+    inputs, their scale and their fake quantization stay on the host, so the input scale is calibrate()'s; the
+    max-abs values agree with the host forward's to float32 rounding, so a graph built from them may differ from the
+    tracked calibration's in the last step of a constant. For new specs and large calibration sets; the tracked
+    calibration fixes the benchmark's graphs."""
+    xs = [to_float_input(spec, params, calib_inputs(spec, i, tag)) for i in range(spec.calib_batches)]
+    sin = max(float(np.abs(x).max()) for x in xs) / 127
+    amax = {}
+    W, Wt = device_params(params, device)
+    for x in xs:
+        deq = (np.clip(np.rint(x / sin), -128, 127) * sin).astype(np.float32)
+        for lo in range(0, len(deq), 4):
+            float_forward_amax_torch(spec, W, Wt, deq[lo:lo + 4], amax, device)
+    return sin, amax
+
+
 # ------------------------------------------------------------------------------------------- graph build
 
 @dataclass
@@ -323,13 +408,16 @@ def write_calibration(spec: BlockSpec, tag: int) -> Path:
     return path
 
 
-def build(spec: BlockSpec, tag: int, stored: bool = True) -> Built:
+def build(spec: BlockSpec, tag: int, stored: bool = True, calib_device=None) -> Built:
     """The quantized graph of `spec` (weights seed spec.wseed, calibration seed tag). With stored=True (the default)
     the calibration (input scale and max-abs values) comes from the tracked calib/ file of this spec, tag and
-    calibration code when there is one, so every machine builds the same constants; otherwise it is computed here."""
+    calibration code when there is one, so every machine builds the same constants; otherwise it is computed here,
+    on the host, or with the float forward on the torch device `calib_device` when one is given."""
     params = init_params(spec)
     path = calib_path(spec, tag)
-    if stored and path.exists():
+    if calib_device is not None:
+        sin, amax = calibrate_on_device(spec, params, tag, calib_device)
+    elif stored and path.exists():
         body = json.loads(path.read_text())
         sin, amax = body["sin"], body["amax"]
     else:

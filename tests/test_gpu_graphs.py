@@ -179,3 +179,4 @@ def test_head_blocked_attention_blocks(n_embd, n_head, seq):
     assert "om" in {v.owner.sym_str for v in cm.plan(nb).kb_values}
     assert np.array_equal(res.ints[cm.outputs[0]], want.values[cm.outputs[0]])
 
+
