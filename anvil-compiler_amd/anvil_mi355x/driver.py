@@ -93,6 +93,9 @@ def _checked_graph(module, consts, prove=True):
     return module, consts
 
 
+PINNED_MAX = 1 << 28       # read-back buffers up to this size download into page-locked host memory
+
+
 class _Plan:
     """Buffers, views and launches of one (batch, keep) configuration."""
 
@@ -103,6 +106,7 @@ class _Plan:
         self.works: list = []          # per step: (kind, algorithmic int ops, algorithmic HBM bytes)
         self.fused_adds: set = set()   # add_requant ops computed in a GEMM epilogue
         self.stage: dict = {}          # device staging buffers of float inputs and token ids
+        self.host_stage: dict = {}     # page-locked host buffers the read-back downloads into, by device buffer
         self.kb_values: set = set()    # values stored K-blocked (read only by GEMMs)
 
     def buf(self, nbytes, name=""):
@@ -918,16 +922,29 @@ class CompiledModel:
             times[label] = times.get(label, 0.0) + 1e3 * self.dev.elapsed_ms(4, 5)
         return times
 
-    def read(self, plan, syms, nb=None, batch=True) -> dict:
+    def read(self, plan, syms, nb=None, batch=True, narrow=None) -> dict:
+        """sym -> int64 array of each of syms, read back from the device. A device buffer of up to PINNED_MAX bytes
+        is downloaded into a page-locked buffer of the plan (DMA straight into it, no pageable staging) and widened
+        from there. With a dict `narrow`, also sym -> the same values as a view at their stored dtype (no copy, into
+        that buffer: use it before the plan's next read)."""
         by_sym = {op.sym_str: op.result for op in self.ops if op.sym_str is not None}
         cache, out = {}, {}
         for s in syms:
             v = plan.views[by_sym[s]]
             key = id(v.buf)
             if key not in cache:
-                cache[key] = v.buf.mem.download((v.buf.nbytes // v.itemsize,), rt.NP_DTYPE[v.dtype])
+                into = None
+                if v.buf.nbytes <= PINNED_MAX:
+                    into = plan.host_stage.get(key)
+                    if into is None or into.nbytes < v.buf.nbytes:
+                        into = plan.host_stage[key] = self.dev.host_alloc(v.buf.nbytes)
+                cache[key] = v.buf.mem.download((v.buf.nbytes // v.itemsize,), rt.NP_DTYPE[v.dtype], into=into)
+            whole = batch or by_sym[s] in self.is_const
             a = v.read(cache[key])
-            out[s] = a if batch or by_sym[s] in self.is_const else a[0]
+            out[s] = a if whole else a[0]
+            if narrow is not None:
+                n = v.view(cache[key])
+                narrow[s] = n if whole else n[0]
         return out
 
     def run(self, x, backend: str = "mi355x", *, quantized=False, keep="outputs", batch=False, profile=False,
@@ -955,9 +972,11 @@ class CompiledModel:
             self.dev.record(3)
             self.dev.sync()
             total_ms = self.dev.elapsed_ms(2, 3)
-            ints = self.read(plan, syms, nb, batch)
+            narrow = {}
+            ints = self.read(plan, syms, nb, batch, narrow)
+            # from the stored dtype (1-2 bytes an element), before another run reuses the plan's host buffers
+            outs = [self.dequantize(s, narrow[s]) for s in self.outputs]
         cycles = {label: (times.get(label) if profile else None) for label, _, _ in plan.steps}
-        outs = [self.dequantize(s, ints[s]) for s in self.outputs]
         consts = frozenset(op.sym_str for op in self.ops if isinstance(op, g.ConstOp))
         result = {"device_ms": total_ms, "batch": nb, "kernels": len(plan.steps), "footprint": plan.footprint}
         return RunOutput(outs[0], outs, ints, cycles, result, None, consts, self)

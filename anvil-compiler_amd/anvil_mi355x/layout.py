@@ -99,13 +99,16 @@ class View:
         """Broadcast over a new leading dim of size n (stride 0)."""
         return View(self.buf, self.dtype, (n,) + self.dims, (0,) + self.strides, self.offset, self.kb)
 
-    def read(self, base: np.ndarray) -> np.ndarray:
-        """This view of `base` (the whole buffer downloaded as self.dtype) as an int64 array."""
+    def view(self, base: np.ndarray) -> np.ndarray:
+        """This view of `base` (the whole buffer downloaded as self.dtype), at that dtype, without a copy."""
         if self.kb:
             raise ValueError("K-blocked storage is planned only for values that are not read back")
-        a = np.lib.stride_tricks.as_strided(base[self.offset:], shape=self.dims,
-                                            strides=tuple(s * self.itemsize for s in self.strides))
-        return hostpar.astype(a, np.int64)
+        return np.lib.stride_tricks.as_strided(base[self.offset:], shape=self.dims,
+                                               strides=tuple(s * self.itemsize for s in self.strides))
+
+    def read(self, base: np.ndarray) -> np.ndarray:
+        """This view of `base` as a new int64 array."""
+        return hostpar.astype(self.view(base), np.int64)
 
 
 def nocopy_strides(dims, strides, newdims):

@@ -12,6 +12,7 @@ softmax row summing to zero). There is no CPU fallback: without the library ever
 from __future__ import annotations
 
 import ctypes as C
+import math
 import os
 import threading
 from pathlib import Path
@@ -43,6 +44,8 @@ SIGNATURES = {
     "anvil_sync": [_p],
     "anvil_alloc": [_p, _sz, C.POINTER(_p)],
     "anvil_free": [_p, _p],
+    "anvil_host_alloc": [_p, _sz, C.POINTER(_p)],
+    "anvil_host_free": [_p, _p],
     "anvil_upload": [_p, _p, _p, _sz],
     "anvil_download": [_p, _p, _p, _sz],
     "anvil_zero": [_p, _p, _sz],
@@ -133,17 +136,50 @@ class DeviceBuffer:
         self.dev.lib.call("anvil_upload", self.dev.ctx, C.c_void_p(self.ptr + offset), arr.ctypes.data_as(C.c_void_p),
                           C.c_size_t(arr.nbytes))
 
-    def download(self, shape, dtype, offset: int = 0) -> np.ndarray:
-        out = np.empty(shape, dtype=dtype)
-        if offset + out.nbytes > self.nbytes:
-            raise ValueError(f"download of {out.nbytes} bytes at {offset} overruns a {self.nbytes}-byte buffer")
+    def download(self, shape, dtype, offset: int = 0, into: "HostBuffer | None" = None) -> np.ndarray:
+        """The buffer's bytes from `offset` as an array of `shape` and `dtype`: a new array, or with `into` a view of
+        that page-locked buffer (valid until its next use)."""
+        count = math.prod(shape) if isinstance(shape, tuple) else int(shape)
+        nbytes = count * np.dtype(dtype).itemsize
+        if offset + nbytes > self.nbytes:
+            raise ValueError(f"download of {nbytes} bytes at {offset} overruns a {self.nbytes}-byte buffer")
+        out = np.empty(shape, dtype=dtype) if into is None else into.array(dtype, count).reshape(shape)
         self.dev.lib.call("anvil_download", self.dev.ctx, out.ctypes.data_as(C.c_void_p), C.c_void_p(self.ptr + offset),
-                          C.c_size_t(out.nbytes))
+                          C.c_size_t(nbytes))
         return out
 
     def free(self):
         if self.ptr and self.dev.ctx:
             self.dev.lib.call("anvil_free", self.dev.ctx, C.c_void_p(self.ptr))
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HostBuffer:
+    """Page-locked host memory of a Device (anvil_host_alloc), freed when collected: the target of downloads that
+    the DMA engine writes directly, with no pageable staging."""
+
+    def __init__(self, dev: "Device", nbytes: int):
+        self.dev, self.nbytes = dev, int(nbytes)
+        out = C.c_void_p()
+        dev.lib.call("anvil_host_alloc", dev.ctx, C.c_size_t(max(1, self.nbytes)), C.byref(out))
+        self.ptr = int(out.value)
+
+    def array(self, dtype, count: int) -> np.ndarray:
+        """The first `count` elements as a numpy array over this memory (no copy; it must not outlive the buffer)."""
+        nbytes = int(count) * np.dtype(dtype).itemsize
+        if nbytes > self.nbytes:
+            raise ValueError(f"{nbytes} bytes asked of a {self.nbytes}-byte host buffer")
+        return np.frombuffer((C.c_char * max(1, nbytes)).from_address(self.ptr), dtype=dtype, count=int(count))
+
+    def free(self):
+        if self.ptr and self.dev.ctx:
+            self.dev.lib.call("anvil_host_free", self.dev.ctx, C.c_void_p(self.ptr))
         self.ptr = 0
 
     def __del__(self):
@@ -166,6 +202,9 @@ class Device:
 
     def alloc(self, nbytes: int) -> DeviceBuffer:
         return DeviceBuffer(self, nbytes)
+
+    def host_alloc(self, nbytes: int) -> HostBuffer:
+        return HostBuffer(self, nbytes)
 
     def upload(self, arr: np.ndarray) -> DeviceBuffer:
         arr = np.ascontiguousarray(arr)

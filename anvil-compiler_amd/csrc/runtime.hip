@@ -137,6 +137,22 @@ int anvil_free(anvil_ctx* ctx, void* dptr) {
   return ANVIL_OK;
 }
 
+int anvil_host_alloc(anvil_ctx* ctx, size_t bytes, void** hptr) {
+  if (int r = check_ctx(ctx)) return r;
+  if (!hptr) return set_error(ANVIL_E_VALUE, "anvil_host_alloc: null output pointer");
+  *hptr = nullptr;
+  ANVIL_HIP(hipHostMalloc(hptr, bytes ? bytes : 1, hipHostMallocDefault));
+  return ANVIL_OK;
+}
+
+int anvil_host_free(anvil_ctx* ctx, void* hptr) {
+  if (int r = check_ctx(ctx)) return r;
+  if (!hptr) return ANVIL_OK;
+  ANVIL_HIP(hipStreamSynchronize(ctx->stream));
+  ANVIL_HIP(hipHostFree(hptr));
+  return ANVIL_OK;
+}
+
 int anvil_upload(anvil_ctx* ctx, void* dst, const void* src, size_t bytes) {
   if (int r = check_ctx(ctx)) return r;
   if (!bytes) return ANVIL_OK;

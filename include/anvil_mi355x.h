@@ -51,6 +51,11 @@ int anvil_sync(anvil_ctx* ctx);
 /* ------------------------------------------------------------------------------------------- memory */
 int anvil_alloc(anvil_ctx* ctx, size_t bytes, void** dptr);
 int anvil_free(anvil_ctx* ctx, void* dptr);
+/* Page-locked host memory (hipHostMalloc) for downloads that go straight to it over DMA. No counterpart in the
+ * reference (its values never leave the host): the read-back side of CompiledModel.run (anvil/driver.py:305-322)
+ * downloads into it. anvil_host_free waits for the context's stream first. */
+int anvil_host_alloc(anvil_ctx* ctx, size_t bytes, void** hptr);
+int anvil_host_free(anvil_ctx* ctx, void* hptr);
 /* Host <-> device copies on the context's stream; they complete before the call returns. */
 int anvil_upload(anvil_ctx* ctx, void* dst, const void* src, size_t bytes);
 int anvil_download(anvil_ctx* ctx, void* dst, const void* src, size_t bytes);

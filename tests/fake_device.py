@@ -29,10 +29,25 @@ class FakeBuffer:
         o = self.ptr - BASE + offset
         self.dev.heap[o:o + raw.size] = raw
 
-    def download(self, shape, dtype, offset=0):
+    def download(self, shape, dtype, offset=0, into=None):
         n = int(np.prod(shape)) * np.dtype(dtype).itemsize
         o = self.ptr - BASE + offset
-        return self.dev.heap[o:o + n].copy().view(dtype).reshape(shape)
+        if into is None:
+            return self.dev.heap[o:o + n].copy().view(dtype).reshape(shape)
+        out = into.array(dtype, n // np.dtype(dtype).itemsize).reshape(shape)
+        out.view(np.uint8).reshape(-1)[:] = self.dev.heap[o:o + n]
+        return out
+
+
+class FakeHostBuffer:
+    """Host memory standing in for a page-locked buffer: downloads write into it and views of it are reused."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.mem = np.zeros(max(1, self.nbytes), dtype=np.uint8)
+
+    def array(self, dtype, count):
+        return self.mem[:int(count) * np.dtype(dtype).itemsize].view(dtype)
 
     def free(self):
         pass
@@ -56,6 +71,10 @@ class FakeDevice:
 
     def alloc(self, nbytes):
         return FakeBuffer(self, nbytes)
+
+    def host_alloc(self, nbytes):
+        self.host_allocs = getattr(self, "host_allocs", 0) + 1
+        return FakeHostBuffer(nbytes)
 
     def upload(self, arr):
         arr = np.ascontiguousarray(arr)

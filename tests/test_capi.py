@@ -43,6 +43,10 @@ def test_null_context_is_a_value_error():
         lib.call("anvil_gemm_i8", None, None, None, None, 1, 1, 1, 1, 1, None, 1, 0, None, 1)
     with pytest.raises(ValueError):
         lib.call("anvil_init", 0, None)            # null output pointer
+    with pytest.raises(ValueError, match="null context"):
+        lib.call("anvil_host_alloc", None, 16, None)
+    with pytest.raises(ValueError, match="null context"):
+        lib.call("anvil_host_free", None, None)
 
 
 def test_gemm_argument_validation_precedes_the_device():

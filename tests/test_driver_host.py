@@ -403,3 +403,24 @@ def test_kblocked_planning_only_for_values_read_by_linear_products(fake):
     assert sum(bool(f & rt.GEMM_C_KBLOCK) for f in gemms) == 1      # a
     assert sum(bool(f & rt.GEMM_A_KBLOCK) for f in gemms) == 2      # c and d read a K-blocked
     assert all(f & rt.GEMM_B_KBLOCK for f in gemms)             # every weight
+
+
+def test_read_back_reuses_page_locked_buffers(fake):
+    """cm.run downloads into the plan's page-locked host buffers (one per read-back device buffer, allocated once)
+    and returns new arrays: a second run leaves the first run's ints and dequantized outputs as they were, and both
+    equal the oracle's."""
+    spec = models.BlockSpec(n_embd=64, n_head=1, seq=32, calib_batches=2, calib_batch=2)
+    built = models.build(spec, 14, stored=False)
+    cm = anvil_mi355x.compile(built)
+    xa, xb = models.eval_inputs(built.spec, 2, 14, 0), models.eval_inputs(built.spec, 2, 14, 1)
+    ra = cm.run(xa, "mi355x", batch=True)
+    kept = {k: v.copy() for k, v in ra.ints.items()}, ra.output.copy()
+    allocs = fake.host_allocs
+    rb = cm.run(xb, "mi355x", batch=True)
+    assert fake.host_allocs == allocs == 2                        # x and out, reused by the second run
+    assert all(np.array_equal(ra.ints[k], v) for k, v in kept[0].items()) and np.array_equal(ra.output, kept[1])
+    for x, r in ((xa, ra), (xb, rb)):
+        want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
+        assert np.array_equal(r.ints["out"], want.values["out"]) and np.array_equal(r.ints["x"], want.values["x"])
+        assert np.array_equal(r.output, want.values["out"] * cm.scale("out"))
+    assert not np.array_equal(ra.ints["out"], rb.ints["out"])

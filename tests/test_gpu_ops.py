@@ -545,3 +545,20 @@ def test_embed_quantize(dev, dtype):
     dev.sync()
     assert np.array_equal(out.download((B, T, C), rt.NP_DTYPE[dtype]).astype(np.int64), want)
     assert (want == lo).any() and (want == hi).any()           # saturation on both sides is exercised
+
+
+def test_page_locked_download_round_trip(dev):
+    """anvil_host_alloc memory as a download target: every byte of a device buffer arrives, a second download into
+    the same host buffer replaces the first, and an oversized request is refused before the copy."""
+    rng = np.random.default_rng(77)
+    a = rng.integers(-128, 128, (3, 1000), dtype=np.int8)
+    b = rng.integers(-2 ** 15, 2 ** 15, (1500,), dtype=np.int16)
+    da, db = dev.upload(a), dev.upload(b)
+    host = dev.host_alloc(3000)
+    got = da.download((3, 1000), np.int8, into=host)
+    assert np.array_equal(got, a)
+    got = db.download((1500,), np.int16, into=host)
+    assert np.array_equal(got, b) and np.array_equal(host.array(np.int16, 1500), b)
+    with pytest.raises(ValueError):
+        da.download((3001,), np.int8, into=host)
+    host.free()
