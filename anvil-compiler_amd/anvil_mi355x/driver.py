@@ -844,9 +844,9 @@ class CompiledModel:
             else:
                 if self.scale(sym) is None:
                     raise ValueError(f"input {sym!r} has no scale: pass integer inputs with quantized=True")
-                if v.dtype.kind == "f" and not hostpar.all_finite(v):
-                    raise ValueError(f"input {sym!r} has NaN or infinite values")
-                # quantized on the device (clamp(rint(x / scale)) in float64, as quantize_input does on the host)
+                # quantized on the device (clamp(rint(x / scale)) in float64, as quantize_input does on the host);
+                # the kernel also flags NaN and infinite values, which upload_inputs turns into the reference's
+                # ValueError (anvil/driver.py:265-266) before the forward is launched
                 out[sym] = _FloatInput(np.ascontiguousarray(v, dtype=np.float32 if v.dtype == np.float32
                                                             else np.float64))
             if not batch:
@@ -885,6 +885,12 @@ class CompiledModel:
                 stage = self._stage(plan, op.sym_str + ".float", f.nbytes)
                 stage.upload(f)
                 self.dev.quantize(stage, f.dtype == np.float64, self.scale(op.sym_str), f.size, v.ptr, v.dtype)
+                try:
+                    self.dev.sync()
+                except ValueError as e:
+                    if "NaN or infinite" in str(e):
+                        raise ValueError(f"input {op.sym_str!r} has NaN or infinite values") from None
+                    raise
             else:
                 v.buf.mem.upload(np.ascontiguousarray(x).astype(rt.NP_DTYPE[v.dtype]))
 

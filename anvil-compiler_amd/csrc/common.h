@@ -19,6 +19,7 @@ enum : unsigned {
   FLAG_SHIFT = 2u,      // rmsnorm shift s + k above 31            -> ValueError (round_term)
   FLAG_ZERODIV = 4u,    // softmax row sum 0                       -> ZeroDivisionError
   FLAG_RANGE = 8u,      // an operand outside its dtype            -> ValueError
+  FLAG_NONFINITE = 16u, // a float input NaN or infinite           -> ValueError
 };
 
 constexpr int EVENT_SLOTS = 512;

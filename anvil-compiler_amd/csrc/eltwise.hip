@@ -98,14 +98,20 @@ __global__ __launch_bounds__(E_THREADS) void copy_dense16_kernel(const uint4* __
 }
 
 // --------------------------------------------------------------------------------------------- quantize
+// A NaN or infinite x raises FLAG_NONFINITE (the reference refuses such an input before quantizing) and stores 0.
 template <typename TI, typename TO>
 __global__ __launch_bounds__(E_THREADS) void quantize_kernel(const TI* __restrict__ x, double scale, long long n,
-                                                              TO* __restrict__ out, int lo, int hi) {
+                                                              TO* __restrict__ out, int lo, int hi, unsigned* flags) {
+  bool bad = false;
   for (long long i = (long long)blockIdx.x * E_THREADS + threadIdx.x; i < n; i += (long long)gridDim.x * E_THREADS) {
-    double v = rint((double)x[i] / scale);
+    const double xv = (double)x[i];
+    const bool fin = isfinite(xv);
+    bad |= !fin;
+    double v = rint(xv / scale);
     v = v < lo ? lo : (v > hi ? hi : v);
-    out[i] = (TO)v;
+    out[i] = fin ? (TO)v : (TO)0;
   }
+  if (bad) raise_flag(flags, FLAG_NONFINITE);
 }
 
 // the float prelude of a token model: out[r][c] = clamp_out(rint((wte[ids[r]][c] + wpe[r % T][c]) / scale)), the
@@ -252,16 +258,16 @@ int anvil_quantize(anvil_ctx* ctx, const void* x, int x_is_f64, double scale, in
   dim3 gr(grid_for(n)), bl(E_THREADS);
   if (x_is_f64 && out_dtype == ANVIL_I8)
     ANVIL_LAUNCH((quantize_kernel<double, int8_t>), gr, bl, 0, ctx->stream, (const double*)x, scale, (long long)n,
-                       (int8_t*)out, lo, hi);
+                       (int8_t*)out, lo, hi, ctx->flags);
   else if (x_is_f64)
     ANVIL_LAUNCH((quantize_kernel<double, int16_t>), gr, bl, 0, ctx->stream, (const double*)x, scale,
-                       (long long)n, (int16_t*)out, lo, hi);
+                       (long long)n, (int16_t*)out, lo, hi, ctx->flags);
   else if (out_dtype == ANVIL_I8)
     ANVIL_LAUNCH((quantize_kernel<float, int8_t>), gr, bl, 0, ctx->stream, (const float*)x, scale, (long long)n,
-                       (int8_t*)out, lo, hi);
+                       (int8_t*)out, lo, hi, ctx->flags);
   else
     ANVIL_LAUNCH((quantize_kernel<float, int16_t>), gr, bl, 0, ctx->stream, (const float*)x, scale,
-                       (long long)n, (int16_t*)out, lo, hi);
+                       (long long)n, (int16_t*)out, lo, hi, ctx->flags);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }

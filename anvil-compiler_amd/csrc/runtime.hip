@@ -118,6 +118,7 @@ int anvil_sync(anvil_ctx* ctx) {
   if (flags & FLAG_OVERFLOW) return set_error(ANVIL_E_OVERFLOW, "an int32 intermediate overflowed on the device");
   if (flags & FLAG_ZERODIV) return set_error(ANVIL_E_ZERODIV, "a softmax row summed to zero");
   if (flags & FLAG_SHIFT) return set_error(ANVIL_E_VALUE, "an rmsnorm shift s + k left [0, 31]");
+  if (flags & FLAG_NONFINITE) return set_error(ANVIL_E_VALUE, "a float input holds NaN or infinite values");
   return set_error(ANVIL_E_VALUE, "an operand left its dtype range on the device (flags %u)", flags);
 }
 

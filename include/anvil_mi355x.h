@@ -236,7 +236,8 @@ int anvil_copy_strided(anvil_ctx* ctx, const void* src, void* dst, int elem_size
                        const int64_t* src_strides);
 
 /* CompiledModel.quantize_input (reference anvil/driver.py:233-241): out = clamp_out(rint(x / scale)), round half
- * to even, x float32 or float64 (x_is_f64), out ANVIL_I8 or ANVIL_I16. */
+ * to even, x float32 or float64 (x_is_f64), out ANVIL_I8 or ANVIL_I16. A NaN or infinite x (which the reference
+ * refuses, driver.py:265-266) stores 0 and makes the next anvil_sync return ANVIL_E_VALUE. */
 int anvil_quantize(anvil_ctx* ctx, const void* x, int x_is_f64, double scale, int64_t n, void* out, int out_dtype);
 
 /* The float prelude of a token model, on the device: rows = batch * T token ids (int64), float32 tables wte

@@ -279,7 +279,10 @@ class FakeDevice:
         self.calls.append(("quantize", n, bool(x_is_f64)))
         v = self._raw(x, np.float64 if x_is_f64 else np.float32, n).astype(np.float64)
         lo, hi = {"i8": (-128, 127), "i16": (-32768, 32767)}[out_dtype]
-        self.store(out, out_dtype, (n,), (1,), np.clip(np.rint(v / scale), lo, hi))
+        fin = np.isfinite(v)
+        if not fin.all():                                # the kernel's flag: the next sync raises
+            self.flags = self.flags or ValueError("a float input holds NaN or infinite values")
+        self.store(out, out_dtype, (n,), (1,), np.where(fin, np.clip(np.rint(np.where(fin, v, 0) / scale), lo, hi), 0))
 
     def embed_quantize(self, ids, rows, T, Cdim, wte, vocab, wpe, scale, out, out_dtype):
         self.calls.append(("embed", rows, T, Cdim))

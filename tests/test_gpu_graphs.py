@@ -180,3 +180,18 @@ def test_head_blocked_attention_blocks(n_embd, n_head, seq):
     assert np.array_equal(res.ints[cm.outputs[0]], want.values[cm.outputs[0]])
 
 
+
+
+def test_nonfinite_input_is_refused_before_the_forward():
+    """A float input with a NaN raises the reference's ValueError (anvil/driver.py:265-266), found by the device
+    quantization; the next run on a finite input is unaffected and equals the oracle."""
+    built, _ = models.config(1)
+    cm = anvil_mi355x.compile(built)
+    x = models.eval_inputs(built.spec, 2, 1)
+    bad = x.copy()
+    bad[1, 5, 9] = np.nan
+    with pytest.raises(ValueError, match="input 'x' has NaN or infinite values"):
+        cm.run(bad, "mi355x", batch=True)
+    res = cm.run(x, "mi355x", batch=True)
+    want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
+    assert np.array_equal(res.ints["out"], want.values["out"])

@@ -315,6 +315,25 @@ def test_quantize_input(dev, f64):
     assert np.array_equal(out.download((x.size,), np.int8).astype(np.int64), want)
 
 
+@pytest.mark.parametrize("f64", [False, True])
+def test_quantize_flags_nonfinite_input(dev, f64):
+    """A NaN or infinite element (refused by the reference, anvil/driver.py:265-266) makes the next sync raise
+    ValueError and is stored as 0; every finite element is quantized as usual, and the flag is cleared."""
+    rng = np.random.default_rng(15)
+    x = (rng.standard_normal(3000) * 3).astype(np.float64 if f64 else np.float32)
+    bad = [7, 1500, 2999]
+    x[bad] = [np.nan, np.inf, -np.inf]
+    xd, out = dev.upload(np.ascontiguousarray(x)), dev.alloc(x.size)
+    dev.quantize(xd, f64, 0.025, x.size, out, "i8")
+    with pytest.raises(ValueError, match="NaN or infinite"):
+        dev.sync()
+    dev.sync()                                            # cleared
+    got = out.download((x.size,), np.int8).astype(np.int64)
+    fin = np.isfinite(x)
+    want = np.clip(np.rint(np.asarray(x[fin], dtype=np.float64) / 0.025), -128, 127)
+    assert np.array_equal(got[fin], want) and not got[bad].any()
+
+
 def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127):
     """Random q, k, v (B, T, H D) i8 with scores and output requants that spread over int8, the reference chain
     qmatmul -> softmax_lut -> qmatmul evaluated by the oracle, and the head-split views the fused kernel reads.
