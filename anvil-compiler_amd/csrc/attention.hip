@@ -149,10 +149,14 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
   // loads whatever the wave's tile count
   const __amdgpu_buffer_rsrc_t krs = uniform_rsrc(a.K + b0 * a.sk0 + b1 * a.sk1, (int)((long long)a.T * a.ldk));
   const unsigned koff = (unsigned)(bperm(l32) * a.ldk) + 16 * half;
+  // Past the wave's last tile the tile part of the offset is 2^31: every lane's offset (below T ldk < 2^31 for a
+  // real tile) then lands in [2^31, 2^32), beyond the descriptor, so the tile test stays on the scalar unit.
   auto kload = [&](int nt, v4i* kf) {
+    const unsigned tile = nt < ntiles ? (unsigned)(nt * 32 * a.ldk) : 0x80000000u;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const unsigned o = nt < ntiles && 32 * ks + 16 * half < D ? koff + 32 * ks + (unsigned)(nt * 32 * a.ldk) : OOB;
+      const unsigned o = D >= 32 ? koff + 32 * ks + tile                    // every lane's chunk inside the head dim
+                                 : (nt < ntiles && 32 * ks + 16 * half < D ? koff + 32 * ks + tile : OOB);
       kf[ks] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(krs, o, 0, 0));
     }
   };
@@ -201,10 +205,12 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
 
   // the first V^T tile loads while the row maxima are reduced and the sums run
   const __amdgpu_buffer_rsrc_t vrs = uniform_rsrc(Vb, (int)((long long)D * a.ldv));
-  auto vload = [&](int nt, v4i* vf) {
+  auto vload = [&](int nt, v4i* vf) {                    // as for K: offsets below D ldv < 2^31, tile part 2^31 past
+    const unsigned tile = nt < ntiles ? (unsigned)(nt * 32) : 0x80000000u;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      const unsigned o = nt < ntiles && 32 * ct + l32 < D ? (unsigned)((32 * ct + l32) * a.ldv + 16 * half + nt * 32) : OOB;
+      const unsigned row = (unsigned)((32 * ct + l32) * a.ldv + 16 * half);
+      const unsigned o = D >= 32 ? row + tile : (nt < ntiles && 32 * ct + l32 < D ? row + tile : OOB);
       vf[ct] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(vrs, o, 0, 0));
     }
   };
