@@ -932,7 +932,8 @@ class CompiledModel:
         """sym -> int64 array of each of syms, read back from the device. A device buffer of up to PINNED_MAX bytes
         is downloaded into a page-locked buffer of the plan (DMA straight into it, no pageable staging) and widened
         from there. With a dict `narrow`, also sym -> the same values as a view at their stored dtype (no copy, into
-        that buffer: use it before the plan's next read)."""
+        that buffer: use it before the plan's next read). Reads of one plan from several threads need the device
+        lock around them, as run() holds it."""
         by_sym = {op.sym_str: op.result for op in self.ops if op.sym_str is not None}
         cache, out = {}, {}
         for s in syms:
