@@ -1,4 +1,5 @@
-"""The reference-side binding of INTEGRATION.md, executed as written against a stand-in `anvil` package.
+"""The reference-side binding in the integration guide at the repository root, executed as written against a
+stand-in `anvil` package.
 
 The stand-in's CompiledModel lowers and memory-plans for tiny-gpu the way the reference's does
 (anvil/driver.py:178-210), except that both steps raise here: a graph that reaches them fails the test. The
@@ -21,12 +22,13 @@ from anvil_mi355x.ir_text import print_ir
 from oracle import interp
 
 ROOT = Path(__file__).resolve().parents[1]
+GUIDE = ROOT / "INTEGRATION.md"
 
 
 def snippet(tag):
-    text = (ROOT / "INTEGRATION.md").read_text()
+    text = GUIDE.read_text()
     m = re.search(rf"<!-- binding:{tag} -->\s*```python\n(.*?)```", text, re.S)
-    assert m, f"INTEGRATION.md has no binding:{tag} block"
+    assert m, f"{GUIDE.name} has no binding:{tag} block"
     return m.group(1)
 
 
@@ -90,4 +92,4 @@ def test_compile_snippet_runs_config5_without_tiny_gpu(monkeypatch):
 
 def test_run_snippet_is_valid_python():
     body = "\n".join(("    " + ln if ln.startswith("#") else ln) for ln in snippet("run").splitlines())
-    compile("class CompiledModel:\n" + body.replace("        ...", "        pass"), "INTEGRATION.md", "exec")
+    compile("class CompiledModel:\n" + body.replace("        ...", "        pass"), GUIDE.name, "exec")
