@@ -372,7 +372,8 @@ def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127
 
 
 @pytest.mark.parametrize("B,H,T,D", [(1, 2, 32, 16), (2, 3, 64, 32), (1, 2, 96, 64), (2, 2, 128, 32),
-                                     (1, 3, 256, 64), (1, 2, 160, 128), (1, 2, 1024, 64), (2, 1, 512, 16)])
+                                     (1, 3, 256, 64), (1, 2, 160, 128), (1, 2, 1024, 64), (2, 1, 512, 16),
+                                     (1, 1, 1024, 128), (1, 2, 1024, 32), (1, 2, 992, 64)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
     """anvil_attention_i8 over q, k (B, T, H D), v^T (B, H D, T) and o (B, T, H D), as the planner lays them out,
