@@ -107,6 +107,7 @@ class _Plan:
         self.fused_adds: set = set()   # add_requant ops computed in a GEMM epilogue
         self.stage: dict = {}          # device staging buffers of float inputs and token ids
         self.host_stage: dict = {}     # page-locked host buffers the read-back downloads into, by device buffer
+        self.graph = None              # the steps captured as one HIP graph (run(..., graph=True))
         self.kb_values: set = set()    # values stored K-blocked (read only by GEMMs)
 
     def buf(self, nbytes, name=""):
@@ -915,12 +916,19 @@ class CompiledModel:
             plan.stage[key] = b
         return b
 
-    def launch(self, plan, profile=False):
-        """Enqueue every kernel of the plan on the device stream (asynchronous unless profile)."""
+    def launch(self, plan, profile=False, graph=False):
+        """Enqueue every kernel of the plan on the device stream (asynchronous unless profile). graph=True replays
+        the steps as one HIP graph, captured on the plan's first such launch right after an ordinary launch of the
+        same steps (which allocates every workspace they need, so the capture records kernels only)."""
         times = {}
+        if not profile and graph:
+            if plan.graph is None:
+                _launch_steps(plan)
+                plan.graph = self.dev.capture(_launch_steps, plan)
+            plan.graph.launch()
+            return times
         if not profile:
-            for _, fn, args in plan.steps:
-                fn(*args)
+            _launch_steps(plan)
             return times
         # each step's kernels carry their own pair of events (anvil_time_kernels): device time of the kernels alone
         for label, fn, args in plan.steps:
@@ -955,10 +963,11 @@ class CompiledModel:
         return out
 
     def run(self, x, backend: str = "mi355x", *, quantized=False, keep="outputs", batch=False, profile=False,
-            tokens=False, **run_kw) -> RunOutput:
+            tokens=False, graph=False, **run_kw) -> RunOutput:
         """Quantize x (unless quantized=True), run the graph on the GPU, read back (reference driver.py:305-322).
         Float inputs are quantized on the device. tokens=True: x holds token ids of a model compiled with embedding
-        tables, gathered and quantized on the device."""
+        tables, gathered and quantized on the device. graph=True runs the forward as one HIP graph of the plan
+        (captured on first use): the same kernels with no launch gaps between them, for repeated small runs."""
         if backend not in BACKENDS:
             raise ValueError(f"unknown backend {backend!r}: {', '.join(BACKENDS)}")
         if run_kw:
@@ -975,7 +984,7 @@ class CompiledModel:
             else:
                 self.upload_inputs(plan, ints_in)
             self.dev.record(2)
-            times = self.launch(plan, profile)
+            times = self.launch(plan, profile, graph)
             self.dev.record(3)
             self.dev.sync()
             total_ms = self.dev.elapsed_ms(2, 3)
@@ -994,6 +1003,11 @@ class CompiledModel:
 
 
 # ------------------------------------------------------------------------------------------ launch helpers
+
+def _launch_steps(plan):
+    for _, fn, args in plan.steps:
+        fn(*args)
+
 
 class _FloatInput:
     """A float input array (float32 or float64, batch dim included) to be quantized on the device."""

@@ -49,6 +49,10 @@ SIGNATURES = {
     "anvil_upload": [_p, _p, _p, _sz],
     "anvil_download": [_p, _p, _p, _sz],
     "anvil_zero": [_p, _p, _sz],
+    "anvil_graph_begin": [_p],
+    "anvil_graph_end": [_p, C.POINTER(_p)],
+    "anvil_graph_launch": [_p, _p],
+    "anvil_graph_destroy": [_p, _p],
     "anvil_event_record": [_p, _i],
     "anvil_event_elapsed": [_p, _i, _i, C.POINTER(C.c_float)],
     "anvil_time_kernels": [_p, _i, _i],
@@ -189,6 +193,27 @@ class HostBuffer:
             pass
 
 
+class HipGraph:
+    """An executable HIP graph of a Device's stream (anvil_graph_end), replayed by launch(); freed when collected."""
+
+    def __init__(self, dev: "Device", handle: int):
+        self.dev, self.handle = dev, int(handle)
+
+    def launch(self):
+        self.dev.lib.call("anvil_graph_launch", self.dev.ctx, C.c_void_p(self.handle))
+
+    def free(self):
+        if self.handle and self.dev.ctx:
+            self.dev.lib.call("anvil_graph_destroy", self.dev.ctx, C.c_void_p(self.handle))
+        self.handle = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Device:
     """One anvil_ctx: a HIP device and the stream every op of this context runs on."""
 
@@ -205,6 +230,24 @@ class Device:
 
     def host_alloc(self, nbytes: int) -> HostBuffer:
         return HostBuffer(self, nbytes)
+
+    def capture(self, fn, *args) -> HipGraph:
+        """fn(*args) recorded as a HIP graph of this context's stream instead of run (anvil_graph_begin / _end): the
+        op calls it makes must need no first-use allocation and no synchronisation. The capture ends whatever fn
+        raises."""
+        self.lib.call("anvil_graph_begin", self.ctx)
+        handle = C.c_void_p()
+        try:
+            fn(*args)
+        except BaseException:
+            try:
+                self.lib.call("anvil_graph_end", self.ctx, C.byref(handle))
+                HipGraph(self, handle.value or 0).free()
+            except Exception:
+                pass
+            raise
+        self.lib.call("anvil_graph_end", self.ctx, C.byref(handle))
+        return HipGraph(self, handle.value)
 
     def upload(self, arr: np.ndarray) -> DeviceBuffer:
         arr = np.ascontiguousarray(arr)

@@ -179,7 +179,42 @@ int anvil_zero(anvil_ctx* ctx, void* dst, size_t bytes) {
   return zero_fill(ctx->stream, dst, bytes);
 }
 
-// The context's events only time work (anvil_event_elapsed, anvil_time_kernels); nothing reads device memory through
+int anvil_graph_begin(anvil_ctx* ctx) {
+  if (int r = check_ctx(ctx)) return r;
+  ANVIL_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+  return ANVIL_OK;
+}
+
+int anvil_graph_end(anvil_ctx* ctx, void** graph) {
+  if (int r = check_ctx(ctx)) return r;
+  if (!graph) return set_error(ANVIL_E_VALUE, "anvil_graph_end: null output pointer");
+  *graph = nullptr;
+  hipGraph_t g = nullptr;
+  ANVIL_HIP(hipStreamEndCapture(ctx->stream, &g));       // ends the capture whatever happened inside it
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return ::anvil::hip_fail(e, "hipGraphInstantiate");
+  *graph = exec;
+  return ANVIL_OK;
+}
+
+int anvil_graph_launch(anvil_ctx* ctx, void* graph) {
+  if (int r = check_ctx(ctx)) return r;
+  if (!graph) return set_error(ANVIL_E_VALUE, "anvil_graph_launch: null graph");
+  ANVIL_HIP(hipGraphLaunch((hipGraphExec_t)graph, ctx->stream));
+  return ANVIL_OK;
+}
+
+int anvil_graph_destroy(anvil_ctx* ctx, void* graph) {
+  if (int r = check_ctx(ctx)) return r;
+  if (!graph) return ANVIL_OK;
+  ANVIL_HIP(hipStreamSynchronize(ctx->stream));
+  ANVIL_HIP(hipGraphExecDestroy((hipGraphExec_t)graph));
+  return ANVIL_OK;
+}
+
+// The context's events only time work// The context's events only time work (anvil_event_elapsed, anvil_time_kernels); nothing reads device memory through
 // them, so they are created without the system-scope release / acquire fence: recording one then costs no L2
 // writeback and invalidation, which would also slow the next kernel.
 static int ensure_event(anvil_ctx* ctx, int slot) {

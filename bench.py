@@ -13,7 +13,8 @@ kernel trace. --config 1, 3, 4 run the other blocks; --config 2 the standalone i
 
 Printed: one JSON line with the metric, the dominant kernel's roofline, a per-kernel breakdown from an untimed
 profiled pass (kernel-bound events again, so the figures add up to less than ms_per_step), a stream-copy figure for
-the achievable HBM bandwidth, the PCIe-inclusive rate of `cm.run` on the host float input (never `value`), and the
+the achievable HBM bandwidth, the PCIe-inclusive rate of `cm.run` on the host float input (never `value`), the step
+time of the same kernels replayed as one captured HIP graph (`hip_graph`, never `value`), and the
 CPU baseline: this repo's literal numpy restatement of the reference interpreter (oracle/, int64 `@`, single-threaded
 per process) on P sequences of the same batch in P processes on this host's cores (exact, as batched evaluation
 equals per-sample evaluation), scaled to tokens/s. It runs before the GPU is first touched, so the worker processes
@@ -150,6 +151,7 @@ def bench_block(args):
     wall_s, device_ms, dom_us, n = timed_steps(dev, steps, K, dom)
     value = nb * spec.seq * K / wall_s
     per = kernel_times(dev, steps)           # after the timed steps: the clock has settled
+    graph = graph_steps(cm, plan, K)
 
     kind, ops, nbytes = plan.works[dom]
     roof = roofline(kind, ops, nbytes, dom_us, steps[dom][0], n)
@@ -199,6 +201,7 @@ def bench_block(args):
         "roofline": roof,
         "hbm_stream": stream,
         "end_to_end": e2e,
+        "hip_graph": graph,
         "kernels": kernels,
         "kernels_us_sum": round(sum(per), 2),
         "kernels_note": "per launch, device time of each launch's kernels alone (events bound to the kernels' dispatch, "
@@ -346,6 +349,20 @@ def cpu_baseline(built, xq, outs):
                      f"affinity={affinity}",
            "one_core_tokens_s": round(one, 2), "seconds": round(wall, 2)}
     return rec, {i: o for i, _, o in res}
+
+
+def graph_steps(cm, plan, K):
+    """The same forward replayed as one HIP graph of the plan (cm.launch(plan, graph=True), captured on first use):
+    K replays between device synchronisations, host wall clock. Never `value`; it shows what the launch gaps cost."""
+    cm.launch(plan, graph=True)
+    cm.dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        cm.launch(plan, graph=True)
+    cm.dev.sync()
+    dt = time.perf_counter() - t0
+    return {"ms_per_step": round(dt / K * 1e3, 4), "steps": K,
+            "covers": "the timed forward's kernels replayed as one captured HIP graph (run(..., graph=True))"}
 
 
 def end_to_end(cm, x, nb, seq, keep, calls=3):

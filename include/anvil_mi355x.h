@@ -62,6 +62,20 @@ int anvil_download(anvil_ctx* ctx, void* dst, const void* src, size_t bytes);
 /* Zero `bytes` of device memory with a fill kernel (safe inside a captured graph). */
 int anvil_zero(anvil_ctx* ctx, void* dst, size_t bytes);
 
+/* ------------------------------------------------------------------------------------------ HIP graphs */
+/* No counterpart in the reference (its interpreter runs each op as it walks the graph): the device-side form of a
+ * repeated CompiledModel.run forward (anvil/driver.py:305-322). anvil_graph_begin starts capturing the launches issued
+ * on the context's stream (relaxed mode); the op entry points called until anvil_graph_end are recorded, not run.
+ * anvil_graph_end instantiates them into *graph, an executable graph that anvil_graph_launch replays on the stream
+ * (with the arguments they were recorded with), and anvil_graph_destroy frees after waiting for the stream. Between
+ * begin and end, call only op entry points whose workspace is already allocated (run the same calls once first):
+ * anvil_upload, anvil_download, anvil_sync and a first-use allocation end the capture with an error. The library's
+ * kernels clear memory with fill kernels, never hipMemsetAsync, so a captured graph holds kernel nodes only. */
+int anvil_graph_begin(anvil_ctx* ctx);
+int anvil_graph_end(anvil_ctx* ctx, void** graph);
+int anvil_graph_launch(anvil_ctx* ctx, void* graph);
+int anvil_graph_destroy(anvil_ctx* ctx, void* graph);
+
 /* -------------------------------------------------------------------------------------------- timing */
 /* Events on the context's stream, in 512 slots: record two, then read the elapsed milliseconds between them. They
  * time work only: they are created without the system-scope fence (hipEventDisableSystemFence), so waiting on one

@@ -39,6 +39,15 @@ class FakeBuffer:
         return out
 
 
+class FakeGraph:
+    def __init__(self, fn, args):
+        self.fn, self.args, self.launches = fn, args, 0
+
+    def launch(self):
+        self.launches += 1
+        self.fn(*self.args)
+
+
 class FakeHostBuffer:
     """Host memory standing in for a page-locked buffer: downloads write into it and views of it are reused."""
 
@@ -71,6 +80,11 @@ class FakeDevice:
 
     def alloc(self, nbytes):
         return FakeBuffer(self, nbytes)
+
+    def capture(self, fn, *args):
+        """A stand-in graph: nothing runs at capture, every launch() makes the recorded calls again."""
+        self.captures = getattr(self, "captures", 0) + 1
+        return FakeGraph(fn, args)
 
     def host_alloc(self, nbytes):
         self.host_allocs = getattr(self, "host_allocs", 0) + 1

@@ -424,3 +424,20 @@ def test_read_back_reuses_page_locked_buffers(fake):
         assert np.array_equal(r.ints["out"], want.values["out"]) and np.array_equal(r.ints["x"], want.values["x"])
         assert np.array_equal(r.output, want.values["out"] * cm.scale("out"))
     assert not np.array_equal(ra.ints["out"], rb.ints["out"])
+
+
+def test_graph_runs_replay_the_captured_steps(fake):
+    """run(..., graph=True): the plan's steps run once and are captured on the first such run, then every run
+    replays the capture over the freshly uploaded input; each result equals the oracle's, as an ordinary run's does."""
+    spec = models.BlockSpec(n_embd=64, n_head=2, seq=32, calib_batches=2, calib_batch=2)
+    built = models.build(spec, 15, stored=False)
+    cm = anvil_mi355x.compile(built)
+    for j in range(3):
+        x = models.eval_inputs(built.spec, 2, 15, j)
+        res = cm.run(x, "mi355x", batch=True, graph=True)
+        want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
+        assert np.array_equal(res.ints["out"], want.values["out"])
+        eager = cm.run(x, "mi355x", batch=True)
+        assert np.array_equal(eager.ints["out"], res.ints["out"])
+    plan = cm.plan(2)
+    assert fake.captures == 1 and plan.graph.launches == 3

@@ -195,3 +195,23 @@ def test_nonfinite_input_is_refused_before_the_forward():
     res = cm.run(x, "mi355x", batch=True)
     want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
     assert np.array_equal(res.ints["out"], want.values["out"])
+
+
+@pytest.mark.parametrize("n", [1, 4, 5])
+def test_hip_graph_replays_equal_ordinary_runs(n):
+    """run(..., graph=True) replays the forward as one captured HIP graph. Three replays, each on a new input and
+    each followed by an ordinary run of the same input (device synchronisations between them), equal those runs in
+    every returned value; config 4 goes through its token prelude."""
+    built, nb = models.config(n)
+    cm = anvil_mi355x.compile(built)
+    nb = min(nb, 4)
+    tokens = bool(built.spec.vocab)
+    for j in range(3):
+        print(f"config {n}, graph replay {j}", flush=True)
+        x = models.eval_inputs(built.spec, nb, n, j)
+        g = cm.run(x, "mi355x", batch=True, graph=True, tokens=tokens)
+        e = cm.run(x, "mi355x", batch=True, tokens=tokens)
+        assert sorted(g.ints) == sorted(e.ints)
+        for k, v in e.ints.items():
+            assert np.array_equal(g.ints[k], v), (j, k)
+    assert cm.plan(nb).graph is not None
