@@ -47,6 +47,10 @@ def test_null_context_is_a_value_error():
         lib.call("anvil_host_alloc", None, 16, None)
     with pytest.raises(ValueError, match="null context"):
         lib.call("anvil_host_free", None, None)
+    for name, args in (("anvil_graph_begin", ()), ("anvil_graph_end", (None,)), ("anvil_graph_launch", (None,)),
+                       ("anvil_graph_destroy", (None,))):
+        with pytest.raises(ValueError, match="null context"):
+            lib.call(name, None, *args)
 
 
 def test_gemm_argument_validation_precedes_the_device():
