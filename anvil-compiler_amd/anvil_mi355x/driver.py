@@ -94,6 +94,7 @@ def _checked_graph(module, consts, prove=True):
 
 
 PINNED_MAX = 1 << 28       # read-back buffers up to this size download into page-locked host memory
+PINNED_PLAN_MAX = 1 << 30  # page-locked read-back memory one plan keeps at most; larger reads go pageable
 
 
 class _Plan:
@@ -939,7 +940,8 @@ class CompiledModel:
     def read(self, plan, syms, nb=None, batch=True, narrow=None) -> dict:
         """sym -> int64 array of each of syms, read back from the device. A device buffer of up to PINNED_MAX bytes
         is downloaded into a page-locked buffer of the plan (DMA straight into it, no pageable staging) and widened
-        from there. With a dict `narrow`, also sym -> the same values as a view at their stored dtype (no copy, into
+        from there, while the plan's page-locked buffers stay within PINNED_PLAN_MAX bytes in total; beyond that a
+        read downloads into ordinary (pageable) memory. With a dict `narrow`, also sym -> the same values as a view at their stored dtype (no copy, into
         that buffer: use it before the plan's next read). Reads of one plan from several threads need the device
         lock around them, as run() holds it."""
         by_sym = {op.sym_str: op.result for op in self.ops if op.sym_str is not None}
@@ -952,7 +954,11 @@ class CompiledModel:
                 if v.buf.nbytes <= PINNED_MAX:
                     into = plan.host_stage.get(key)
                     if into is None or into.nbytes < v.buf.nbytes:
-                        into = plan.host_stage[key] = self.dev.host_alloc(v.buf.nbytes)
+                        held = sum(h.nbytes for k, h in plan.host_stage.items() if k != key)
+                        if held + v.buf.nbytes <= PINNED_PLAN_MAX:
+                            into = plan.host_stage[key] = self.dev.host_alloc(v.buf.nbytes)
+                        else:
+                            into = None
                 cache[key] = v.buf.mem.download((v.buf.nbytes // v.itemsize,), rt.NP_DTYPE[v.dtype], into=into)
             whole = batch or by_sym[s] in self.is_const
             a = v.read(cache[key])

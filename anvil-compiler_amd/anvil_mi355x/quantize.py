@@ -321,8 +321,15 @@ class BoundWalker:
         return DTYPE_MAG[g.qt(op.result).dtype], [("requant numerator", num)]
 
     def _view(self, op):
+        """A const seen through a transpose or reshape. The reference policy keeps the operand's array as it was
+        (anvil/frontend/quantize.py:242-245), so its column sums follow the original axes; the sound policy applies
+        the view, so a later matmul sums |w| over the K axis the product really contracts."""
         if op.x in self.values:
-            self.values[op.result] = self.values[op.x]
+            v = self.values[op.x]
+            if not self.reference:
+                v = (np.transpose(v, op.perm_list) if isinstance(op, g.TransposeOp)
+                     else v.reshape(g.qt(op.result).dims))
+            self.values[op.result] = v
         return self.mag[op.x], []
 
 

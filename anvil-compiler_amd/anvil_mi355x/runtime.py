@@ -59,6 +59,7 @@ SIGNATURES = {
     "anvil_gemm_i8": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i],
     "anvil_gemm_i8_ex": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _i],
     "anvil_gemm_i8_noalloc": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _i],
+    "anvil_workspace_sums": [_p, C.POINTER(C.c_longlong)],
     "anvil_gemm_i8_group": [_p, _p, _i],
     "anvil_gemm_i8_add": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _p, _i32, _i32, _i, _p, _p, _i],
     "anvil_rmsnorm_int": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p],

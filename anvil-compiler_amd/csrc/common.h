@@ -9,6 +9,7 @@
 #include <string>
 #include <type_traits>
 #include <utility>
+#include <vector>
 
 #include "../../include/anvil_mi355x.h"
 
@@ -31,9 +32,12 @@ struct anvil_ctx {
   hipEvent_t events[EVENT_SLOTS] = {};   // created on first use of a slot
   int num_cu = 0;
   int gemm_cfg = 0;               // ANVIL_GEMM_CFG at init: pins one GEMM tile shape (benchmarking); 0 = by problem
-  // split-K workspace of anvil_gemm_i8_ex (int32 partial tiles), allocated on first use and grown as needed
+  // split-K workspace of anvil_gemm_i8_ex (int32 partial tiles), allocated on first use and grown as needed. A HIP
+  // graph captured on the context's stream holds the workspace address of its split-K launches, so a buffer the
+  // workspace outgrows is kept (ws_retired) until anvil_destroy instead of being freed under such a graph.
   int* ws = nullptr;
   long long ws_elems = 0;
+  std::vector<int*> ws_retired;
 };
 
 namespace anvil {
@@ -45,6 +49,8 @@ int check_ctx(anvil_ctx* ctx);
 int zero_fill(hipStream_t s, void* dst, size_t bytes);
 // once per device, with that device current: the device address of the GEMM's static split-K scratch
 int gemm_scratch_setup(int device);
+// at anvil_destroy, after the context's stream has drained: the device's static scratch is free for other contexts
+void gemm_scratch_release(anvil_ctx* ctx);
 
 #define ANVIL_HIP(call)                                        \
   do {                                                         \

@@ -1281,12 +1281,34 @@ static void launch_gemm(GemmArgs& g, bool checked, int osz, bool vec, int batch,
 // Static split-K scratch of anvil_gemm_i8_noalloc: SCRATCH_SUMS int32 partial sums. Each device holds its own copy
 // until the process ends; the library only ever uses it through the per-device address hipGetSymbolAddress returns
 // (the array's name is a host-side stand-in in host code). A split-K run writes every partial sum before it reads it,
-// so nothing needs clearing between calls; anvil_gemm_i8_noalloc calls that overlap on one device race.
+// so nothing needs clearing between calls. Calls on one stream run in order; calls from two streams could overlap on
+// the device and race, so a device's scratch belongs to the first context that splits into it, until that context
+// is destroyed (its stream drained first), and any other context's split is refused.
 constexpr long long SCRATCH_SUMS = 1ll << 22;     // 16 MiB: 64 tiles of 128 x 128 in four K chunks
 constexpr int SCRATCH_DEVICES = 64;
 static __device__ __align__(256) int scratch[SCRATCH_SUMS];
 static int* g_scratch[SCRATCH_DEVICES];
+static anvil_ctx* g_scratch_owner[SCRATCH_DEVICES];
 static std::mutex g_scratch_mu;
+
+// The device's scratch for ctx: claimed on first use, refused while another context holds it.
+static int claim_scratch(anvil_ctx* ctx, int** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[ctx->device]) return set_error(ANVIL_E_RUNTIME, "anvil_gemm_i8_noalloc: scratch not set up");
+  if (g_scratch_owner[ctx->device] && g_scratch_owner[ctx->device] != ctx)
+    return set_error(ANVIL_E_RUNTIME,
+                     "anvil_gemm_i8_noalloc: device %d's static split-K scratch belongs to another context until it "
+                     "is destroyed (split-K calls from two contexts could overlap on the device)", ctx->device);
+  g_scratch_owner[ctx->device] = ctx;
+  *out = g_scratch[ctx->device];
+  return ANVIL_OK;
+}
+
+void gemm_scratch_release(anvil_ctx* ctx) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (ctx->device >= 0 && ctx->device < SCRATCH_DEVICES && g_scratch_owner[ctx->device] == ctx)
+    g_scratch_owner[ctx->device] = nullptr;
+}
 
 int gemm_scratch_setup(int device) {
   if (device < 0 || device >= SCRATCH_DEVICES)
@@ -1439,10 +1461,10 @@ static int gemm_prepare(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void*
 }
 
 // The context's split-K workspace, grown to hold `sums` partial sums (written before they are read: no clearing).
+// The buffer it outgrows is retired, not freed: a graph captured earlier may still replay launches that use it.
 static int ensure_workspace(anvil_ctx* ctx, long long sums) {
   if (ctx->ws_elems >= sums) return ANVIL_OK;
-  ANVIL_HIP(hipStreamSynchronize(ctx->stream));
-  if (ctx->ws) ANVIL_HIP(hipFree(ctx->ws));
+  if (ctx->ws) ctx->ws_retired.push_back(ctx->ws);
   ctx->ws = nullptr;
   ctx->ws_elems = 0;
   ANVIL_HIP(hipMalloc(&ctx->ws, sizeof(int) * sums));
@@ -1466,8 +1488,7 @@ static int gemm_launch(anvil_ctx* ctx, Prepared& p, bool noalloc = false) {
         return set_error(ANVIL_E_VALUE,
                          "anvil_gemm_i8_noalloc: a split-K product of %lld partial sums (%lld tiles of 128 x 128 in "
                          "%d K chunks) exceeds the static scratch (%lld sums)", sums, tiles, splits, SCRATCH_SUMS);
-      if (!g_scratch[ctx->device]) return set_error(ANVIL_E_RUNTIME, "anvil_gemm_i8_noalloc: scratch not set up");
-      p.g.ws = g_scratch[ctx->device];
+      if (int r = claim_scratch(ctx, &p.g.ws)) return r;
     } else {
       if (int r = ensure_workspace(ctx, sums)) return r;
       p.g.ws = ctx->ws;
@@ -1542,6 +1563,13 @@ extern "C" int anvil_gemm_i8_noalloc(anvil_ctx* ctx, const int8_t* A, const int8
                                      int batch1, int M, int N, int K, const int64_t* strides, int32_t mult, int shift,
                                      const int8_t* lut, int out_dtype, int flags) {
   return gemm_entry(ctx, A, Bt, C, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags, nullptr, true);
+}
+
+extern "C" int anvil_workspace_sums(anvil_ctx* ctx, long long* sums) {
+  if (int r = check_ctx(ctx)) return r;
+  if (!sums) return set_error(ANVIL_E_VALUE, "anvil_workspace_sums: null pointer");
+  *sums = ctx->ws_elems;
+  return ANVIL_OK;
 }
 
 extern "C" int anvil_gemm_i8_add(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, int8_t* C, int batch0,

@@ -99,10 +99,12 @@ int anvil_destroy(anvil_ctx* ctx) {
   if (g_timer.stream == ctx->stream) g_timer = KernelTimer{};
   hipSetDevice(ctx->device);
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
+  gemm_scratch_release(ctx);
   for (auto& ev : ctx->events)
     if (ev) hipEventDestroy(ev);
   if (ctx->flags) hipFree(ctx->flags);
   if (ctx->ws) hipFree(ctx->ws);
+  for (int* w : ctx->ws_retired) hipFree(w);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
   return ANVIL_OK;
@@ -214,7 +216,7 @@ int anvil_graph_destroy(anvil_ctx* ctx, void* graph) {
   return ANVIL_OK;
 }
 
-// The context's events only time work// The context's events only time work (anvil_event_elapsed, anvil_time_kernels); nothing reads device memory through
+// The context's events only time work (anvil_event_elapsed, anvil_time_kernels); nothing reads device memory through
 // them, so they are created without the system-scope release / acquire fence: recording one then costs no L2
 // writeback and invalidation, which would also slow the next kernel.
 static int ensure_event(anvil_ctx* ctx, int slot) {

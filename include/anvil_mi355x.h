@@ -139,16 +139,21 @@ int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C,
                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
                      int flags);
 
-/* anvil_gemm_i8_ex that allocates nothing (no reference counterpart: it is for callers that cannot allocate device
- * memory at call time, such as code under HIP graph capture or a tight serving loop). Same arguments and results as
- * anvil_gemm_i8_ex (reference anvil/semantics.py:95-103); where anvil_gemm_i8_ex would split K into its context
- * workspace (allocated on first use), this keeps the partial tiles in a static per-device scratch of 2^22 int32
- * (16 MiB, held by each device the library runs on until the process ends) and fails with ANVIL_E_VALUE when the
- * split needs more (128 x 128 output tiles x K chunks x 16384 sums). Calls that overlap on one device race on that
- * scratch: issue them on one stream or context at a time. */
+/* anvil_gemm_i8_ex that allocates nothing. It has no counterpart in the reference: it is for callers that cannot
+ * allocate device memory at call time, such as code under HIP graph capture or a tight serving loop. Same arguments
+ * and results as anvil_gemm_i8_ex; where anvil_gemm_i8_ex would split K into its context workspace (allocated on
+ * first use), this keeps the partial tiles in a static per-device scratch of 2^22 int32 (16 MiB, held by each device
+ * the library runs on until the process ends) and fails with ANVIL_E_VALUE when the split needs more (128 x 128
+ * output tiles x K chunks x 16384 sums). Calls on one context run in its stream's order and never overlap; the
+ * scratch of a device belongs to the first context whose call splits into it, until anvil_destroy of that context,
+ * and a split-K call from any other context fails with ANVIL_E_RUNTIME instead of racing on it. */
 int anvil_gemm_i8_noalloc(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
                           int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut,
                           int out_dtype, int flags);
+
+/* The number of int32 partial sums the context's split-K workspace holds: 0 until an anvil_gemm_i8_ex product splits
+ * K, then the largest split so far (the workspace grows and is never shrunk before anvil_destroy). */
+int anvil_workspace_sums(anvil_ctx* ctx, long long* sums);
 
 /* The arguments of one anvil_gemm_i8_ex call. */
 typedef struct anvil_gemm_desc {

@@ -426,6 +426,24 @@ def test_read_back_reuses_page_locked_buffers(fake):
     assert not np.array_equal(ra.ints["out"], rb.ints["out"])
 
 
+def test_page_locked_read_back_is_capped_per_plan(fake, monkeypatch):
+    """With the plan's page-locked budget below the two read-back buffers (x and out), only the first gets a
+    page-locked buffer; the second downloads into ordinary memory, and both still equal the oracle."""
+    from anvil_mi355x import driver
+    spec = models.BlockSpec(n_embd=64, n_head=1, seq=32, calib_batches=2, calib_batch=2)
+    built = models.build(spec, 14, stored=False)
+    cm = anvil_mi355x.compile(built)
+    monkeypatch.setattr(driver, "PINNED_PLAN_MAX", 2 * 32 * 64 + 100)
+    before = getattr(fake, "host_allocs", 0)
+    x = models.eval_inputs(built.spec, 2, 14, 0)
+    for _ in range(2):
+        r = cm.run(x, "mi355x", batch=True)
+        want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
+        assert np.array_equal(r.ints["out"], want.values["out"]) and np.array_equal(r.ints["x"], want.values["x"])
+    assert fake.host_allocs - before == 1
+    assert sum(h.nbytes for h in cm.plan(2).host_stage.values()) <= driver.PINNED_PLAN_MAX
+
+
 def test_graph_runs_replay_the_captured_steps(fake):
     """run(..., graph=True): the plan's steps run once and are captured on the first such run, then every run
     replays the capture over the freshly uploaded input; each result equals the oracle's, as an ordinary run's does."""

@@ -215,3 +215,46 @@ def test_hip_graph_replays_equal_ordinary_runs(n):
         for k, v in e.ints.items():
             assert np.array_equal(g.ints[k], v), (j, k)
     assert cm.plan(nb).graph is not None
+
+
+def _workspace_sums(dev) -> int:
+    import ctypes as C
+    out = C.c_longlong(-1)
+    dev.lib.call("anvil_workspace_sums", dev.ctx, C.byref(out))
+    return int(out.value)
+
+
+def test_hip_graph_of_a_split_k_plan_survives_a_larger_workspace():
+    """A one-sequence plan of a long-K, few-tile qlinear splits K into the context's workspace, and its captured HIP
+    graph records that workspace's address. A 32-sequence run of the same graph then needs a larger workspace (64
+    tiles of 128 x 128 instead of 1), which replaces the buffer. Replays of the first graph afterwards still write
+    correct outputs: the outgrown buffer is kept alive for graphs that hold it (every output against the oracle)."""
+    from anvil_mi355x import quantize as Q
+    from anvil_mi355x.ir import GraphBuilder
+    from oracle import semantics as sem
+
+    rng = np.random.default_rng(2024)
+    T, K, N = 128, 2048, 256
+    w = rng.integers(-128, 128, (K, N))
+    # about six standard deviations of a random int8 accumulator (sqrt(K) * 128^2 / 3) map to 127
+    (m,), s = Q.choose_shift([127 / (6 * K ** 0.5 * 128 ** 2 / 3)], [128 * int(np.abs(w).sum(axis=0).max())])
+    b = GraphBuilder("splitk_graph")
+    x = b.input("x", [T, K])
+    b.output(b.qlinear("y", x, b.const("w", [K, N]), m, s))
+    cm = anvil_mi355x.compile((b.module(), {"w": w}))
+    assert cm.proven
+
+    def check(nb, graph):
+        xs = rng.integers(-128, 128, (nb, T, K))
+        got = cm.run(xs, "mi355x", quantized=True, batch=True, graph=graph).ints["y"]
+        want = sem.qmatmul(xs, w, m, s, fast=True)
+        assert np.array_equal(got, want), (nb, graph, int((got != want).sum()))
+
+    check(1, True)                         # eager run, capture, first replay
+    small = _workspace_sums(cm.dev)
+    assert small > 0, "the one-sequence product did not split K"
+    check(32, False)
+    assert _workspace_sums(cm.dev) > small, "the 32-sequence product did not grow the workspace"
+    for _ in range(3):
+        check(1, True)                     # replays of the graph captured before the growth
+    assert cm.plan(1).graph is not None

@@ -84,6 +84,43 @@ def test_batched_const_operand_bounds():
     assert Q.int32_bounds(mod).acc[y] == 128 * 200
 
 
+def test_transposed_const_operand_is_bounded_over_its_contracted_axis():
+    """qmatmul(x, transpose(W)) with W (256, 3072): the product contracts W's second axis (K = 3072), so the sound
+    bound is 128 * 3072 * 127. Summing the untransposed array's first axis would give 128 * 256 * 127, below 2^23,
+    and wrongly admit the 24-bit requant."""
+    b = GraphBuilder("tw")
+    x = b.input("x", [4, 3072])
+    w = b.const("w", [256, 3072], value=np.full((256, 3072), 127))
+    wt = b.transpose("wt", w, [1, 0])
+    b.output(b.qmatmul("y", x, wt, 1, 24))
+    mod = b.module()
+    y = mod.ops[0].ops[-2].result
+    bounds = Q.int32_bounds(mod)
+    assert bounds.acc[y] == 128 * 3072 * 127
+    # a column of W^T is a row of W: one loud row of W bounds one column of the product
+    v = np.zeros((256, 3072), dtype=np.int64)
+    v[7] = 127
+    b = GraphBuilder("tw1")
+    x = b.input("x", [4, 3072])
+    wt = b.transpose("wt", b.const("w", [256, 3072], value=v), [1, 0])
+    b.output(b.qmatmul("y", x, wt, 1, 24))
+    mod = b.module()
+    assert Q.int32_bounds(mod).acc[mod.ops[0].ops[-2].result] == 128 * 3072 * 127
+
+
+def test_reshaped_const_operand_is_bounded_in_its_new_shape():
+    """A const of 12 entries reshaped to (3, 4) and used as the right operand: the sound bound sums each column of
+    the (3, 4) array; the largest column of arange(12) so reshaped is 3 + 7 + 11 = 21."""
+    b = GraphBuilder("rw")
+    x = b.input("x", [5, 3])
+    w = b.reshape("w2", b.const("w", [12], value=np.arange(12)), [3, 4])
+    b.output(b.qmatmul("y", x, w, 1, 0))
+    mod = b.module()
+    y = mod.ops[0].ops[-2].result
+    assert Q.int32_bounds(mod).acc[y] == 128 * 21
+    Q.prove_no_overflow(mod)          # the reference policy still takes the graph as the reference does
+
+
 def test_choose_shift_matches_a_brute_force_scan():
     """choose_shift equals the first admissible shift of a downward scan over [0, 31 - extra]."""
     rng = np.random.default_rng(11)

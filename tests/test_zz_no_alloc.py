@@ -42,6 +42,55 @@ def _both(dev, a, w, m, s, flags):
     return C1.download((M, N), np.int8), C2.download((M, N), np.int8)
 
 
+def _workspace_sums(d) -> int:
+    out = C.c_longlong(-1)
+    d.lib.call("anvil_workspace_sums", d.ctx, C.byref(out))
+    return int(out.value)
+
+
+def test_noalloc_split_allocates_no_workspace_and_keeps_the_scratch_to_one_context():
+    """A fresh context that has never split K runs a split-K product through anvil_gemm_i8_noalloc: its workspace
+    stays empty (nothing allocated), while anvil_gemm_i8_ex on the same product then allocates one. Until that
+    context is destroyed, a second context's split into the device's scratch is refused rather than racing. (First
+    in this file: the shared context of the tests below claims the scratch for the rest of the process.)"""
+    first = rt.Device(0)
+    second = rt.Device(0)
+    try:
+        a, w, m, s = _inputs(256, 3072, 3072, 2)
+        M, K = a.shape
+        N = w.shape[1]
+        A = first.upload(np.ascontiguousarray(a).astype(np.int8))
+        Bt = first.upload(np.ascontiguousarray(w.T).astype(np.int8))
+        C1, C2 = first.alloc(M * N), first.alloc(M * N)
+        strides = [0, 0, K, 0, 0, K, 0, 0, N]
+        flags = rt.GEMM_UNCHECKED | rt.GEMM_SPLITK
+        assert _workspace_sums(first) == 0
+        first.gemm_i8_noalloc(A, Bt, C2, 1, 1, M, N, K, strides, m, s, None, "i8", flags)
+        first.sync()
+        assert _workspace_sums(first) == 0
+        with pytest.raises(RuntimeError, match="belongs to another context"):
+            second.gemm_i8_noalloc(A, Bt, C1, 1, 1, M, N, K, strides, m, s, None, "i8", flags)
+        first.gemm_i8(A, Bt, C1, 1, 1, M, N, K, strides, m, s, None, "i8", flags)
+        first.sync()
+        assert _workspace_sums(first) > 0
+        assert np.array_equal(C1.download((M, N), np.int8), C2.download((M, N), np.int8))
+        for buf in (A, Bt, C1, C2):
+            buf.free()
+        first.close()
+        # the scratch is free again once its holder is destroyed
+        A = second.upload(np.ascontiguousarray(a).astype(np.int8))
+        Bt = second.upload(np.ascontiguousarray(w.T).astype(np.int8))
+        C3 = second.alloc(M * N)
+        second.gemm_i8_noalloc(A, Bt, C3, 1, 1, M, N, K, strides, m, s, None, "i8", flags)
+        second.sync()
+        assert np.array_equal(C3.download((M, N), np.int8).astype(np.int64), sem.qmatmul(a, w, m, s, fast=True))
+        for buf in (A, Bt, C3):
+            buf.free()
+    finally:
+        first.close()
+        second.close()
+
+
 CASES = [  # (first shape, second smaller shape, flags): split-K by the library's choice, forced, and one-pass
     ((256, 3072, 3072), (256, 768, 768), rt.GEMM_UNCHECKED),
     ((640, 2048, 1024), (100, 512, 48), rt.GEMM_UNCHECKED | rt.GEMM_SPLITK),
