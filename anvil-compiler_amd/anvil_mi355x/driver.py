@@ -345,7 +345,8 @@ class CompiledModel:
                 if op.b in self.is_const:
                     b = dense_copy(b.prepend(nb), label + ".b")
                 step(label, _call_ptrs, dev.add_requant, [a, g.qt(op.a).dtype, b, g.qt(op.b).dtype, int(op.Ma),
-                                                          int(op.Mb), int(op.s), out.size, out, t.dtype])
+                                                          int(op.Mb), int(op.s), out.size, out, t.dtype,
+                                                          rt.OP_UNCHECKED if self.proven else 0])
             elif isinstance(op, g.LutOp):
                 x = dense(views[op.x], label + ".x")
                 if op.x in self.is_const:
@@ -359,7 +360,8 @@ class CompiledModel:
                 if op.y in self.is_const:
                     y = dense_copy(y.prepend(nb), label + ".y")
                 step(label, _call_ptrs, dev.lut_mul, [x, y, dense(views[op.table], label + ".t"), int(op.M),
-                                                      int(op.s), out.size, out])
+                                                      int(op.s), out.size, out,
+                                                      rt.OP_UNCHECKED if self.proven else 0])
             else:
                 raise NotImplementedError(op.name)
         if self.group_gemms:
@@ -617,19 +619,21 @@ class CompiledModel:
         return op.value if op.value is not None else self.consts[op.sym_str]
 
     def _residual_fusions(self, keep) -> dict:
-        """{matmul: add_requant} for int8 matmul results y that feed an add_requant of int8 operands with a residual
-        computed earlier in the graph, in a proven graph: the add runs in the GEMM's epilogue (y itself is still
-        written when it is returned or read elsewhere)."""
+        """{matmul: add_requant} for matmul results y that feed an add_requant with a residual computed earlier in the
+        graph, in a proven graph, where y, the residual and the sum share one dtype (all int8, or all int16: the wide
+        residual stream of docs/decisions/ADR-004-small-inputs.md:59-82): the add runs in the GEMM's epilogue (y itself
+        is still written when it is returned or read elsewhere)."""
         if not self.proven:
             return {}
         order = {op: i for i, op in enumerate(self.ops)}
         found, taken = {}, set()
         for op in self.ops:
-            if not isinstance(op, (g.QMatmulOp, g.QLinearOp)) or g.qt(op.result).dtype != "i8" or op.result in self.phys:
+            dt = g.qt(op.result).dtype if isinstance(op, (g.QMatmulOp, g.QLinearOp)) else None
+            if dt not in ("i8", "i16") or op.result in self.phys:
                 continue
             for u in self.users.get(op.result, []):
-                if (not isinstance(u, g.AddRequantOp) or u in taken or g.qt(u.result).dtype != "i8"
-                        or g.qt(u.a).dtype != "i8" or g.qt(u.b).dtype != "i8" or u.a is u.b):
+                if (not isinstance(u, g.AddRequantOp) or u in taken or g.qt(u.result).dtype != dt
+                        or g.qt(u.a).dtype != dt or g.qt(u.b).dtype != dt or u.a is u.b):
                     continue
                 other = u.b if u.a is op.result else u.a
                 own = other.owner
@@ -729,14 +733,15 @@ class CompiledModel:
         if (rv is None or rv.strides[-1] != 1 or K % 16 or not ok16(a2.strides[0]) or not ok16(bt.strides[-2])
                 or not ok16(a2.offset) or not ok16(bt.offset) or 256 * max(a2.strides[0], bt.strides[-2]) >= 1 << 31):
             return False
-        d = P.dense((rows, N), "i8", (add.sym_str or "add"))
+        dt = g.qt(op.result).dtype
+        d = P.dense((rows, N), dt, (add.sym_str or "add"))
         store_y = keep == "all" or op.result in self.output_values or len(self.users.get(op.result, [])) > 1
         ma, mb = (int(add.Mb), int(add.Ma)) if y_first else (int(add.Ma), int(add.Mb))   # (residual, y)
         rstrides = [0, 0, rv.strides[0], 0, 0, d.strides[0]]
         a2, bt = self._kblock_weight(op, a2, bt, strides, K, False)
         strides, flags = self._kb_call(a2, bt, c2 if store_y else None, strides, flags)
         step(label, _call_gemm_add, self.dev, a2, bt, c2 if store_y else None, rows, N, K, strides, op, lut, rv, ma,
-             mb, int(add.s), d, rstrides, flags)
+             mb, int(add.s), d, rstrides, flags, dt)
         views[add.result] = d.reshape(tuple(views[other].dims))
         P.fused_adds.add(add)
         return True
@@ -1056,7 +1061,8 @@ def _work(fn, args):
         return "gemm", 2 * nb * M * N * K, nb * M * K + b_batches * N * K + nb * M * N * isz[dt]
     if fn is _call_gemm_add:
         _, a, bt, c, M, N, K = args[:7]
-        return "gemm", 2 * M * N * K, M * K + N * K + M * N * (3 if c is not None else 2)
+        osz = isz[args[-1]] if len(args) > 17 else 1
+        return "gemm", 2 * M * N * K, M * K + N * K + M * N * osz * (3 if c is not None else 2)
     if fn is _call_attention:
         _, q, k, v, o, b0, b1, T, D = args[:9]
         nb = b0 * b1
@@ -1133,9 +1139,9 @@ def _call_attention(dev, q: View, k: View, v: View, o: View, b0, b1, T, D, strid
 
 
 def _call_gemm_add(dev, a: View, bt: View, c, M, N, K, strides, op, lut, r: View, ma, mb, shift2, d: View, rstrides,
-                   flags):
+                   flags, out_dtype="i8"):
     dev.gemm_i8_add(a.ptr, bt.ptr, None if c is None else c.ptr, 1, 1, M, N, K, strides, int(op.M), int(op.s),
-                    None if lut is None else lut.ptr, r.ptr, ma, mb, shift2, d.ptr, rstrides, flags)
+                    None if lut is None else lut.ptr, r.ptr, ma, mb, shift2, d.ptr, rstrides, flags, out_dtype)
 
 
 def _swap_last2(n):

@@ -62,14 +62,18 @@ SIGNATURES = {
     "anvil_workspace_sums": [_p, C.POINTER(C.c_longlong)],
     "anvil_gemm_i8_group": [_p, _p, _i],
     "anvil_gemm_i8_add": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _p, _i32, _i32, _i, _p, _p, _i],
+    "anvil_gemm_i8_add_ex": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _p, _i32, _i32, _i, _p, _p,
+                             _i],
     "anvil_rmsnorm_int": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p],
     "anvil_rmsnorm_int_ex": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p, _i],
     "anvil_softmax_lut": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i],
     "anvil_softmax_lut_ex": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i, _i],
     "anvil_attention_i8": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p, _i32, _i, _p, _i32, _i, _i32, _i, _i],
     "anvil_add_requant": [_p, _p, _i, _p, _i, _i32, _i32, _i, _i64, _p, _i],
+    "anvil_add_requant_ex": [_p, _p, _i, _p, _i, _i32, _i32, _i, _i64, _p, _i, _i],
     "anvil_lut_i8": [_p, _p, _p, _i64, _p],
     "anvil_lut_mul": [_p, _p, _p, _p, _i32, _i, _i64, _p],
+    "anvil_lut_mul_ex": [_p, _p, _p, _p, _i32, _i, _i64, _p, _i],
     "anvil_copy_strided": [_p, _p, _p, _i, _i, _p, _p],
     "anvil_quantize": [_p, _p, _i, _f64, _i64, _p, _i],
     "anvil_embed_quantize": [_p, _p, _i64, _i, _i, _p, _i, _p, _f64, _p, _i],
@@ -317,13 +321,15 @@ class Device:
         self.lib.call("anvil_gemm_i8_group", self.ctx, descs, len(calls))
 
     def gemm_i8_add(self, A, Bt, Cp, batch0, batch1, M, N, K, strides, mult, shift, lut, R, ma, mb, shift2, D,
-                    rstrides, flags):
+                    rstrides, flags, out_dtype="i8"):
+        """anvil_gemm_i8_add_ex: y = the product's requant, D = add_requant(R, y) in its epilogue; y, R and D are
+        out_dtype."""
         st = (C.c_int64 * 9)(*[int(s) for s in strides])
         rs = (C.c_int64 * 6)(*[int(s) for s in rstrides])
-        self.lib.call("anvil_gemm_i8_add", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)),
+        self.lib.call("anvil_gemm_i8_add_ex", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)),
                       C.c_void_p(_ptr(Cp) if Cp is not None else 0), batch0, batch1, M, N, K, st, int(mult), shift,
-                      C.c_void_p(_ptr(lut) if lut is not None else 0), C.c_void_p(_ptr(R)), int(ma), int(mb), shift2,
-                      C.c_void_p(_ptr(D)), rs, int(flags))
+                      C.c_void_p(_ptr(lut) if lut is not None else 0), DTYPE_CODE[out_dtype], C.c_void_p(_ptr(R)),
+                      int(ma), int(mb), shift2, C.c_void_p(_ptr(D)), rs, int(flags))
 
     def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out, flags=0):
         self.lib.call("anvil_rmsnorm_int_ex", self.ctx, C.c_void_p(_ptr(x)), DTYPE_CODE[x_dtype], C.c_void_p(_ptr(w)),
@@ -340,17 +346,18 @@ class Device:
                       C.c_void_p(_ptr(O)), b0, b1, T, D, st, int(ms), ss, C.c_void_p(_ptr(lut)), int(one),
                       int(bool(causal)), int(mo), so, int(flags))
 
-    def add_requant(self, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype):
-        self.lib.call("anvil_add_requant", self.ctx, C.c_void_p(_ptr(a)), DTYPE_CODE[a_dtype], C.c_void_p(_ptr(b)),
-                      DTYPE_CODE[b_dtype], int(ma), int(mb), shift, n, C.c_void_p(_ptr(out)), DTYPE_CODE[out_dtype])
+    def add_requant(self, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype, flags=0):
+        self.lib.call("anvil_add_requant_ex", self.ctx, C.c_void_p(_ptr(a)), DTYPE_CODE[a_dtype], C.c_void_p(_ptr(b)),
+                      DTYPE_CODE[b_dtype], int(ma), int(mb), shift, n, C.c_void_p(_ptr(out)), DTYPE_CODE[out_dtype],
+                      int(flags))
 
     def lut_i8(self, x, table, n, out):
         self.lib.call("anvil_lut_i8", self.ctx, C.c_void_p(_ptr(x)), C.c_void_p(_ptr(table)), n,
                       C.c_void_p(_ptr(out)))
 
-    def lut_mul(self, x, y, table, mult, shift, n, out):
-        self.lib.call("anvil_lut_mul", self.ctx, C.c_void_p(_ptr(x)), C.c_void_p(_ptr(y)), C.c_void_p(_ptr(table)),
-                      int(mult), shift, n, C.c_void_p(_ptr(out)))
+    def lut_mul(self, x, y, table, mult, shift, n, out, flags=0):
+        self.lib.call("anvil_lut_mul_ex", self.ctx, C.c_void_p(_ptr(x)), C.c_void_p(_ptr(y)), C.c_void_p(_ptr(table)),
+                      int(mult), shift, n, C.c_void_p(_ptr(out)), int(flags))
 
     def copy_strided(self, src, dst, elem_size, dims, src_strides):
         r = len(dims)

@@ -33,6 +33,70 @@ __global__ __launch_bounds__(E_THREADS) void add_requant_kernel(const TA* __rest
   if (bad) raise_flag(flags, FLAG_OVERFLOW);
 }
 
+// ------------------------------------------------------------------------------------- 16-element chunks
+// The vector kernels below take 16 elements a lane per step (chunk c = elements 16 c .. 16 c + 15): one 16-byte
+// access per int8 operand, two per int16 operand, so every load and store is a full dwordx4 and a wave moves whole
+// 1 KiB (or 2 KiB) spans. They need 16-byte aligned arrays; the n % 16 trailing elements go to the one-element
+// kernels, whose arithmetic is the same.
+template <typename T>
+__device__ __forceinline__ void load16(const T* __restrict__ p, long long c, int v[16]) {
+  if constexpr (sizeof(T) == 1) {
+    const uint4 w = reinterpret_cast<const uint4*>(p)[c];
+    const unsigned d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = (int)(int8_t)(d[e >> 2] >> (8 * (e & 3)));
+  } else {
+    const uint4 w0 = reinterpret_cast<const uint4*>(p)[2 * c], w1 = reinterpret_cast<const uint4*>(p)[2 * c + 1];
+    const unsigned d[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = (int)(int16_t)(d[e >> 1] >> (16 * (e & 1)));
+  }
+}
+
+// 16 results already inside T's range
+template <typename T>
+__device__ __forceinline__ void store16(T* __restrict__ p, long long c, const int v[16]) {
+  if constexpr (sizeof(T) == 1) {
+    reinterpret_cast<uint4*>(p)[c] = uint4{pack4(v[0], v[1], v[2], v[3]), pack4(v[4], v[5], v[6], v[7]),
+                                           pack4(v[8], v[9], v[10], v[11]), pack4(v[12], v[13], v[14], v[15])};
+  } else {
+    unsigned d[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) d[q] = __builtin_amdgcn_perm((unsigned)v[2 * q + 1], (unsigned)v[2 * q], 0x05040100u);
+    reinterpret_cast<uint4*>(p)[2 * c] = uint4{d[0], d[1], d[2], d[3]};
+    reinterpret_cast<uint4*>(p)[2 * c + 1] = uint4{d[4], d[5], d[6], d[7]};
+  }
+}
+
+// add_requant over 16-element chunks. CHECKED repeats add_requant_kernel's int32 checks; otherwise the graph's
+// static proof keeps a Ma + b Mb + rnd inside int32 and it is computed in 32 bits, with 24-bit multiplies (MUL24)
+// when |Ma|, |Mb| < 2^23 (|a|, |b| <= 2^15 as i8 / i16).
+template <typename TA, typename TB, typename TO, bool CHECKED, bool MUL24>
+__global__ __launch_bounds__(E_THREADS) void add_requant_vec(const TA* __restrict__ a, const TB* __restrict__ b,
+                                                              int ma, int mb, int shift, int rnd, long long n16,
+                                                              TO* __restrict__ out, unsigned* flags) {
+  constexpr int lo = sizeof(TO) == 1 ? -128 : -32768, hi = sizeof(TO) == 1 ? 127 : 32767;
+  unsigned bad = 0;
+  for (long long c = (long long)blockIdx.x * E_THREADS + threadIdx.x; c < n16; c += (long long)gridDim.x * E_THREADS) {
+    int va[16], vb[16], o[16];
+    load16(a, c, va);
+    load16(b, c, vb);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      if constexpr (CHECKED) {
+        const long long pa = (long long)va[e] * ma, pb = (long long)vb[e] * mb, acc = pa + pb;
+        bad |= (pa < I32_MIN) | (pa > I32_MAX) | (pb < I32_MIN) | (pb > I32_MAX) | (acc < I32_MIN) | (acc > I32_MAX);
+        o[e] = requant_checked((int)acc, 1, shift, rnd, lo, hi, bad);
+      } else {
+        const int x = MUL24 ? __mul24(va[e], ma) + __mul24(vb[e], mb) + rnd : va[e] * ma + vb[e] * mb + rnd;
+        o[e] = min(max(x >> shift, lo), hi);
+      }
+    }
+    store16(out, c, o);
+  }
+  if (CHECKED && bad) raise_flag(flags, FLAG_OVERFLOW);
+}
+
 // ------------------------------------------------------------------------------------------------ lut ops
 __global__ __launch_bounds__(E_THREADS) void lut_kernel(const int8_t* __restrict__ x, const int8_t* __restrict__ table,
                                                          long long n, int8_t* __restrict__ out) {
@@ -54,6 +118,54 @@ __global__ __launch_bounds__(E_THREADS) void lut_mul_kernel(const int8_t* __rest
   for (long long i = (long long)blockIdx.x * E_THREADS + threadIdx.x; i < n; i += (long long)gridDim.x * E_THREADS)
     out[i] = (int8_t)requant_checked((int)t_s[x[i] + 128] * (int)y[i], mult, shift, rnd, -128, 127, bad);
   if (bad) raise_flag(flags, FLAG_OVERFLOW);
+}
+
+// lut and lut_mul over 16-element chunks. The table is staged rotated (the entry of v at index v & 255), so a
+// lookup's index is the operand byte itself. lut_mul: |T[x] y| <= 2^14, so with |M| < 2^23 (MUL24) T[x] y M + rnd is
+// one 24-bit multiply-add after the product; CHECKED keeps lut_mul_kernel's int32 checks.
+__global__ __launch_bounds__(E_THREADS) void lut_vec(const int8_t* __restrict__ x, const int8_t* __restrict__ table,
+                                                      long long n16, int8_t* __restrict__ out) {
+  __shared__ int8_t t_s[256];
+  t_s[threadIdx.x ^ 128] = table[threadIdx.x];
+  __syncthreads();
+  for (long long c = (long long)blockIdx.x * E_THREADS + threadIdx.x; c < n16; c += (long long)gridDim.x * E_THREADS) {
+    const uint4 w = reinterpret_cast<const uint4*>(x)[c];
+    const unsigned d[4] = {w.x, w.y, w.z, w.w};
+    int o[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[e] = t_s[(d[e >> 2] >> (8 * (e & 3))) & 255];
+    reinterpret_cast<uint4*>(out)[c] = uint4{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
+                                             pack4(o[8], o[9], o[10], o[11]), pack4(o[12], o[13], o[14], o[15])};
+  }
+}
+
+template <bool CHECKED, bool MUL24>
+__global__ __launch_bounds__(E_THREADS) void lut_mul_vec(const int8_t* __restrict__ x, const int8_t* __restrict__ y,
+                                                          const int8_t* __restrict__ table, int mult, int shift,
+                                                          int rnd, long long n16, int8_t* __restrict__ out,
+                                                          unsigned* flags) {
+  __shared__ int8_t t_s[256];
+  t_s[threadIdx.x ^ 128] = table[threadIdx.x];
+  __syncthreads();
+  unsigned bad = 0;
+  for (long long c = (long long)blockIdx.x * E_THREADS + threadIdx.x; c < n16; c += (long long)gridDim.x * E_THREADS) {
+    const uint4 w = reinterpret_cast<const uint4*>(x)[c];
+    const unsigned d[4] = {w.x, w.y, w.z, w.w};
+    int vy[16], o[16];
+    load16(y, c, vy);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int p = (int)t_s[(d[e >> 2] >> (8 * (e & 3))) & 255] * vy[e];
+      if constexpr (CHECKED) {
+        o[e] = requant_checked(p, mult, shift, rnd, -128, 127, bad);
+      } else {
+        const int v = MUL24 ? __mul24(p, mult) + rnd : p * mult + rnd;
+        o[e] = min(max(v >> shift, -128), 127);
+      }
+    }
+    store16(out, c, o);
+  }
+  if (CHECKED && bad) raise_flag(flags, FLAG_OVERFLOW);
 }
 
 // ------------------------------------------------------------------------------------------ strided copy
@@ -114,6 +226,43 @@ __global__ __launch_bounds__(E_THREADS) void quantize_kernel(const TI* __restric
   if (bad) raise_flag(flags, FLAG_NONFINITE);
 }
 
+// quantize over 16-element chunks: 64 (float) or 128 (double) input bytes and one or two 16-byte stores a lane; each
+// element as in quantize_kernel (float64 division, round half to even, clamp; a non-finite element flags and stores 0)
+template <typename TI, typename TO>
+__global__ __launch_bounds__(E_THREADS) void quantize_vec(const TI* __restrict__ x, double scale, long long n16,
+                                                           TO* __restrict__ out, int lo, int hi, unsigned* flags) {
+  bool bad = false;
+  for (long long c = (long long)blockIdx.x * E_THREADS + threadIdx.x; c < n16; c += (long long)gridDim.x * E_THREADS) {
+    double xv[16];
+    if constexpr (sizeof(TI) == 4) {
+      const float4* p = reinterpret_cast<const float4*>(x) + 4 * c;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 f = p[q];
+        xv[4 * q] = f.x, xv[4 * q + 1] = f.y, xv[4 * q + 2] = f.z, xv[4 * q + 3] = f.w;
+      }
+    } else {
+      const double2* p = reinterpret_cast<const double2*>(x) + 8 * c;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const double2 f = p[q];
+        xv[2 * q] = f.x, xv[2 * q + 1] = f.y;
+      }
+    }
+    int o[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const bool fin = isfinite(xv[e]);
+      bad |= !fin;
+      double v = rint(xv[e] / scale);
+      v = v < lo ? lo : (v > hi ? hi : v);
+      o[e] = fin ? (int)v : 0;
+    }
+    store16(out, c, o);
+  }
+  if (bad) raise_flag(flags, FLAG_NONFINITE);
+}
+
 // the float prelude of a token model: out[r][c] = clamp_out(rint((wte[ids[r]][c] + wpe[r % T][c]) / scale)), the
 // float32 tables read as float64, as the host computes x = wte[ids] + wpe[positions] in float64 and quantizes it
 template <typename TO>
@@ -139,16 +288,87 @@ __global__ __launch_bounds__(E_THREADS) void embed_quantize_kernel(const int64_t
   }
 }
 
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// One-element kernel over elements [from, n) of the operands (the tail past the vector kernel's chunks, or every
+// element when an operand is not 16-byte aligned).
+template <typename TA, typename TB, typename TO>
+static void launch_add_scalar(anvil_ctx* ctx, const TA* a, const TB* b, int ma, int mb, int s, long long from,
+                              long long n, TO* out) {
+  if (from >= n) return;
+  const long long rnd = s ? (1ll << (s - 1)) : 0;
+  const int lo = sizeof(TO) == 1 ? -128 : -32768, hi = sizeof(TO) == 1 ? 127 : 32767;
+  ANVIL_LAUNCH((add_requant_kernel<TA, TB, TO>), dim3(grid_for(n - from)), dim3(E_THREADS), 0, ctx->stream,
+               a + from, b + from, ma, mb, s, rnd, n - from, out + from, lo, hi, ctx->flags);
+}
+
+template <typename TA, typename TB, typename TO>
+static void launch_add_typed(anvil_ctx* ctx, const TA* a, const TB* b, int ma, int mb, int s, long long n, TO* out,
+                             bool unchecked) {
+  const long long n16 = (al16(a) && al16(b) && al16(out)) ? n / 16 : 0;
+  if (n16) {
+    const int rnd = s ? (int)(1u << (s - 1)) : 0;
+    const bool m24 = ma > -(1 << 23) && ma < (1 << 23) && mb > -(1 << 23) && mb < (1 << 23);
+    const dim3 gr(grid_for(n16)), bl(E_THREADS);
+    if (!unchecked)
+      ANVIL_LAUNCH((add_requant_vec<TA, TB, TO, true, false>), gr, bl, 0, ctx->stream, a, b, ma, mb, s, rnd, n16, out,
+                   ctx->flags);
+    else if (m24)
+      ANVIL_LAUNCH((add_requant_vec<TA, TB, TO, false, true>), gr, bl, 0, ctx->stream, a, b, ma, mb, s, rnd, n16, out,
+                   ctx->flags);
+    else
+      ANVIL_LAUNCH((add_requant_vec<TA, TB, TO, false, false>), gr, bl, 0, ctx->stream, a, b, ma, mb, s, rnd, n16,
+                   out, ctx->flags);
+  }
+  launch_add_scalar(ctx, a, b, ma, mb, s, n16 * 16, n, out);
+}
+
+// embed_quantize four columns a lane: float4 reads of the token's and the position's rows (C a multiple of 4), and
+// one 4-byte (i8) or 8-byte (i16) store; each element as in embed_quantize_kernel
+template <typename TO>
+__global__ __launch_bounds__(E_THREADS) void embed_quantize_vec4(const int64_t* __restrict__ ids,
+                                                                 const float* __restrict__ wte,
+                                                                 const float* __restrict__ wpe, long long rows,
+                                                                 int T, int C, int vocab, double scale,
+                                                                 TO* __restrict__ out, int lo, int hi,
+                                                                 unsigned* flags) {
+  const int c4 = C >> 2;
+  const long long n4 = rows * c4;
+  for (long long i = (long long)blockIdx.x * E_THREADS + threadIdx.x; i < n4; i += (long long)gridDim.x * E_THREADS) {
+    const long long r = i / c4;
+    const int c = (int)(i - r * c4) * 4;
+    const long long id = ids[r];
+    int o[4] = {0, 0, 0, 0};
+    if (id < 0 || id >= vocab) {
+      raise_flag(flags, FLAG_RANGE);
+    } else {
+      const float4 w = *reinterpret_cast<const float4*>(wte + id * C + c);
+      const float4 p = *reinterpret_cast<const float4*>(wpe + (r % T) * C + c);
+      const double xs[4] = {(double)w.x + (double)p.x, (double)w.y + (double)p.y, (double)w.z + (double)p.z,
+                            (double)w.w + (double)p.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        double v = rint(xs[e] / scale);
+        v = v < lo ? lo : (v > hi ? hi : v);
+        o[e] = (int)v;
+      }
+    }
+    if constexpr (sizeof(TO) == 1) {
+      reinterpret_cast<unsigned*>(out)[i] = pack4(o[0], o[1], o[2], o[3]);
+    } else {
+      reinterpret_cast<uint2*>(out)[i] = uint2{__builtin_amdgcn_perm((unsigned)o[1], (unsigned)o[0], 0x05040100u),
+                                               __builtin_amdgcn_perm((unsigned)o[3], (unsigned)o[2], 0x05040100u)};
+    }
+  }
+}
+
 template <typename TA, typename TB>
 static void launch_add(anvil_ctx* ctx, const void* a, const void* b, int ma, int mb, int s, long long n, void* out,
-                       int out_dtype) {
-  const long long rnd = s ? (1ll << (s - 1)) : 0;
+                       int out_dtype, bool unchecked) {
   if (out_dtype == ANVIL_I8)
-    ANVIL_LAUNCH((add_requant_kernel<TA, TB, int8_t>), dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream,
-                       (const TA*)a, (const TB*)b, ma, mb, s, rnd, n, (int8_t*)out, -128, 127, ctx->flags);
+    launch_add_typed(ctx, (const TA*)a, (const TB*)b, ma, mb, s, n, (int8_t*)out, unchecked);
   else
-    ANVIL_LAUNCH((add_requant_kernel<TA, TB, int16_t>), dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream,
-                       (const TA*)a, (const TB*)b, ma, mb, s, rnd, n, (int16_t*)out, -32768, 32767, ctx->flags);
+    launch_add_typed(ctx, (const TA*)a, (const TB*)b, ma, mb, s, n, (int16_t*)out, unchecked);
 }
 
 }  // namespace anvil
@@ -159,7 +379,14 @@ extern "C" {
 
 int anvil_add_requant(anvil_ctx* ctx, const void* a, int a_dtype, const void* b, int b_dtype, int32_t ma, int32_t mb,
                       int shift, int64_t n, void* out, int out_dtype) {
+  return anvil_add_requant_ex(ctx, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype, 0);
+}
+
+int anvil_add_requant_ex(anvil_ctx* ctx, const void* a, int a_dtype, const void* b, int b_dtype, int32_t ma,
+                         int32_t mb, int shift, int64_t n, void* out, int out_dtype, int flags) {
   if (int r = check_ctx(ctx)) return r;
+  if (flags & ~ANVIL_OP_UNCHECKED) return set_error(ANVIL_E_VALUE, "anvil_add_requant_ex: unknown flags %d", flags);
+  const bool unchecked = (flags & ANVIL_OP_UNCHECKED) != 0;
   if (!a || !b || !out) return set_error(ANVIL_E_VALUE, "anvil_add_requant: null pointer");
   auto wide = [](int d) { return d == ANVIL_I8 || d == ANVIL_I16; };
   if (!wide(a_dtype) || !wide(b_dtype) || !wide(out_dtype))
@@ -168,13 +395,13 @@ int anvil_add_requant(anvil_ctx* ctx, const void* a, int a_dtype, const void* b,
   if (n < 0) return set_error(ANVIL_E_VALUE, "anvil_add_requant: negative size");
   if (n == 0) return ANVIL_OK;
   if (a_dtype == ANVIL_I8 && b_dtype == ANVIL_I8)
-    launch_add<int8_t, int8_t>(ctx, a, b, ma, mb, shift, n, out, out_dtype);
+    launch_add<int8_t, int8_t>(ctx, a, b, ma, mb, shift, n, out, out_dtype, unchecked);
   else if (a_dtype == ANVIL_I8)
-    launch_add<int8_t, int16_t>(ctx, a, b, ma, mb, shift, n, out, out_dtype);
+    launch_add<int8_t, int16_t>(ctx, a, b, ma, mb, shift, n, out, out_dtype, unchecked);
   else if (b_dtype == ANVIL_I8)
-    launch_add<int16_t, int8_t>(ctx, a, b, ma, mb, shift, n, out, out_dtype);
+    launch_add<int16_t, int8_t>(ctx, a, b, ma, mb, shift, n, out, out_dtype, unchecked);
   else
-    launch_add<int16_t, int16_t>(ctx, a, b, ma, mb, shift, n, out, out_dtype);
+    launch_add<int16_t, int16_t>(ctx, a, b, ma, mb, shift, n, out, out_dtype, unchecked);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }
@@ -184,21 +411,46 @@ int anvil_lut_i8(anvil_ctx* ctx, const int8_t* x, const int8_t* table, int64_t n
   if (!x || !table || !out) return set_error(ANVIL_E_VALUE, "anvil_lut_i8: null pointer");
   if (n < 0) return set_error(ANVIL_E_VALUE, "anvil_lut_i8: negative size");
   if (n == 0) return ANVIL_OK;
-  ANVIL_LAUNCH(lut_kernel, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, x, table, (long long)n, out);
+  const long long n16 = (al16(x) && al16(out)) ? n / 16 : 0;
+  if (n16) ANVIL_LAUNCH(lut_vec, dim3(grid_for(n16)), dim3(E_THREADS), 0, ctx->stream, x, table, n16, out);
+  if (n16 * 16 < n)
+    ANVIL_LAUNCH(lut_kernel, dim3(grid_for(n - n16 * 16)), dim3(E_THREADS), 0, ctx->stream, x + n16 * 16, table,
+                 (long long)(n - n16 * 16), out + n16 * 16);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }
 
 int anvil_lut_mul(anvil_ctx* ctx, const int8_t* x, const int8_t* y, const int8_t* table, int32_t mult, int shift,
                   int64_t n, int8_t* out) {
+  return anvil_lut_mul_ex(ctx, x, y, table, mult, shift, n, out, 0);
+}
+
+int anvil_lut_mul_ex(anvil_ctx* ctx, const int8_t* x, const int8_t* y, const int8_t* table, int32_t mult, int shift,
+                     int64_t n, int8_t* out, int flags) {
   if (int r = check_ctx(ctx)) return r;
+  if (flags & ~ANVIL_OP_UNCHECKED) return set_error(ANVIL_E_VALUE, "anvil_lut_mul_ex: unknown flags %d", flags);
   if (!x || !y || !table || !out) return set_error(ANVIL_E_VALUE, "anvil_lut_mul: null pointer");
   if (shift < 0 || shift > 31) return set_error(ANVIL_E_VALUE, "shift %d outside [0, 31]", shift);
   if (n < 0) return set_error(ANVIL_E_VALUE, "anvil_lut_mul: negative size");
   if (n == 0) return ANVIL_OK;
   const long long rnd = shift ? (1ll << (shift - 1)) : 0;
-  ANVIL_LAUNCH(lut_mul_kernel, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, x, y, table, mult, shift,
-                     rnd, (long long)n, out, ctx->flags);
+  const long long n16 = (al16(x) && al16(y) && al16(out)) ? n / 16 : 0;
+  if (n16) {
+    const dim3 gr(grid_for(n16)), bl(E_THREADS);
+    if (!(flags & ANVIL_OP_UNCHECKED))
+      ANVIL_LAUNCH((lut_mul_vec<true, false>), gr, bl, 0, ctx->stream, x, y, table, mult, shift, (int)rnd, n16, out,
+                   ctx->flags);
+    else if (mult > -(1 << 23) && mult < (1 << 23))
+      ANVIL_LAUNCH((lut_mul_vec<false, true>), gr, bl, 0, ctx->stream, x, y, table, mult, shift, (int)rnd, n16, out,
+                   ctx->flags);
+    else
+      ANVIL_LAUNCH((lut_mul_vec<false, false>), gr, bl, 0, ctx->stream, x, y, table, mult, shift, (int)rnd, n16,
+                   out, ctx->flags);
+  }
+  const long long from = n16 * 16;
+  if (from < n)
+    ANVIL_LAUNCH(lut_mul_kernel, dim3(grid_for(n - from)), dim3(E_THREADS), 0, ctx->stream, x + from, y + from, table,
+                 mult, shift, rnd, (long long)(n - from), out + from, ctx->flags);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
 }
@@ -255,6 +507,30 @@ int anvil_quantize(anvil_ctx* ctx, const void* x, int x_is_f64, double scale, in
   if (out_dtype != ANVIL_I8 && out_dtype != ANVIL_I16) return set_error(ANVIL_E_VALUE, "quantize result i8 or i16");
   if (n <= 0) return n < 0 ? set_error(ANVIL_E_VALUE, "anvil_quantize: negative size") : ANVIL_OK;
   const int lo = dtype_lo(out_dtype), hi = dtype_hi(out_dtype);
+  const long long n16 = (al16(x) && al16(out)) ? n / 16 : 0;
+  if (n16) {
+    const dim3 g16(grid_for(n16)), b16(E_THREADS);
+    if (x_is_f64 && out_dtype == ANVIL_I8)
+      ANVIL_LAUNCH((quantize_vec<double, int8_t>), g16, b16, 0, ctx->stream, (const double*)x, scale, n16,
+                   (int8_t*)out, lo, hi, ctx->flags);
+    else if (x_is_f64)
+      ANVIL_LAUNCH((quantize_vec<double, int16_t>), g16, b16, 0, ctx->stream, (const double*)x, scale, n16,
+                   (int16_t*)out, lo, hi, ctx->flags);
+    else if (out_dtype == ANVIL_I8)
+      ANVIL_LAUNCH((quantize_vec<float, int8_t>), g16, b16, 0, ctx->stream, (const float*)x, scale, n16,
+                   (int8_t*)out, lo, hi, ctx->flags);
+    else
+      ANVIL_LAUNCH((quantize_vec<float, int16_t>), g16, b16, 0, ctx->stream, (const float*)x, scale, n16,
+                   (int16_t*)out, lo, hi, ctx->flags);
+  }
+  const long long from = n16 * 16;
+  if (from == n) {
+    ANVIL_LAUNCHED();
+    return ANVIL_OK;
+  }
+  n -= from;
+  x = (const char*)x + from * (x_is_f64 ? 8 : 4);
+  out = (char*)out + from * (out_dtype == ANVIL_I8 ? 1 : 2);
   dim3 gr(grid_for(n)), bl(E_THREADS);
   if (x_is_f64 && out_dtype == ANVIL_I8)
     ANVIL_LAUNCH((quantize_kernel<double, int8_t>), gr, bl, 0, ctx->stream, (const double*)x, scale, (long long)n,
@@ -286,6 +562,16 @@ int anvil_embed_quantize(anvil_ctx* ctx, const int64_t* ids, int64_t rows, int T
   if (rows == 0) return ANVIL_OK;
   const long long n = rows * C;
   const int lo = dtype_lo(out_dtype), hi = dtype_hi(out_dtype);
+  if (C % 4 == 0 && al16(wte) && al16(wpe) && ((uintptr_t)out & (out_dtype == ANVIL_I8 ? 3 : 7)) == 0) {
+    if (out_dtype == ANVIL_I8)
+      ANVIL_LAUNCH(embed_quantize_vec4<int8_t>, dim3(grid_for(n / 4)), dim3(E_THREADS), 0, ctx->stream, ids, wte, wpe,
+                   (long long)rows, T, C, vocab, scale, (int8_t*)out, lo, hi, ctx->flags);
+    else
+      ANVIL_LAUNCH(embed_quantize_vec4<int16_t>, dim3(grid_for(n / 4)), dim3(E_THREADS), 0, ctx->stream, ids, wte,
+                   wpe, (long long)rows, T, C, vocab, scale, (int16_t*)out, lo, hi, ctx->flags);
+    ANVIL_LAUNCHED();
+    return ANVIL_OK;
+  }
   if (out_dtype == ANVIL_I8)
     ANVIL_LAUNCH(embed_quantize_kernel<int8_t>, dim3(grid_for(n)), dim3(E_THREADS), 0, ctx->stream, ids, wte, wpe,
                        (long long)rows, T, C, vocab, scale, (int8_t*)out, lo, hi, ctx->flags);

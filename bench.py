@@ -43,6 +43,13 @@ def main():
     ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--keep", default="outputs", choices=["outputs", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--model", choices=["v1", "v2"],
+                    help="run the reference's frozen 2-layer model (v1 int8, v2 with the int16 residual stream) over "
+                         "--batch sequences instead of a config block, checked against the oracle on a sample")
+    ap.add_argument("--batch", type=int, default=16384, help="sequences per step with --model")
+    ap.add_argument("--eltwise", action="store_true",
+                    help="time the element-wise kernels (add_requant, lut, lut_mul, quantize, embed_quantize) at "
+                         "config-5 sizes against the stream-copy bandwidth, and print that line instead")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a contiguous 1 GiB device copy: the known-size kernel that scales the FETCH_SIZE / "
                          "WRITE_SIZE counters behind roofline.traffic")
@@ -57,6 +64,15 @@ def main():
         sys.exit("bench.py: --steps must be >= 1 and --warmup >= 0")
     if args.copy_calibration:
         return copy_calibration()
+    if args.eltwise:
+        print(json.dumps(bench_eltwise(args)), flush=True)
+        return
+    if args.model:
+        line = bench_frozen(args)
+        print(json.dumps(line), flush=True)
+        if not line["oracle_check"]["matches"]:
+            sys.exit("bench.py: the GPU output differs from the oracle on the sampled sequences")
+        return
     line = bench_linear(args) if args.config == 2 else bench_block(args)
     print(json.dumps(line), flush=True)
     base = line.get("cpu_baseline") or {}
@@ -271,6 +287,138 @@ def bench_linear(args):
                         "second bound",
         "cpu_baseline": cpu,
     }
+
+
+def bench_frozen(args):
+    """The reference's two frozen 2-layer models (anvil/codesign/workloads.py:40-72; the model files
+    data/cost/model_graph.json.gz and data/codesign/model_graph.json.gz, kept here as tests/golden/model_graph_v1 and
+    _v2), loaded from their printed IR and run batched: --batch sequences of 16 tokens, seeded integer inputs over the
+    input dtype's range. A step is one forward of the model over the batch (keep="outputs", inputs resident in HBM).
+    v2 carries the int16 residual stream: its four add_requant ops run in the epilogues of the GEMMs that produce
+    their int16 operand. The GPU's outputs are checked against the oracle on 64 sampled sequences."""
+    import gzip
+
+    import numpy as np
+
+    import anvil_mi355x
+    from oracle import interp
+
+    body = json.load(gzip.open(ROOT / "tests" / "golden" / f"model_graph_{args.model}.json.gz", "rt"))
+    consts = {k: np.asarray(v, dtype=np.int64).reshape(body["shapes"][k]) for k, v in body["consts"].items()}
+    module = anvil_mi355x.parse_ir(body["ir"])
+    cm = anvil_mi355x.compile((module, consts))
+    nb = args.batch
+    t, c = cm.meta[cm.inputs[0]][1]
+    dt = cm.meta[cm.inputs[0]][2]
+    lim = {"i8": 128, "i16": 1 << 15}[dt]
+    xs = np.random.default_rng(17).integers(-lim, lim, (nb, t, c))
+    plan = cm.plan(nb)
+    dev = cm.dev
+    cm.upload_inputs(plan, {cm.inputs[0]: xs})
+    steps = plan.steps
+    for _ in range(args.warmup):
+        cm.launch(plan)
+    dev.sync()
+    first = kernel_times(dev, steps)
+    dom = max(range(len(steps)), key=first.__getitem__)
+    K = args.steps
+    wall_s, device_ms, dom_us, n = timed_steps(dev, steps, K, dom)
+    per = kernel_times(dev, steps)
+    graph = graph_steps(cm, plan, K)
+    sample = np.unique(np.concatenate([[0, nb - 1], np.random.default_rng(3).integers(0, nb, 62)]))
+    got = cm.read(plan, cm.outputs)
+    want = interp.run(module, {cm.inputs[0]: xs[sample]}, consts, batch=True)
+    matches = all(np.array_equal(got[o][sample], want.values[o]) for o in cm.outputs)
+    kernels = {}
+    for i, (label, _, _) in enumerate(steps):
+        k_, o_, b_ = plan.works[i]
+        e = {"kind": k_, "us": round(per[i], 2), "GBs": round(b_ / (per[i] * 1e-6) / 1e9, 1)}
+        if k_ in ("gemm", "attention"):
+            e["TOPS"] = round(o_ / (per[i] * 1e-6) / 1e12, 2)
+        kernels[label] = e
+    kind, ops, nbytes = plan.works[dom]
+    return {"metric": f"frozen 2-layer model {args.model} tokens/sec at 1 MI355X", "value": round(nb * t * K / wall_s, 1),
+            "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
+            "ms_per_step": round(wall_s / K * 1e3, 4), "higher_is_better": True, "dtype": dt, "data": "synthetic",
+            "config": {"workload": f"reference frozen model {args.model} (2 layers, C {c}, T {t}, input {dt}), "
+                                   f"batch {nb}, keep=outputs", "batch": nb, "seq_len": t, "n_embd": c},
+            "device_ms_per_step": round(device_ms / K, 4),
+            "dominant": roofline(kind, ops, nbytes, dom_us, steps[dom][0], n),
+            "hip_graph": graph, "kernels": kernels, "kernels_us_sum": round(sum(per), 2),
+            "standalone_adds": sum(1 for k in kernels.values() if k["kind"] == "add"),
+            "oracle_check": {"sequences": int(len(sample)), "matches": bool(matches)}}
+
+
+def bench_eltwise(args):
+    """The element-wise kernels at config-5 sizes (R = 32768 rows of C = 768, F = 3072), inputs resident in HBM, each
+    launch timed on the kernel alone (events bound to its dispatch), mean over --steps launches after --warmup:
+
+    * add_requant (anvil/semantics.py:106-115) of R x C elements, i8 + i8 -> i8 (the block's residual add when it is
+      not fused), i16 + i16 -> i16 and i16 + i8 -> i16 (the wide residual stream, ADR-004), proven (unchecked) and
+      checked;
+    * lut (anvil/semantics.py:87-92) and lut_mul (anvil/interp/graph.py:67-68) over R x F: an unfused GELU table on
+      the fc result, and a SwiGLU gate;
+    * quantize (anvil/driver.py:233-241) of R x C float32 and float64 inputs to i8: cm.run's float input;
+    * embed_quantize: R rows of token ids through float32 tables of C columns (config 4's prelude at config-5 size).
+
+    Algorithmic bytes count every operand and result once at its dtype (tables excluded). Each figure is reported
+    against the stream-copy bandwidth measured in the same run and against the 8 TB/s peak."""
+    import numpy as np
+
+    from anvil_mi355x import runtime as rt
+    dev = rt.device(0)
+    R, C, F = 32768, 768, 3072
+    rng = np.random.default_rng(5)
+
+    def ints(n, dt):
+        lim = {"i8": 128, "i16": 1 << 15}[dt]
+        return dev.upload(rng.integers(-lim, lim, n).astype(rt.NP_DTYPE[dt]))
+
+    n1, n4 = R * C, R * F
+    a8, b8, a16, b16 = ints(n1, "i8"), ints(n1, "i8"), ints(n1, "i16"), ints(n1, "i16")
+    x4, y4 = ints(n4, "i8"), ints(n4, "i8")
+    table = ints(256, "i8")
+    out1, out4 = dev.alloc(2 * n1), dev.alloc(n4)
+    xf32 = dev.upload((rng.standard_normal(n1) * 2).astype(np.float32))
+    xf64 = dev.upload((rng.standard_normal(n1) * 2).astype(np.float64))
+    vocab, T = 512, 1024
+    ids = dev.upload(rng.integers(0, vocab, R).astype(np.int64))
+    wte = dev.upload((rng.standard_normal((vocab, C)) * 0.02).astype(np.float32))
+    wpe = dev.upload((rng.standard_normal((T, C)) * 0.02).astype(np.float32))
+    U = rt.OP_UNCHECKED
+    # multipliers of the wide stream's scale: a Ma + b Mb + rnd stays inside int32 at every operand value
+    cases = [
+        ("add_i8_i8_i8", 3 * n1, dev.add_requant, (a8, "i8", b8, "i8", 3000, -2500, 13, n1, out1, "i8", U)),
+        ("add_i16_i16_i16", 6 * n1, dev.add_requant, (a16, "i16", b16, "i16", 16000, -12000, 15, n1, out1, "i16", U)),
+        ("add_i16_i8_i16", 5 * n1, dev.add_requant, (a16, "i16", b8, "i8", 16000, -3000000, 15, n1, out1, "i16", U)),
+        ("add_i16_i16_i16_checked", 6 * n1, dev.add_requant,
+         (a16, "i16", b16, "i16", 16000, -12000, 15, n1, out1, "i16", 0)),
+        ("lut", 2 * n4, dev.lut_i8, (x4, table, n4, out4)),
+        ("lut_mul", 3 * n4, dev.lut_mul, (x4, y4, table, 300, 12, n4, out4, U)),
+        ("quantize_f32_i8", 5 * n1, dev.quantize, (xf32, False, 0.025, n1, out1, "i8")),
+        ("quantize_f64_i8", 9 * n1, dev.quantize, (xf64, True, 0.025, n1, out1, "i8")),
+        ("embed_quantize_i8", 9 * n1 + 8 * R, dev.embed_quantize, (ids, R, T, C, wte, vocab, wpe, 0.01, out1, "i8")),
+    ]
+    stream = stream_copy(dev)
+    reps = max(1, min(args.steps, SLOTS))
+    kernels = {}
+    for name, nbytes, fn, a in cases:
+        for _ in range(max(1, args.warmup)):
+            fn(*a)
+        dev.sync()
+        for k in range(reps):
+            dev.timed(16 + 2 * k, 17 + 2 * k, fn, *a)
+        dev.sync()
+        us = 1e3 * sum(dev.elapsed_ms(16 + 2 * k, 17 + 2 * k) for k in range(reps)) / reps
+        gbs = nbytes / (us * 1e-6) / 1e9
+        kernels[name] = {"us": round(us, 2), "bytes": nbytes, "GBs": round(gbs, 1),
+                         "frac_stream": round(gbs / stream["GBs"], 3), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    return {"metric": "element-wise kernels at config-5 sizes: achieved HBM GB/s against the stream copy and peak",
+            "unit": "GB/s", "n_gpus": 1, "launches": reps, "warmup": args.warmup, "data": "synthetic",
+            "config": {"workload": "config5 sizes: R = 32768 rows, C = 768, F = 3072; inputs resident in HBM"},
+            "hbm_stream": stream, "kernels": kernels,
+            "note": "bytes = every operand and result once at its dtype; us = mean over the launches, each timed on "
+                    "the kernel alone (events bound to its dispatch)"}
 
 
 def measured_traffic(config, keep, label):

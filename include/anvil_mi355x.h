@@ -184,6 +184,15 @@ int anvil_gemm_i8_add(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, int8_t*
                       const int8_t* R, int32_t ma, int32_t mb, int shift2, int8_t* D, const int64_t* rstrides,
                       int flags);
 
+/* anvil_gemm_i8_add with the result dtype as an argument (ADR-004's wide residual stream, reference
+ * docs/decisions/ADR-004-small-inputs.md:59-82 and anvil/semantics.py:106-115): y, R and D are all out_dtype, ANVIL_I8
+ * or ANVIL_I16 (no LUT with i16), D = clamp_out((R * ma + y * mb + 2^(shift2-1)) >> shift2). Same conditions as
+ * anvil_gemm_i8_add. */
+int anvil_gemm_i8_add_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
+                         int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
+                         const void* R, int32_t ma, int32_t mb, int shift2, void* D, const int64_t* rstrides,
+                         int flags);
+
 /* rmsnorm_int over rows of `cols` elements (reference anvil/semantics.py:158-182, golden.rmsnorm_int):
  *   ss = ss_init + sum_j ((x_j^2 + 2^(ss_shift-1)) >> ss_shift); (i, k) = rsqrt_index(ss, lut_len);
  *   out_j = clamp_i8((x_j * w_j * lut[i] * mult + 2^(shift+k-1)) >> (shift + k)).
@@ -241,6 +250,13 @@ int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const i
  *   out = clamp_out((a * ma + b * mb + 2^(shift-1)) >> shift), a and b ANVIL_I8 or ANVIL_I16, n elements. */
 int anvil_add_requant(anvil_ctx* ctx, const void* a, int a_dtype, const void* b, int b_dtype, int32_t ma, int32_t mb,
                       int shift, int64_t n, void* out, int out_dtype);
+/* anvil_add_requant with flags (reference anvil/semantics.py:106-115, anvil/interp/graph.py:65-66): flags 0 keeps the
+ * reference's int32 checks (an overflow makes the next anvil_sync return ANVIL_E_OVERFLOW); ANVIL_OP_UNCHECKED states
+ * that the caller has proven a * ma + b * mb + 2^(shift-1) inside int32 for every element (the quantizer's
+ * prove_no_overflow, anvil/frontend/quantize.py:235-238), and the sum is computed in 32 bits. 16-byte aligned
+ * operands run 16 elements a lane. */
+int anvil_add_requant_ex(anvil_ctx* ctx, const void* a, int a_dtype, const void* b, int b_dtype, int32_t ma,
+                         int32_t mb, int shift, int64_t n, void* out, int out_dtype, int flags);
 
 /* lut (reference anvil/semantics.py:87-92): out = table[x + 128], int8, n elements. */
 int anvil_lut_i8(anvil_ctx* ctx, const int8_t* x, const int8_t* table, int64_t n, int8_t* out);
@@ -248,6 +264,10 @@ int anvil_lut_i8(anvil_ctx* ctx, const int8_t* x, const int8_t* table, int64_t n
 /* lut_mul (golden.swiglu_lut via anvil/interp/graph.py:67-68): out = requant(table[x + 128] * y, mult, shift). */
 int anvil_lut_mul(anvil_ctx* ctx, const int8_t* x, const int8_t* y, const int8_t* table, int32_t mult, int shift,
                   int64_t n, int8_t* out);
+/* anvil_lut_mul with flags (same op): flags 0 keeps the reference's int32 checks; ANVIL_OP_UNCHECKED states that
+ * table[x + 128] * y * mult + 2^(shift-1) is proven inside int32 (anvil/frontend/quantize.py:206-210). */
+int anvil_lut_mul_ex(anvil_ctx* ctx, const int8_t* x, const int8_t* y, const int8_t* table, int32_t mult, int shift,
+                     int64_t n, int8_t* out, int flags);
 
 /* transpose / reshape (reference anvil/interp/graph.py:76-81) when a consumer needs a view laid out densely:
  * dst (contiguous, dims[0..rank)) = src viewed with element strides src_strides. elem_size 1, 2 or 4; rank <= 6. */

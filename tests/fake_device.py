@@ -22,6 +22,7 @@ class FakeBuffer:
     def __init__(self, dev, nbytes):
         self.dev, self.nbytes = dev, int(nbytes)
         self.ptr = dev._bump(max(1, self.nbytes))
+        dev.buffers.append((self.ptr, self.ptr + self.nbytes))
 
     def upload(self, arr, offset=0):
         arr = np.ascontiguousarray(arr)
@@ -70,6 +71,7 @@ class FakeDevice:
         self.lock = threading.Lock()
         self.calls = []
         self.flags = 0
+        self.buffers = []            # (start, end) of every allocation, for the operand-range checks
 
     def _bump(self, n):
         p = BASE + self.top
@@ -130,9 +132,22 @@ class FakeDevice:
             return None
 
     # ---------------------------------------------------------------------------------------------- ops
+    def _in_one_buffer(self, ptr, nbytes, what):
+        """The kernels' buffer resource of a GEMM operand spans [ptr, ptr + nbytes): from the first row's base to the
+        last row's K-th byte (row-major) or the last K block's last row (K-blocked). Loads anywhere inside it must
+        stay inside the allocation the operand lives in, as the kernels read stages past K within that range."""
+        ptr = ptr.ptr if hasattr(ptr, "ptr") else int(ptr)
+        assert any(s <= ptr and ptr + nbytes <= e for s, e in self.buffers), \
+            f"{what}: operand range [{ptr:#x}, {ptr + nbytes:#x}) leaves its allocation"
+
+    def _check_operands(self, A, Bt, b0, b1, M, N, K, strides, flags):
+        self._in_one_buffer(A, 1 + self._operand_end((b0, b1, M), strides[0:3], flags & rt.GEMM_A_KBLOCK, K), "A")
+        self._in_one_buffer(Bt, 1 + self._operand_end((b0, b1, N), strides[3:6], flags & rt.GEMM_B_KBLOCK, K), "Bt")
+
     def gemm_i8(self, A, Bt, Cp, b0, b1, M, N, K, strides, mult, shift, lut, out_dtype, flags=0):
         """Every output is computed, also under the causal flags (a superset of what the kernel writes)."""
         self.calls.append(("gemm", b0, b1, M, N, K, tuple(strides), flags))
+        self._check_operands(A, Bt, b0, b1, M, N, K, strides, flags)
         sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc = strides
         a = self._operand(A, b0, b1, M, K, sa0, sa1, lda, flags & rt.GEMM_A_KBLOCK)
         bt = self._operand(Bt, b0, b1, N, K, sb0, sb1, ldb, flags & rt.GEMM_B_KBLOCK)
@@ -201,24 +216,26 @@ class FakeDevice:
             self.gemm_i8(*c)
 
     def gemm_i8_add(self, A, Bt, Cp, b0, b1, M, N, K, strides, mult, shift, lut, R, ma, mb, shift2, D, rstrides,
-                    flags):
-        """y = qmatmul epilogue, D = add_requant of the residual R (times ma) and y (times mb)."""
-        self.calls.append(("gemm_add", b0, b1, M, N, K, tuple(strides), flags, Cp is not None))
+                    flags, out_dtype="i8"):
+        """y = qmatmul epilogue, D = add_requant of the residual R (times ma) and y (times mb); y, R, D out_dtype."""
+        dt = out_dtype
+        self.calls.append(("gemm_add", b0, b1, M, N, K, tuple(strides), flags, Cp is not None, dt))
+        self._check_operands(A, Bt, b0, b1, M, N, K, strides, flags)
         sa0, sa1, lda, sb0, sb1, ldb, sc0, sc1, ldc = strides
         sr0, sr1, ldr, sd0, sd1, ldd = rstrides
         a = self._operand(A, b0, b1, M, K, sa0, sa1, lda, flags & rt.GEMM_A_KBLOCK)
         bt = self._operand(Bt, b0, b1, N, K, sb0, sb1, ldb, flags & rt.GEMM_B_KBLOCK)
         lt = None if lut is None else self.view(lut, "i8", (256,), (1,)).astype(np.int64)
-        r = self.view(R, "i8", (b0, b1, M, N), (sr0, sr1, ldr, 1)).astype(np.int64)
+        r = self.view(R, dt, (b0, b1, M, N), (sr0, sr1, ldr, 1)).astype(np.int64)
 
         def both():
-            y = sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, "i8", fast=self.fast)
-            return y, sem.add_requant(r, y, ma, mb, shift2, "i8")
+            y = sem.qmatmul(a, np.swapaxes(bt, -1, -2), mult, shift, lt, dt, fast=self.fast)
+            return y, sem.add_requant(r, y, ma, mb, shift2, dt)
         out = self._guard(both)
         if out is not None:
             if Cp is not None:
-                self._store_result(Cp, "i8", b0, b1, M, N, (sc0, sc1, ldc), flags & rt.GEMM_C_KBLOCK, out[0])
-            self.store(D, "i8", (b0, b1, M, N), (sd0, sd1, ldd, 1), out[1])
+                self._store_result(Cp, dt, b0, b1, M, N, (sc0, sc1, ldc), flags & rt.GEMM_C_KBLOCK, out[0])
+            self.store(D, dt, (b0, b1, M, N), (sd0, sd1, ldd, 1), out[1])
 
     def attention_i8(self, Q, K, Vt, O, b0, b1, T, D, strides, ms, ss, lut, one, causal, mo, so, flags):
         """The three ops the fused kernel replaces, over the same strided operands."""
@@ -256,8 +273,8 @@ class FakeDevice:
         if r is not None:
             self.store(out, out_dtype, (batch, t1, t2), (t1 * t2, t2, 1), r)
 
-    def add_requant(self, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype):
-        self.calls.append(("add", n))
+    def add_requant(self, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype, flags=0):
+        self.calls.append(("add", n, flags))
         av = self.view(a, a_dtype, (n,), (1,)).astype(np.int64)
         bv = self.view(b, b_dtype, (n,), (1,)).astype(np.int64)
         r = self._guard(lambda: sem.add_requant(av, bv, ma, mb, shift, out_dtype))
@@ -269,8 +286,8 @@ class FakeDevice:
         r = sem.lut_i8(self.view(x, "i8", (n,), (1,)).astype(np.int64), self.view(table, "i8", (256,), (1,)))
         self.store(out, "i8", (n,), (1,), r)
 
-    def lut_mul(self, x, y, table, mult, shift, n, out):
-        self.calls.append(("lut_mul", n))
+    def lut_mul(self, x, y, table, mult, shift, n, out, flags=0):
+        self.calls.append(("lut_mul", n, flags))
         xv = self.view(x, "i8", (n,), (1,)).astype(np.int64)
         yv = self.view(y, "i8", (n,), (1,)).astype(np.int64)
         tv = self.view(table, "i8", (256,), (1,)).astype(np.int64)

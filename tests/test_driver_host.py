@@ -311,6 +311,28 @@ def test_wide_frozen_model_selects_the_fast_wide_rmsnorm(fake):
     assert all(c[3] & rt.RMS_S24 for c in rms)
 
 
+@pytest.mark.parametrize("keep", ["outputs", "all"])
+def test_wide_frozen_model_fuses_its_i16_residual_adds(fake, keep):
+    """The v2 frozen model's four int16 add_requant ops (i16 residual plus the i16 result of down / y) run in the
+    epilogue of the GEMM that produces y: no standalone add launch is left, every fused call carries the i16 dtype,
+    and every value equals the oracle's."""
+    text, consts, x = helpers.reference_model("v2")
+    m = anvil_mi355x.parse_ir(text)
+    cm = anvil_mi355x.compile((m, consts))
+    xs = np.random.default_rng(6).integers(-32768, 32768, (3, 16, 32))
+    res = cm.run(xs, "mi355x", quantized=True, batch=True, keep=keep)
+    want = interp.run(m, {"x": xs}, consts, batch=True)
+    for k, v in res.ints.items():
+        assert np.array_equal(v, want.values[k]), k
+    kinds = [c[0] for c in fake.calls]
+    adds = [c for c in fake.calls if c[0] == "gemm_add"]
+    n_add = sum(isinstance(op, anvil_mi355x.ir.AddRequantOp) for op in anvil_mi355x.ir.func_of(m).ops)
+    assert n_add == 4
+    assert kinds.count("add") == 0 and len(adds) == n_add and all(c[-1] == "i16" for c in adds)
+    # the products' own i16 results are stored only when they are returned
+    assert all(c[8] == (keep == "all") for c in adds)
+
+
 def test_gemm_operands_are_planned_kblocked(fake, cfg1):
     """keep="outputs" on a proven block: values read only as the left operand of linear products (h1, h2 and the fc
     result) are stored K-blocked by their producers (RMS_OUT_KBLOCK, GEMM_C_KBLOCK) and read K-blocked (A_KBLOCK, or
@@ -459,3 +481,23 @@ def test_graph_runs_replay_the_captured_steps(fake):
         assert np.array_equal(eager.ints["out"], res.ints["out"])
     plan = cm.plan(2)
     assert fake.captures == 1 and plan.graph.launches == 3
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 5])
+@pytest.mark.parametrize("keep", ["outputs", "all"])
+def test_gemm_operand_ranges_stay_inside_their_allocations(monkeypatch, n, keep):
+    """Every GEMM the planner launches for the configs (two sequences each, both keep modes) has operands whose
+    buffer-resource range -- base of the first row up to the last row's K-th byte, or the last K block of a K-blocked
+    operand -- lies inside one allocation. The kernels read stages past K anywhere in that range (so a head's slice
+    of q may be read into the next head's columns), which is only safe inside the operand's own buffer; the stand-in
+    device asserts it on every call."""
+    dev = fake_device.FakeDevice(heap_bytes=1 << 30, fast=True)
+    monkeypatch.setattr(rt, "device", lambda index=0: dev)
+    built, _ = models.config(n)
+    cm = anvil_mi355x.compile(built)
+    x = models.eval_inputs(built.spec, 2, models.config_tag(n))
+    if built.spec.vocab:
+        res = cm.run(x, "mi355x", batch=True, keep=keep, tokens=True)
+    else:
+        res = cm.run(x, "mi355x", batch=True, keep=keep)
+    assert res.ints and any(c[0] in ("gemm", "gemm_add", "gemm_group") for c in dev.calls)

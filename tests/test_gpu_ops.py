@@ -287,6 +287,71 @@ def test_lut_and_lut_mul(dev):
     assert np.array_equal(out.download((n,), np.int8).astype(np.int64), sem.swiglu_lut(x, y, t, 300, 12))
 
 
+@pytest.mark.parametrize("da,db,do", DT_PAIRS)
+@pytest.mark.parametrize("wide_m", [False, True])
+def test_add_requant_unchecked_vector_and_tail(dev, da, db, do, wide_m):
+    """ANVIL_OP_UNCHECKED (a proven graph): 32-bit arithmetic, 24-bit multiplies when |Ma|, |Mb| < 2^23 and 32-bit
+    ones otherwise, 16 elements a lane over aligned operands plus the n % 16 tail, and operands offset off the 16-byte
+    grid (one-element kernel) -- all equal to the reference's checked formula (anvil/semantics.py:106-115)."""
+    rng = np.random.default_rng([23, DT_PAIRS.index((da, db, do)), int(wide_m)])
+    lim = {"i8": 128, "i16": 1 << 15}
+    # multipliers whose worst case a Ma + b Mb + rnd stays inside int32 at these operand ranges: with wide_m, Ma is
+    # past 24 bits (32-bit multiplies) and a's values stay within int8 whatever its dtype
+    alim = 128 if wide_m else lim[da]
+    ma = (1 << 23) + 5 if wide_m else 3000
+    mb = -(((1 << 30) - (1 << 21)) // lim[db])
+    s = 24 if do == "i8" else 16
+    for n, off in ((16 * 4099 + 11, 0), (4096, 0), (999, 1), (15, 0)):
+        a, b = rng.integers(-alim, alim, n), rng.integers(-lim[db], lim[db], n)
+        want = sem.add_requant(a, b, ma, mb, s, do)
+        A = dev.alloc((n + 16) * rt.ITEMSIZE[da])
+        B = dev.alloc((n + 16) * rt.ITEMSIZE[db])
+        A.upload(a.astype(rt.NP_DTYPE[da]), off * rt.ITEMSIZE[da])
+        B.upload(b.astype(rt.NP_DTYPE[db]), off * rt.ITEMSIZE[db])
+        out = dev.alloc((n + 16) * rt.ITEMSIZE[do])
+        dev.add_requant(A.ptr + off * rt.ITEMSIZE[da], da, B.ptr + off * rt.ITEMSIZE[db], db, ma, mb, s, n,
+                        out.ptr + off * rt.ITEMSIZE[do], do, rt.OP_UNCHECKED)
+        dev.sync()
+        got = out.download((n,), rt.NP_DTYPE[do], offset=off * rt.ITEMSIZE[do]).astype(np.int64)
+        assert np.array_equal(got, want), (n, off, int((got != want).sum()))
+
+
+def test_add_requant_checked_vector_flags_overflow(dev):
+    """Checked add over aligned operands (the 16-element kernel): an int32 overflow in one element of the middle of
+    the array raises OverflowError at the next sync, as the interpreter raises for the same op."""
+    n = 16 * 1000
+    a, b = np.zeros(n, int), np.zeros(n, int)
+    a[8007] = 100                                         # 100 * 2^25 leaves int32
+    out = dev.alloc(n)
+    dev.add_requant(up(dev, a, "i8"), "i8", up(dev, b, "i8"), "i8", 1 << 25, 1, 0, n, out, "i8")
+    with pytest.raises(OverflowError):
+        dev.sync()
+    dev.sync()
+
+
+@pytest.mark.parametrize("mult", [300, (1 << 23) + 3])
+def test_lut_and_lut_mul_unchecked_and_unaligned(dev, mult):
+    """lut over 16-byte chunks and its tail, and lut_mul with ANVIL_OP_UNCHECKED (24-bit and 32-bit multiply), on
+    aligned operands and on operands offset by 3 bytes (one-element kernel), against the oracle."""
+    rng = np.random.default_rng([24, mult])
+    # with a 32-bit multiplier the table's entries stay in [-1, 1], so table * y * mult + rnd fits int32
+    t = rng.integers(-128, 128, 256) if mult < (1 << 23) else rng.integers(-1, 2, 256)
+    s = 12 if mult < (1 << 23) else 30
+    for n, off in ((16 * 7001 + 5, 0), (5003, 3)):
+        x, y = rng.integers(-128, 128, n), rng.integers(-128, 128, n)
+        X, Y, O = dev.alloc(n + 16), dev.alloc(n + 16), dev.alloc(n + 16)
+        X.upload(x.astype(np.int8), off)
+        Y.upload(y.astype(np.int8), off)
+        T = up(dev, t, "i8")
+        dev.lut_i8(X.ptr + off, T, n, O.ptr + off)
+        dev.sync()
+        assert np.array_equal(O.download((n,), np.int8, offset=off).astype(np.int64), sem.lut_i8(x, t))
+        dev.lut_mul(X.ptr + off, Y.ptr + off, T, mult, s, n, O.ptr + off, rt.OP_UNCHECKED)
+        dev.sync()
+        assert np.array_equal(O.download((n,), np.int8, offset=off).astype(np.int64),
+                              sem.swiglu_lut(x, y, t, mult, s))
+
+
 @pytest.mark.parametrize("dt", ["i8", "i16", "i32"])
 def test_copy_strided(dev, dt):
     rng = np.random.default_rng(13)
@@ -313,6 +378,16 @@ def test_quantize_input(dev, f64):
     dev.quantize(xd, f64, scale, x.size, out, "i8")
     dev.sync()
     assert np.array_equal(out.download((x.size,), np.int8).astype(np.int64), want)
+    # i16 results, and an input offset off the 16-byte grid (one-element kernel throughout)
+    want16 = np.clip(np.rint(np.asarray(x, dtype=np.float64) / (scale / 300)), -32768, 32767).astype(np.int64)
+    out16 = dev.alloc(2 * x.size)
+    dev.quantize(xd, f64, scale / 300, x.size, out16, "i16")
+    dev.sync()
+    assert np.array_equal(out16.download((x.size,), np.int16).astype(np.int64), want16)
+    isz = x.itemsize
+    dev.quantize(xd.ptr + isz, f64, scale, x.size - 1, out.ptr + 1, "i8")
+    dev.sync()
+    assert np.array_equal(out.download((x.size - 1,), np.int8, offset=1).astype(np.int64), want[1:])
 
 
 @pytest.mark.parametrize("f64", [False, True])
@@ -426,6 +501,39 @@ def test_gemm_with_fused_residual_add(dev, M, K, N, store_y, ma, mb, s2):
     assert np.array_equal(d.download((M, N), np.int8).astype(np.int64), want)
     if store_y:
         assert np.array_equal(c.download((M, N), np.int8).astype(np.int64), y)
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 768, 768), (300, 64, 200), (33, 48, 72), (1024, 256, 384), (4096 + 37, 32, 32),
+                                   (32768, 768, 3072)])
+@pytest.mark.parametrize("store_y", [True, False])
+def test_gemm_with_fused_i16_residual_add(dev, M, K, N, store_y):
+    """anvil_gemm_i8_add_ex on the wide residual stream (ADR-004): y = qlinear(a, w) as int16, D = add_requant(R, y)
+    with R and D int16, in one launch, bit-exact with the two ops. Interior tiles, ragged edges (N not a multiple of
+    8 takes the per-element epilogue), rows of 32 entries (the frozen v2 model's width) and a wide product that the
+    persistent kernels would otherwise take."""
+    rng = np.random.default_rng([32, M, K, N, int(store_y)])
+    a, w = rng.integers(-128, 128, (M, K), dtype=np.int8), rng.integers(-128, 128, (K, N), dtype=np.int8)
+    r = rng.integers(-32768, 32768, (M, N), dtype=np.int16)
+    # the oracle on every row of the small shapes, on the first and last 256 rows and 512 others of the large one
+    rows = (np.arange(M) if M * N <= 1 << 22 else
+            np.unique(np.concatenate([np.arange(256), np.arange(M - 256, M), rng.integers(0, M, 512)])))
+    a64, w64 = a.astype(np.int64), w.astype(np.int64)
+    acc = sem.matmul_i8(a64[rows], w64, fast=True)
+    (m,), s = Q.choose_shift([20000 / (1.5 * max(1, int(np.abs(acc).max())))], [128 * int(np.abs(w64).sum(axis=0).max())])
+    ma, mb, s2 = 16000, -15000, 15
+    y = sem.qmatmul(a64[rows], w64, m, s, None, "i16", fast=True)
+    want = sem.add_requant(r[rows].astype(np.int64), y, ma, mb, s2, "i16")
+    c = dev.alloc(2 * M * N) if store_y else None
+    d = dev.alloc(2 * M * N)
+    flags = rt.GEMM_UNCHECKED | (rt.GEMM_MUL24 if K * 128 * 128 < (1 << 23) and m < (1 << 23) else 0)  # static bound
+    dev.gemm_i8_add(up(dev, a, "i8"), up(dev, np.ascontiguousarray(w.T), "i8"), c, 1, 1, M, N, K,
+                    [0, 0, K, 0, 0, K, 0, 0, N], m, s, None, up(dev, r, "i16"), ma, mb, s2, d, [0, 0, N, 0, 0, N],
+                    flags, "i16")
+    dev.sync()
+    got = d.download((M, N), np.int16)[rows].astype(np.int64)
+    assert np.array_equal(got, want), np.argwhere(got != want)[:5]
+    if store_y:
+        assert np.array_equal(c.download((M, N), np.int16)[rows].astype(np.int64), y)
 
 
 @pytest.mark.parametrize("M,N,K,dtype,lut,add", [(32768, 3072, 768, "i8", True, False),
