@@ -1,5 +1,6 @@
 // Elementwise graph ops (add_requant, lut, lut_mul), the strided copy that materialises a layout view, and
 // input quantization. All are HBM-bound grid-stride loops; LUTs are staged in LDS once per workgroup.
+#include <algorithm>
 #include <cmath>
 
 #include "common.h"
@@ -323,8 +324,9 @@ static void launch_add_typed(anvil_ctx* ctx, const TA* a, const TB* b, int ma, i
   launch_add_scalar(ctx, a, b, ma, mb, s, n16 * 16, n, out);
 }
 
-// embed_quantize four columns a lane: float4 reads of the token's and the position's rows (C a multiple of 4), and
-// one 4-byte (i8) or 8-byte (i16) store; each element as in embed_quantize_kernel
+// embed_quantize four columns a lane: one wave a row (a workgroup takes four rows, then strides by the grid), its
+// lanes over the row's C / 4 float4 columns of the token's and the position's rows, so no lane divides by C; one
+// 4-byte (i8) or 8-byte (i16) store. Each element as in embed_quantize_kernel.
 template <typename TO>
 __global__ __launch_bounds__(E_THREADS) void embed_quantize_vec4(const int64_t* __restrict__ ids,
                                                                  const float* __restrict__ wte,
@@ -332,32 +334,35 @@ __global__ __launch_bounds__(E_THREADS) void embed_quantize_vec4(const int64_t* 
                                                                  int T, int C, int vocab, double scale,
                                                                  TO* __restrict__ out, int lo, int hi,
                                                                  unsigned* flags) {
-  const int c4 = C >> 2;
-  const long long n4 = rows * c4;
-  for (long long i = (long long)blockIdx.x * E_THREADS + threadIdx.x; i < n4; i += (long long)gridDim.x * E_THREADS) {
-    const long long r = i / c4;
-    const int c = (int)(i - r * c4) * 4;
+  const int c4 = C >> 2, lane = threadIdx.x & 63;
+  const long long step = (long long)gridDim.x * (E_THREADS / 64);
+  for (long long r = (long long)blockIdx.x * (E_THREADS / 64) + (threadIdx.x >> 6); r < rows; r += step) {
     const long long id = ids[r];
-    int o[4] = {0, 0, 0, 0};
-    if (id < 0 || id >= vocab) {
-      raise_flag(flags, FLAG_RANGE);
-    } else {
-      const float4 w = *reinterpret_cast<const float4*>(wte + id * C + c);
-      const float4 p = *reinterpret_cast<const float4*>(wpe + (r % T) * C + c);
-      const double xs[4] = {(double)w.x + (double)p.x, (double)w.y + (double)p.y, (double)w.z + (double)p.z,
-                            (double)w.w + (double)p.w};
+    const bool ok = id >= 0 && id < vocab;
+    if (!ok && lane == 0) raise_flag(flags, FLAG_RANGE);
+    const float* te = wte + (ok ? id : 0) * C;
+    const float* pe = wpe + (long long)(int)(r % T) * C;
+    for (int j = lane; j < c4; j += 64) {
+      int o[4] = {0, 0, 0, 0};
+      if (ok) {
+        const float4 w = reinterpret_cast<const float4*>(te)[j];
+        const float4 p = reinterpret_cast<const float4*>(pe)[j];
+        const double xs[4] = {(double)w.x + (double)p.x, (double)w.y + (double)p.y, (double)w.z + (double)p.z,
+                              (double)w.w + (double)p.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        double v = rint(xs[e] / scale);
-        v = v < lo ? lo : (v > hi ? hi : v);
-        o[e] = (int)v;
+        for (int e = 0; e < 4; ++e) {
+          double v = rint(xs[e] / scale);
+          v = v < lo ? lo : (v > hi ? hi : v);
+          o[e] = (int)v;
+        }
       }
-    }
-    if constexpr (sizeof(TO) == 1) {
-      reinterpret_cast<unsigned*>(out)[i] = pack4(o[0], o[1], o[2], o[3]);
-    } else {
-      reinterpret_cast<uint2*>(out)[i] = uint2{__builtin_amdgcn_perm((unsigned)o[1], (unsigned)o[0], 0x05040100u),
-                                               __builtin_amdgcn_perm((unsigned)o[3], (unsigned)o[2], 0x05040100u)};
+      const long long i = r * c4 + j;
+      if constexpr (sizeof(TO) == 1) {
+        reinterpret_cast<unsigned*>(out)[i] = pack4(o[0], o[1], o[2], o[3]);
+      } else {
+        reinterpret_cast<uint2*>(out)[i] = uint2{__builtin_amdgcn_perm((unsigned)o[1], (unsigned)o[0], 0x05040100u),
+                                                 __builtin_amdgcn_perm((unsigned)o[3], (unsigned)o[2], 0x05040100u)};
+      }
     }
   }
 }
@@ -563,12 +568,13 @@ int anvil_embed_quantize(anvil_ctx* ctx, const int64_t* ids, int64_t rows, int T
   const long long n = rows * C;
   const int lo = dtype_lo(out_dtype), hi = dtype_hi(out_dtype);
   if (C % 4 == 0 && al16(wte) && al16(wpe) && ((uintptr_t)out & (out_dtype == ANVIL_I8 ? 3 : 7)) == 0) {
+    const dim3 gr((unsigned)std::min<long long>((rows + 3) / 4, 65536)), bl(E_THREADS);   // four rows a workgroup
     if (out_dtype == ANVIL_I8)
-      ANVIL_LAUNCH(embed_quantize_vec4<int8_t>, dim3(grid_for(n / 4)), dim3(E_THREADS), 0, ctx->stream, ids, wte, wpe,
-                   (long long)rows, T, C, vocab, scale, (int8_t*)out, lo, hi, ctx->flags);
+      ANVIL_LAUNCH(embed_quantize_vec4<int8_t>, gr, bl, 0, ctx->stream, ids, wte, wpe, (long long)rows, T, C, vocab,
+                   scale, (int8_t*)out, lo, hi, ctx->flags);
     else
-      ANVIL_LAUNCH(embed_quantize_vec4<int16_t>, dim3(grid_for(n / 4)), dim3(E_THREADS), 0, ctx->stream, ids, wte,
-                   wpe, (long long)rows, T, C, vocab, scale, (int16_t*)out, lo, hi, ctx->flags);
+      ANVIL_LAUNCH(embed_quantize_vec4<int16_t>, gr, bl, 0, ctx->stream, ids, wte, wpe, (long long)rows, T, C, vocab,
+                   scale, (int16_t*)out, lo, hi, ctx->flags);
     ANVIL_LAUNCHED();
     return ANVIL_OK;
   }

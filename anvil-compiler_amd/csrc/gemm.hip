@@ -485,7 +485,8 @@ __device__ void splitk_finish(const GemmArgs& g, const v16i (&acc)[TN][TM], cons
 // KFULL: K (of the product, or of each split-K chunk) is a whole number of 64-byte blocks, so no chunk of a stage
 // below K needs the per-lane K bound: a load's offset is its lane's fixed offset plus the stage's block offset (one
 // add). A stage at or past K is issued only to keep each stage's load count fixed and is never read: its offsets
-// reach the next rows' bytes inside the buffer resource, or zeros past it.
+// reach the next rows' bytes inside the buffer resource, or zeros past it. With three stages KFULL also means
+// whole rotations (K a multiple of 192), which the launches check.
 template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool SPLIT = false, bool KFULL = false>
 __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int bz) {
   constexpr int BK = 64, CPR = BK / 16;
@@ -624,7 +625,15 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
   stage_barrier();
   load_frags(0, L0, 0);
   int kt = 0;
-  if (NS == 3) {
+  if (NS == 3 && KFULL) {
+    // KFULL launches have nk % 3 == 0: whole rotations and no tail steps, so the accumulators reach the epilogue from
+    // one place (tail steps leave several, and the compiler then copies every accumulator where they join)
+    for (; kt < nk; kt += 3) {
+      step(kt, L0, L2, L1);
+      step(kt + 1, L1, L0, L2);
+      step(kt + 2, L2, L1, L0);
+    }
+  } else if (NS == 3) {
     for (; kt + 3 <= nk; kt += 3) {
       step(kt, L0, L2, L1);
       step(kt + 1, L1, L0, L2);
@@ -1158,14 +1167,15 @@ static void launch_persist(GemmArgs& g, int osz, int batch, int num_cu, hipStrea
     ANVIL_LAUNCH((gemm_i8_persist<BM, BN, BK, NS, NW, WGN, 2, MUL24, false>), dim3(nwg), dim3(NW * 64), 0, s, g);
 }
 
-// KF: the shapes the planner takes (256 x 128 and 128 x 128, three stages) have a KFULL form, used when K % 64 == 0;
-// the benchmarking-override shapes keep the per-lane K bound
+// KF: the shapes the planner takes (256 x 128 and 128 x 128, three stages) have a KFULL form, used when K is a whole
+// number of stage rotations (K % 192 == 0) and not truncated per tile (causal mode 2); the benchmarking-override
+// shapes keep the per-lane K bound
 template <int BM, int BN, int WGM, int NS, bool MUL24, bool KF = false>
 static void launch_fast(GemmArgs& g, int osz, int batch, hipStream_t s) {
   g.tiles_m = (g.M + BM - 1) / BM;
   g.tiles_n = (g.N + BN - 1) / BN;
   dim3 grid(g.tiles_m * g.tiles_n, batch);
-  const bool kfull = KF && g.K % 64 == 0;
+  const bool kfull = KF && g.K % (64 * NS) == 0 && g.causal != 2;
   if (osz == 1 && kfull)
     ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 1, MUL24, KF>), grid, dim3(G_THREADS), 0, s, g);
   else if (osz == 1)
@@ -1192,7 +1202,7 @@ static bool launch_fast_group(GemmArgs* gs, const int* batch, int n, int osz, hi
   a.first[n] = (int)w;
   a.n = n;
   bool kfull = true;
-  for (int i = 0; i < n; ++i) kfull = kfull && gs[i].K % 64 == 0;
+  for (int i = 0; i < n; ++i) kfull = kfull && gs[i].K % (64 * NS) == 0 && gs[i].causal != 2;
   if (osz == 1 && kfull)
     ANVIL_LAUNCH((gemm_i8_fast_group<BM, BN, WGM, NS, 1, MUL24, true>), dim3((unsigned)w), dim3(G_THREADS), 0, s, a);
   else if (osz == 1)
@@ -1214,7 +1224,7 @@ static void launch_splitk(GemmArgs& g, int osz, hipStream_t s) {
   g.tiles_n = (g.N + 127) / 128;
   dim3 grid(g.tiles_m * g.tiles_n, g.splits);
   const dim3 rgrid(g.tiles_m * g.tiles_n * 8);
-  const bool kfull = g.K % 64 == 0;                       // so every chunk (a multiple of 64 bytes) is whole
+  const bool kfull = g.K % 192 == 0 && g.kchunk % 192 == 0;   // every chunk whole rotations of three stages
   if (osz == 1) {
     if (kfull)
       ANVIL_LAUNCH((gemm_i8_splitk<128, 128, 2, 3, 1, MUL24, true>), grid, dim3(G_THREADS), 0, s, g);

@@ -397,7 +397,9 @@ def bench_eltwise(args):
         ("lut_mul", 3 * n4, dev.lut_mul, (x4, y4, table, 300, 12, n4, out4, U)),
         ("quantize_f32_i8", 5 * n1, dev.quantize, (xf32, False, 0.025, n1, out1, "i8")),
         ("quantize_f64_i8", 9 * n1, dev.quantize, (xf64, True, 0.025, n1, out1, "i8")),
-        ("embed_quantize_i8", 9 * n1 + 8 * R, dev.embed_quantize, (ids, R, T, C, wte, vocab, wpe, 0.01, out1, "i8")),
+        # the tables count once (4.7 MB); the kernel gathers a row of each per token from L2
+        ("embed_quantize_i8", n1 + 8 * R + 4 * (vocab + T) * C, dev.embed_quantize,
+         (ids, R, T, C, wte, vocab, wpe, 0.01, out1, "i8")),
     ]
     stream = stream_copy(dev)
     reps = max(1, min(args.steps, SLOTS))

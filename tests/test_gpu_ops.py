@@ -656,10 +656,13 @@ def test_gemm_group_matches_separate_launches(dev, case, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["i8", "i16"])
-def test_embed_quantize(dev, dtype):
-    """anvil_embed_quantize: clamp(rint((wte[id] + wpe[t]) / scale)) in float64, as the host computes it."""
-    rng = np.random.default_rng([51, dtype == "i8"])
-    vocab, T, C, B = 300, 40, 48, 3
+@pytest.mark.parametrize("C", [48, 772, 30])
+def test_embed_quantize(dev, dtype, C):
+    """anvil_embed_quantize: clamp(rint((wte[id] + wpe[t]) / scale)) in float64, as the host computes it. C a multiple
+    of 4 takes the four-columns-a-lane kernel (772: more float4 columns than a wave has lanes), C = 30 the
+    one-element kernel."""
+    rng = np.random.default_rng([51, dtype == "i8", C])
+    vocab, T, B = 300, 40, 3
     wte = rng.normal(0, 0.02, (vocab, C)).astype(np.float32)
     wpe = rng.normal(0, 0.02, (T + 5, C)).astype(np.float32)
     ids = rng.integers(0, vocab, (B, T))
