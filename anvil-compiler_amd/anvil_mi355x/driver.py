@@ -109,6 +109,9 @@ class _Plan:
         self.stage: dict = {}          # device staging buffers of float inputs and token ids
         self.host_stage: dict = {}     # page-locked host buffers the read-back downloads into, by device buffer
         self.graph = None              # the steps captured as one HIP graph (run(..., graph=True))
+        self.eager_ms: list = []       # device ms of the plan's first eager runs (run's default launch choice)
+        self.graph_ms = None           # device ms of its first replay of the captured graph
+        self.replay = None             # run's choice once measured: True = replay the graph, False = launch eagerly
         self.kb_values: set = set()    # values stored K-blocked (read only by GEMMs)
 
     def buf(self, nbytes, name=""):
@@ -973,12 +976,35 @@ class CompiledModel:
                 narrow[s] = n if whole else n[0]
         return out
 
+    AUTO_EAGER_RUNS = 2                # eager runs a plan times before its graph is captured and timed
+
+    def _auto_graph(self, plan) -> bool:
+        """run's default launch: a plan's first AUTO_EAGER_RUNS runs launch eagerly, the next captures the steps
+        as a HIP graph (after running them once more), the one after replays it; from then on the faster of the
+        two, compared on the device time of the forward (launch gaps included)."""
+        if plan.replay is not None:
+            return plan.replay
+        return len(plan.eager_ms) >= self.AUTO_EAGER_RUNS
+
+    def _note_auto(self, plan, graph, captured, ms):
+        """Record one auto run's device time; captured: this run captured the graph (it also ran the steps eagerly
+        first, so its time is no replay time)."""
+        if plan.replay is not None or captured:
+            return
+        if not graph:
+            plan.eager_ms.append(ms)
+        else:
+            plan.graph_ms = ms
+            plan.replay = ms < min(plan.eager_ms)
+
     def run(self, x, backend: str = "mi355x", *, quantized=False, keep="outputs", batch=False, profile=False,
-            tokens=False, graph=False, **run_kw) -> RunOutput:
+            tokens=False, graph=None, **run_kw) -> RunOutput:
         """Quantize x (unless quantized=True), run the graph on the GPU, read back (reference driver.py:305-322).
         Float inputs are quantized on the device. tokens=True: x holds token ids of a model compiled with embedding
         tables, gathered and quantized on the device. graph=True runs the forward as one HIP graph of the plan
-        (captured on first use): the same kernels with no launch gaps between them, for repeated small runs."""
+        (captured on first use): the same kernels with no launch gaps between them; graph=False launches every kernel
+        from the host; graph=None (the default) measures both on the plan's first runs and keeps the faster
+        (small batches gain most: their kernels are short and the launch gaps between them a large share)."""
         if backend not in BACKENDS:
             raise ValueError(f"unknown backend {backend!r}: {', '.join(BACKENDS)}")
         if run_kw:
@@ -994,18 +1020,25 @@ class CompiledModel:
                 self.upload_tokens(plan, ids)
             else:
                 self.upload_inputs(plan, ints_in)
+            auto = graph is None and not profile
+            if auto:
+                graph = self._auto_graph(plan)
+            captured = bool(graph) and plan.graph is None
             self.dev.record(2)
             times = self.launch(plan, profile, graph)
             self.dev.record(3)
             self.dev.sync()
             total_ms = self.dev.elapsed_ms(2, 3)
+            if auto:
+                self._note_auto(plan, graph, captured, total_ms)
             narrow = {}
             ints = self.read(plan, syms, nb, batch, narrow)
             # from the stored dtype (1-2 bytes an element), before another run reuses the plan's host buffers
             outs = [self.dequantize(s, narrow[s]) for s in self.outputs]
         cycles = {label: (times.get(label) if profile else None) for label, _, _ in plan.steps}
         consts = frozenset(op.sym_str for op in self.ops if isinstance(op, g.ConstOp))
-        result = {"device_ms": total_ms, "batch": nb, "kernels": len(plan.steps), "footprint": plan.footprint}
+        result = {"device_ms": total_ms, "batch": nb, "kernels": len(plan.steps), "footprint": plan.footprint,
+                  "hip_graph": bool(graph) and not profile}
         return RunOutput(outs[0], outs, ints, cycles, result, None, consts, self)
 
     def summary(self) -> str:

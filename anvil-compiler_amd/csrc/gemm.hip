@@ -1598,8 +1598,8 @@ static int gemm_entry(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C
   return ANVIL_OK;
 }
 
-// Independent products in one launch when every one of them takes the 256 x 128 one-tile-per-workgroup kernel with
-// the same result type and requant multiply, else one launch each (in order).
+// Independent products in one launch when every one of them takes the same one-tile-per-workgroup kernel (256 x 128
+// or 128 x 128) with the same result type and requant multiply, else one launch each (in order).
 extern "C" int anvil_gemm_i8_group(anvil_ctx* ctx, const anvil_gemm_desc* d, int count) {
   if (!d) return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_group: null pointer");
   if (count < 1 || count > GEMM_GROUP_MAX)
@@ -1613,16 +1613,27 @@ extern "C" int anvil_gemm_i8_group(anvil_ctx* ctx, const anvil_gemm_desc* d, int
     if (int r = gemm_prepare(ctx, d[i].A, d[i].Bt, d[i].C, d[i].batch0, d[i].batch1, d[i].M, d[i].N, d[i].K,
                              d[i].strides, d[i].mult, d[i].shift, d[i].lut, d[i].out_dtype, d[i].flags, nullptr, p[i]))
       return r;
+  // one launch when every member takes the same one-tile-per-workgroup kernel: 256 x 128 tiles, or 128 x 128 tiles
+  // for smaller products (config 3's q, k and v, 256 tiles each), none of them splitting K
+  int shape = 0;
   bool one = count > 1;
-  for (int i = 0; i < count && one; ++i)
-    one = p[i].fast && p[i].osz == p[0].osz && p[i].mul24 == p[0].mul24 &&
-          fast_choice(p[i].g, p[i].batch, ctx->gemm_cfg, ctx->num_cu) == 16;
+  for (int i = 0; i < count && one; ++i) {
+    const int c = fast_choice(p[i].g, p[i].batch, ctx->gemm_cfg, ctx->num_cu);
+    int splits = 0, kchunk = 0;
+    one = p[i].fast && p[i].osz == p[0].osz && p[i].mul24 == p[0].mul24 && (c == 16 || c == 13) &&
+          (i == 0 || c == shape) && !splitk_plan(p[i].g, p[i].batch, ctx->num_cu, p[i].force_split, splits, kchunk);
+    shape = c;
+  }
   if (one) {
     GemmArgs gs[GEMM_GROUP_MAX];
     int batch[GEMM_GROUP_MAX];
     for (int i = 0; i < count; ++i) gs[i] = p[i].g, batch[i] = p[i].batch;
-    one = p[0].mul24 ? launch_fast_group<256, 128, 2, 3, true>(gs, batch, count, p[0].osz, ctx->stream)
-                     : launch_fast_group<256, 128, 2, 3, false>(gs, batch, count, p[0].osz, ctx->stream);
+    if (shape == 16)
+      one = p[0].mul24 ? launch_fast_group<256, 128, 2, 3, true>(gs, batch, count, p[0].osz, ctx->stream)
+                       : launch_fast_group<256, 128, 2, 3, false>(gs, batch, count, p[0].osz, ctx->stream);
+    else
+      one = p[0].mul24 ? launch_fast_group<128, 128, 2, 3, true>(gs, batch, count, p[0].osz, ctx->stream)
+                       : launch_fast_group<128, 128, 2, 3, false>(gs, batch, count, p[0].osz, ctx->stream);
   }
   if (!one)
     for (int i = 0; i < count; ++i)

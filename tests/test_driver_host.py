@@ -477,10 +477,34 @@ def test_graph_runs_replay_the_captured_steps(fake):
         res = cm.run(x, "mi355x", batch=True, graph=True)
         want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
         assert np.array_equal(res.ints["out"], want.values["out"])
-        eager = cm.run(x, "mi355x", batch=True)
+        eager = cm.run(x, "mi355x", batch=True, graph=False)
         assert np.array_equal(eager.ints["out"], res.ints["out"])
     plan = cm.plan(2)
     assert fake.captures == 1 and plan.graph.launches == 3
+
+
+@pytest.mark.parametrize("graph_faster", [True, False])
+def test_default_run_keeps_the_faster_launch(fake, monkeypatch, graph_faster):
+    """run() without graph=: a plan's first two runs launch eagerly (timed on the device), the third captures the
+    steps as a HIP graph, the fourth replays it (timed); later runs take whichever was faster. Every run's result
+    equals the oracle's."""
+    spec = models.BlockSpec(n_embd=64, n_head=2, seq=32, calib_batches=2, calib_batch=2)
+    built = models.build(spec, 15, stored=False)
+    cm = anvil_mi355x.compile(built)
+    # device time of a run: 1.0 ms eager; a replay 0.5 ms or 2.0 ms
+    monkeypatch.setattr(fake, "elapsed_ms", lambda a, b: (0.5 if graph_faster else 2.0) if fake._graph_run else 1.0)
+    launches = []
+    for j in range(6):
+        plan = cm.plan(2)
+        fake._graph_run = plan.graph is not None
+        x = models.eval_inputs(built.spec, 2, 15, j)
+        res = cm.run(x, "mi355x", batch=True)
+        launches.append(res.result["hip_graph"])
+        want = interp.run(built.module, {"x": cm.quantize_input(x)}, built.consts, batch=True)
+        assert np.array_equal(res.ints["out"], want.values["out"])
+    assert launches[:4] == [False, False, True, True]
+    assert launches[4:] == [graph_faster] * 2
+    assert cm.plan(2).replay is graph_faster and fake.captures == 1
 
 
 @pytest.mark.parametrize("n", [1, 3, 4, 5])
