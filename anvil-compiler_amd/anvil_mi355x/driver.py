@@ -390,10 +390,11 @@ class CompiledModel:
 
     def _attention_chains(self, keep) -> dict:
         """{P.V matmul: (scores matmul, softmax)} for every chain qmatmul -> softmax_lut -> qmatmul whose scores and
-        probabilities are read by nothing else and not returned, in a proven graph with int8 values throughout, a
-        square (T x T) score matrix with T a multiple of 32 up to 1024 and one head dim of 16, 32, 64 or 128: the
-        chains anvil_attention_i8 evaluates without materialising scores or p."""
-        if keep != "outputs" or not self.proven:
+        probabilities are read by nothing else, in a proven graph with int8 values throughout, a square (T x T)
+        score matrix with T a multiple of 32 up to 1024 and one head dim of 16, 32, 64 or 128: the chains
+        anvil_attention_i8 evaluates without materialising scores or p, or, when the run returns them (keep="all",
+        or graph outputs), anvil_attention_i8_keep, which also stores them (_kept_chain)."""
+        if not self.proven:
             return {}
         found = {}
         for o_op in self.ops:
@@ -406,8 +407,7 @@ class CompiledModel:
             if (not isinstance(s_op, g.QMatmulOp) or s_op.lut is not None or g.qt(s_op.result).dtype != "i8"
                     or not self._softmax_lut_ok(sm)):
                 continue
-            if any(v in self.output_values or v in self.is_const or self.users.get(v, []) != [u]
-                   for v, u in ((s_op.result, sm), (sm.result, o_op))):
+            if any(v in self.is_const or self.users.get(v, []) != [u] for v, u in ((s_op.result, sm), (sm.result, o_op))):
                 continue
             sd, od = g.qt(s_op.result).dims, g.qt(o_op.result).dims
             T, D = sd[-1], g.qt(s_op.a).dims[-1]
@@ -416,9 +416,15 @@ class CompiledModel:
             found[o_op] = (s_op, sm)
         return found
 
+    def _kept_chain(self, s_op, sm, keep) -> bool:
+        """Whether a fused chain's scores and probabilities are returned, and so stored by the kernel."""
+        return keep == "all" or s_op.result in self.output_values or sm.result in self.output_values
+
     def _plan_attention(self, P, o_op, s_op, sm, views, nb, label, dense, step, keep):
-        """One anvil_attention_i8 launch for a fused chain, or the three ops when the operand views do not fit it."""
+        """One anvil_attention_i8 launch for a fused chain (anvil_attention_i8_keep when the run returns its scores
+        and probabilities), or the three ops when the operand views do not fit it."""
         n = len(g.qt(o_op.result).dims) + 1
+        kept = self._kept_chain(s_op, sm, keep)
         qa = views[s_op.a]
         kb = views[s_op.b].permute(_swap_last2(n))           # key rows (..., T, d)
         vb = views[o_op.b].permute(_swap_last2(n))           # V^T rows (..., d, T)
@@ -433,6 +439,10 @@ class CompiledModel:
         else:
             out = self._alloc_result(P, o_op, (nb, *g.qt(o_op.result).dims), label)
         vs = [qa, kb, vb, out]
+        if kept:
+            sv = self._alloc_result(P, s_op, (nb, *g.qt(s_op.result).dims), label + ".scores")
+            pv = P.dense((nb, *g.qt(sm.result).dims), "i8", label + ".p")
+            vs += [sv, pv]
         lead = out.dims[:-2]
         idx = [i for i, d in enumerate(lead) if d != 1]
         fits = (all(len(v.dims) == n and v.dims[:-2] == lead and v.strides[-1] == 1 for v in vs)
@@ -446,10 +456,13 @@ class CompiledModel:
             T, D = qa.dims[-2], qa.dims[-1]
             # K and V^T go through 32-bit buffer offsets over one head: rows at least D (keys) / T (V^T) apart; O's
             # 32-row tiles through 32-bit offsets too
-            fits = (all(st % 16 == 0 for st in strides[:9]) and all(st % 4 == 0 for st in strides[9:])
+            fits = (all(st % 16 == 0 for st in strides[:9]) and all(st % 4 == 0 for st in strides[9:12])
                     and all(o % 16 == 0 for o in offs[:3]) and offs[3] % 4 == 0
                     and strides[5] >= D and strides[8] >= T and T * strides[5] < 1 << 31 and D * strides[8] < 1 << 31
                     and strides[11] >= D and 32 * strides[11] < 1 << 31)
+            if kept:                     # S and P: 16-byte stores into 32-row tiles through 32-bit offsets
+                fits = (fits and all(st % 16 == 0 for st in strides[12:]) and all(o % 16 == 0 for o in offs[4:])
+                        and all(T <= st and 32 * st < 1 << 31 for st in (strides[14], strides[17])))
         if not fits:
             sv = self._plan_matmul(P, s_op, views, (nb, *g.qt(s_op.result).dims), label + ".scores", dense, step,
                                    keep)
@@ -463,8 +476,13 @@ class CompiledModel:
         flags = rt.OP_UNCHECKED
         if self.acc_bounds.get(s_op.result, 1 << 31) < (1 << 23) and abs(int(s_op.M)) < (1 << 23):
             flags |= rt.ATTN_S24
-        step(label, _call_attention, self.dev, qa, kb, vb, out, b0, b1, T, D, strides, s_op, sm, o_op,
-             views[sm.lut], flags)
+        if kept:
+            views[s_op.result], views[sm.result] = sv, pv
+            step(label, _call_attention_keep, self.dev, qa, kb, vb, out, sv, pv, b0, b1, T, D, strides, s_op, sm,
+                 o_op, views[sm.lut], flags)
+        else:
+            step(label, _call_attention, self.dev, qa, kb, vb, out, b0, b1, T, D, strides, s_op, sm, o_op,
+                 views[sm.lut], flags)
         return out
 
     def _alloc_result(self, P, op, out_dims, label):
@@ -1100,6 +1118,10 @@ def _work(fn, args):
         _, q, k, v, o, b0, b1, T, D = args[:9]
         nb = b0 * b1
         return "attention", 4 * nb * T * T * D, 4 * nb * T * D + 1024
+    if fn is _call_attention_keep:               # also writes the T x T scores and probabilities
+        _, q, k, v, o, s, p, b0, b1, T, D = args[:11]
+        nb = b0 * b1
+        return "attention", 4 * nb * T * T * D, 4 * nb * T * D + 2 * nb * T * T + 1024
     if fn is _copy_view:
         src = args[1]
         return "copy", 0, 2 * src.size * src.itemsize
@@ -1169,6 +1191,12 @@ def _call_attention(dev, q: View, k: View, v: View, o: View, b0, b1, T, D, strid
                     flags):
     dev.attention_i8(q.ptr, k.ptr, v.ptr, o.ptr, b0, b1, T, D, strides, int(s_op.M), int(s_op.s), lut.ptr,
                      int(sm.one), bool(sm.causal), int(o_op.M), int(o_op.s), flags)
+
+
+def _call_attention_keep(dev, q: View, k: View, v: View, o: View, s: View, p: View, b0, b1, T, D, strides, s_op, sm,
+                         o_op, lut: View, flags):
+    dev.attention_i8_keep(q.ptr, k.ptr, v.ptr, o.ptr, s.ptr, p.ptr, b0, b1, T, D, strides, int(s_op.M), int(s_op.s),
+                          lut.ptr, int(sm.one), bool(sm.causal), int(o_op.M), int(o_op.s), flags)
 
 
 def _call_gemm_add(dev, a: View, bt: View, c, M, N, K, strides, op, lut, r: View, ma, mb, shift2, d: View, rstrides,

@@ -69,6 +69,7 @@ SIGNATURES = {
     "anvil_softmax_lut": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i],
     "anvil_softmax_lut_ex": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i, _i],
     "anvil_attention_i8": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p, _i32, _i, _p, _i32, _i, _i32, _i, _i],
+    "anvil_attention_i8_keep": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p, _i32, _i, _p, _i32, _i, _i32, _i, _i],
     "anvil_add_requant": [_p, _p, _i, _p, _i, _i32, _i32, _i, _i64, _p, _i],
     "anvil_add_requant_ex": [_p, _p, _i, _p, _i, _i32, _i32, _i, _i64, _p, _i, _i],
     "anvil_lut_i8": [_p, _p, _p, _i64, _p],
@@ -345,6 +346,13 @@ class Device:
         self.lib.call("anvil_attention_i8", self.ctx, C.c_void_p(_ptr(Q)), C.c_void_p(_ptr(K)), C.c_void_p(_ptr(Vt)),
                       C.c_void_p(_ptr(O)), b0, b1, T, D, st, int(ms), ss, C.c_void_p(_ptr(lut)), int(one),
                       int(bool(causal)), int(mo), so, int(flags))
+
+    def attention_i8_keep(self, Q, K, Vt, O, S, P, b0, b1, T, D, strides, ms, ss, lut, one, causal, mo, so, flags):
+        """attention_i8 that also stores the scores into S and the probabilities into P (18 strides)."""
+        st = (C.c_int64 * 18)(*[int(s) for s in strides])
+        self.lib.call("anvil_attention_i8_keep", self.ctx, C.c_void_p(_ptr(Q)), C.c_void_p(_ptr(K)),
+                      C.c_void_p(_ptr(Vt)), C.c_void_p(_ptr(O)), C.c_void_p(_ptr(S)), C.c_void_p(_ptr(P)), b0, b1, T, D,
+                      st, int(ms), ss, C.c_void_p(_ptr(lut)), int(one), int(bool(causal)), int(mo), so, int(flags))
 
     def add_requant(self, a, a_dtype, b, b_dtype, ma, mb, shift, n, out, out_dtype, flags=0):
         self.lib.call("anvil_add_requant_ex", self.ctx, C.c_void_p(_ptr(a)), DTYPE_CODE[a_dtype], C.c_void_p(_ptr(b)),

@@ -60,6 +60,12 @@ struct AttnArgs {
   int nqt;             // query tiles of 32 rows per head
   unsigned long long mq, mb;   // n / nqt and n / batch1 as (n m) >> (32 + k): m = ceil(2^(32+k) / d), 2^k >= d
   int kq, kb;
+  // the kept form (anvil_attention_i8_keep): scores and probabilities also stored, (batch, head, T, T) int8 with
+  // strides (sc0, sc1, ldsc) and (pr0, pr1, ldpr); one 32-row tile spans 31 ld + T bytes of each (scbytes, prbytes)
+  int8_t* Sc;
+  int8_t* Pr;
+  long long sc0, sc1, ldsc, pr0, pr1, ldpr;
+  int ldsc32, ldpr32, scbytes, prbytes;
 };
 
 // n / d for a uniform n < 2^32 by one 64-bit multiply-high (scalar ALU): with m = ceil(2^(32+k) / d) and 2^k >= d,
@@ -96,8 +102,15 @@ __device__ __forceinline__ v4i chunk16(const int8_t* row, int chunk) {
   return *reinterpret_cast<const v4i*>(row + chunk * 16);
 }
 
-template <int NTW, int D, bool S24>
-__global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(AttnArgs a) {
+// 16 bytes to a buffer at a 32-bit offset
+__device__ __forceinline__ void store16(v4i v, __amdgpu_buffer_rsrc_t rs, unsigned off) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), rs, off,
+                                         0, 0);
+}
+
+// Six workgroups a CU at D <= 64; the kept form's stores need a few more registers, five.
+template <int NTW, int D, bool S24, bool KEEP>
+__global__ __launch_bounds__(A_THREADS, (D <= 64 ? (KEEP ? 5 : 6) : 1)) void attention_i8(AttnArgs a) {
   constexpr int KS = (D + 31) / 32;         // 32-wide MFMA k-steps over the head dim
   constexpr int CT = (D + 31) / 32;         // 32-wide output column tiles
   constexpr int OROW = CT * 32 + 4;         // partial-O row stride in LDS (ints), padded off the bank period
@@ -136,6 +149,16 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) qf[ks] = chunk16<D>(Qr, 2 * ks + half);
 
+  // The kept form stores each score and probability tile as the lanes hold it: lane l's 16 bytes of a 32-key tile
+  // are keys 16 (l / 32) .. + 15 of row q0 + l % 32 (the key rows entered the score MFMA in bperm order), one
+  // 16-byte store at column 32 nt + 16 (l / 32).
+  const __amdgpu_buffer_rsrc_t srs =            // (unused, and dropped, in the plain form)
+      uniform_rsrc(KEEP ? a.Sc + b0 * a.sc0 + b1 * a.sc1 + (long long)q0 * a.ldsc : nullptr, KEEP ? a.scbytes : 0);
+  const __amdgpu_buffer_rsrc_t prs =
+      uniform_rsrc(KEEP ? a.Pr + b0 * a.pr0 + b1 * a.pr1 + (long long)q0 * a.ldpr : nullptr, KEEP ? a.prbytes : 0);
+  const unsigned sofs = KEEP ? (unsigned)(l32 * a.ldsc32 + 16 * half) : 0u;
+  const unsigned pofs = KEEP ? (unsigned)(l32 * a.ldpr32 + 16 * half) : 0u;
+
   // ---- 1. scores of this wave's tiles (w + 4 i), partial row max
   // The requant clamps before its shift (clamp(x >> s) = clamp'(x) >> s with the bounds scaled by 2^s), so the
   // max runs on the clamped values and each score byte is one shift written into its byte lane.
@@ -151,15 +174,48 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
   const unsigned koff = (unsigned)(bperm(l32) * a.ldk) + 16 * half;
   // Past the wave's last tile the tile part of the offset is 2^31: every lane's offset (below T ldk < 2^31 for a
   // real tile) then lands in [2^31, 2^32), beyond the descriptor, so the tile test stays on the scalar unit.
-  auto kload = [&](int nt, v4i* kf) {
-    const unsigned tile = nt < ntiles ? (unsigned)(nt * 32 * a.ldk) : 0x80000000u;
+  auto kload_below = [&](int nt, int lim, v4i* kf) {     // tile nt if nt < lim, else zeros
+    const unsigned tile = nt < lim ? (unsigned)(nt * 32 * a.ldk) : 0x80000000u;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const unsigned o = D >= 32 ? koff + 32 * ks + tile                    // every lane's chunk inside the head dim
-                                 : (nt < ntiles && 32 * ks + 16 * half < D ? koff + 32 * ks + tile : OOB);
+                                 : (nt < lim && 32 * ks + 16 * half < D ? koff + 32 * ks + tile : OOB);
       kf[ks] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(krs, o, 0, 0));
     }
   };
+  auto kload = [&](int nt, v4i* kf) { kload_below(nt, ntiles, kf); };
+  // The kept form's tiles past the causal diagonal: their scores are stored like any other (the graph's scores are
+  // the whole T x T product) and their probabilities are 0. The wave takes tiles ntiles + w, + 4, ... (at most NTW)
+  // before its own, each pass loading the next K tile once its MFMAs have read the current one and storing after
+  // that load. Passes nest as for the wave's own tiles (below): every pass has one path into it, so its wait covers
+  // its own K tile and leaves the previous pass's two stores in flight.
+  if constexpr (KEEP) {
+    if (a.causal && ntiles + w < a.nqt) {
+      v4i uf[KS];
+      kload_below(ntiles + w, a.nqt, uf);
+      auto upass = [&](auto self, auto ic) __attribute__((always_inline)) -> void {
+        constexpr int i = decltype(ic)::value;
+        const int nt = ntiles + w + 4 * i;
+        v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(uf[ks], qf[ks], acc, 0, 0, 0);
+        if (i + 1 < NTW) kload_below(nt + 4, a.nqt, uf);
+        int x[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          x[r] = med3i(S24 ? __mul24(acc[r], a.ms) + a.rnds : acc[r] * a.ms + a.rnds, a.clo, a.chi);
+        v4i sv;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) sv[g] = (int)sra_pack4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3], a.ss);
+        store16(sv, srs, sofs + 32 * nt);
+        store16(v4i{0, 0, 0, 0}, prs, pofs + 32 * nt);
+        if constexpr (i + 1 < NTW) {
+          if (nt + 4 < a.nqt) self(self, std::integral_constant<int, i + 1>{});
+        }
+      };
+      upass(upass, std::integral_constant<int, 0>{});
+    }
+  }
   // The next K tile loads into kf as soon as this pass's score MFMAs have read it, so its latency overlaps the
   // requant of this tile; one buffer (not two, loaded two tiles ahead) keeps the kernel at 80 registers, six waves a
   // SIMD. The wave's tiles are a prefix of its passes, and pass i + 1 is entered from the end of pass i only
@@ -184,6 +240,12 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
     // the diagonal tile: a key past the row takes the lowest score (clo >> ss), which leaves the row max as it is;
     // the sums subtract its LUT term and the probabilities mask it
     if (a.causal && nt == ntiles - 1) {
+      if constexpr (KEEP) {                           // the kept scores are the unmasked ones
+        v4i sv;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) sv[g] = (int)sra_pack4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3], a.ss);
+        store16(sv, srs, sofs + 32 * nt);
+      }
       const int lim = qrow - nt * 32 - 16 * half;     // key r of this lane is kept iff r <= lim
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] = r <= lim ? x[r] : a.clo;
@@ -195,6 +257,10 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
     tmx_s[i] = (int8_t)(tm >> a.ss);
 #pragma unroll
     for (int g = 0; g < 4; ++g) sc[i][g] = sra_pack4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3], a.ss);
+    if constexpr (KEEP) {
+      if (!(a.causal && nt == ntiles - 1))
+        store16(v4i{(int)sc[i][0], (int)sc[i][1], (int)sc[i][2], (int)sc[i][3]}, srs, sofs + 32 * nt);
+    }
 
     if constexpr (i + 1 < NTW) {
       if (nt + 4 < ntiles) self(self, std::integral_constant<int, i + 1>{});
@@ -329,8 +395,8 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
   auto pass3 = [&](auto self, auto ic) __attribute__((always_inline)) -> void {   // nested passes, as for K
     constexpr int i = decltype(ic)::value;
     const int nt = w + 4 * i;
+    v4i pf = {0, 0, 0, 0};                               // a dead tile's probabilities (kept form)
     if ((live >> i) & 1) {
-    v4i pf;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const unsigned sw = sc[i][g] ^ swz;
@@ -354,6 +420,7 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
     // pass's lookups. Issued at the start of this pass instead (into a second buffer), the kernel ran 10 % slower
     // (115 against 104 us at config 5, with or without a register copy between the buffers).
     if (i + 1 < NTW) vload(nt + 4, vf);
+    if constexpr (KEEP) store16(pf, prs, pofs + 32 * nt);   // after the prefetch: its wait need not cover the store
     if constexpr (i + 1 < NTW) {
       if (nt + 4 < ntiles) self(self, std::integral_constant<int, i + 1>{});
     }
@@ -413,27 +480,27 @@ __global__ __launch_bounds__(A_THREADS, (D <= 64 ? 6 : 1)) void attention_i8(Att
     store(std::false_type{});
 }
 
-template <int NTW, bool S24>
+template <int NTW, bool S24, bool KEEP>
 static void launch_attention(const AttnArgs& a, int D, unsigned grid, hipStream_t s) {
   switch (D) {
-    case 16: ANVIL_LAUNCH((attention_i8<NTW, 16, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
-    case 32: ANVIL_LAUNCH((attention_i8<NTW, 32, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
-    case 64: ANVIL_LAUNCH((attention_i8<NTW, 64, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
-    default: ANVIL_LAUNCH((attention_i8<NTW, 128, S24>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    case 16: ANVIL_LAUNCH((attention_i8<NTW, 16, S24, KEEP>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    case 32: ANVIL_LAUNCH((attention_i8<NTW, 32, S24, KEEP>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    case 64: ANVIL_LAUNCH((attention_i8<NTW, 64, S24, KEEP>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
+    default: ANVIL_LAUNCH((attention_i8<NTW, 128, S24, KEEP>), dim3(grid), dim3(A_THREADS), 0, s, a); break;
   }
 }
 
-template <bool S24>
+template <bool S24, bool KEEP>
 static void launch_attention_nt(const AttnArgs& a, int D, unsigned grid, hipStream_t s) {
   const int ntw = (a.nqt + 3) / 4;                       // key tiles per wave
   if (ntw <= 1)
-    launch_attention<1, S24>(a, D, grid, s);
+    launch_attention<1, S24, KEEP>(a, D, grid, s);
   else if (ntw <= 2)
-    launch_attention<2, S24>(a, D, grid, s);
+    launch_attention<2, S24, KEEP>(a, D, grid, s);
   else if (ntw <= 4)
-    launch_attention<4, S24>(a, D, grid, s);
+    launch_attention<4, S24, KEEP>(a, D, grid, s);
   else
-    launch_attention<8, S24>(a, D, grid, s);
+    launch_attention<8, S24, KEEP>(a, D, grid, s);
 }
 
 }  // namespace anvil
@@ -442,10 +509,13 @@ using namespace anvil;
 
 static bool al(const void* p, int n) { return ((uintptr_t)p % n) == 0; }
 
-extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const int8_t* Vt, int8_t* O,
-                                  int batch0, int batch1, int T, int D, const int64_t* strides, int32_t m_s, int s_s,
-                                  const int32_t* lut, int32_t one, int causal, int32_t m_o, int s_o, int flags) {
-  if (!Q || !K || !Vt || !O || !strides || !lut) return set_error(ANVIL_E_VALUE, "anvil_attention_i8: null pointer");
+// Both entry points: keep = false leaves S, P and strides[12..17] unread.
+static int attention_entry(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const int8_t* Vt, int8_t* O, int8_t* S,
+                           int8_t* P, bool keep, int batch0, int batch1, int T, int D, const int64_t* strides,
+                           int32_t m_s, int s_s, const int32_t* lut, int32_t one, int causal, int32_t m_o, int s_o,
+                           int flags) {
+  if (!Q || !K || !Vt || !O || !strides || !lut || (keep && (!S || !P)))
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: null pointer");
   if (!(flags & ANVIL_OP_UNCHECKED) || (flags & ~(ANVIL_OP_UNCHECKED | ANVIL_ATTN_S24)))
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: flags must hold ANVIL_OP_UNCHECKED (a proven graph)");
   if (batch0 < 1 || batch1 < 1 || T < 32 || T % 32 || T > 1024)
@@ -472,6 +542,16 @@ extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t*
                      (long long)st[5], (long long)st[8]);
   if (st[11] < D || 32 * st[11] >= (1ll << 31))   // a 32-row output tile is stored through 32-bit offsets
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: O row stride %lld out of range", (long long)st[11]);
+  if (keep) {                                      // S and P: 16-byte stores into 32-row tiles, 32-bit offsets
+    for (int i = 12; i < 18; ++i)
+      if (st[i] < 0 || st[i] % 16)
+        return set_error(ANVIL_E_VALUE, "anvil_attention_i8_keep: stride %d (%lld) not a multiple of 16", i,
+                         (long long)st[i]);
+    if (st[14] < T || st[17] < T || 32 * st[14] >= (1ll << 31) || 32 * st[17] >= (1ll << 31))
+      return set_error(ANVIL_E_VALUE, "anvil_attention_i8_keep: S / P row stride %lld / %lld out of range",
+                       (long long)st[14], (long long)st[17]);
+    if (!al(S, 16) || !al(P, 16)) return set_error(ANVIL_E_VALUE, "anvil_attention_i8_keep: S or P not aligned");
+  }
   if (int r = check_ctx(ctx)) return r;
   AttnArgs a;
   a.Q = Q;
@@ -505,11 +585,38 @@ extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t*
   magic(a.nqt, a.mq, a.kq);
   magic(batch1, a.mb, a.kb);
   magic(one, a.mone, a.kone);
+  a.Sc = S;
+  a.Pr = P;
+  if (keep) {
+    a.sc0 = st[12], a.sc1 = st[13], a.ldsc = st[14];
+    a.pr0 = st[15], a.pr1 = st[16], a.ldpr = st[17];
+    a.ldsc32 = (int)st[14], a.ldpr32 = (int)st[17];
+    a.scbytes = (int)(31 * st[14] + T), a.prbytes = (int)(31 * st[17] + T);
+  } else {
+    a.sc0 = a.sc1 = a.ldsc = a.pr0 = a.pr1 = a.ldpr = 0;
+    a.ldsc32 = a.ldpr32 = a.scbytes = a.prbytes = 0;
+  }
   const unsigned grid = (unsigned)((long long)batch0 * batch1 * a.nqt);
-  if (flags & ANVIL_ATTN_S24)
-    launch_attention_nt<true>(a, D, grid, ctx->stream);
+  const bool s24 = flags & ANVIL_ATTN_S24;
+  if (keep)
+    s24 ? launch_attention_nt<true, true>(a, D, grid, ctx->stream) : launch_attention_nt<false, true>(a, D, grid, ctx->stream);
   else
-    launch_attention_nt<false>(a, D, grid, ctx->stream);
+    s24 ? launch_attention_nt<true, false>(a, D, grid, ctx->stream) : launch_attention_nt<false, false>(a, D, grid, ctx->stream);
   ANVIL_LAUNCHED();
   return ANVIL_OK;
+}
+
+extern "C" int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const int8_t* Vt, int8_t* O,
+                                  int batch0, int batch1, int T, int D, const int64_t* strides, int32_t m_s, int s_s,
+                                  const int32_t* lut, int32_t one, int causal, int32_t m_o, int s_o, int flags) {
+  return attention_entry(ctx, Q, K, Vt, O, nullptr, nullptr, false, batch0, batch1, T, D, strides, m_s, s_s, lut, one,
+                         causal, m_o, s_o, flags);
+}
+
+extern "C" int anvil_attention_i8_keep(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const int8_t* Vt, int8_t* O,
+                                       int8_t* S, int8_t* P, int batch0, int batch1, int T, int D,
+                                       const int64_t* strides, int32_t m_s, int s_s, const int32_t* lut, int32_t one,
+                                       int causal, int32_t m_o, int s_o, int flags) {
+  return attention_entry(ctx, Q, K, Vt, O, S, P, true, batch0, batch1, T, D, strides, m_s, s_s, lut, one, causal, m_o,
+                         s_o, flags);
 }

@@ -14,7 +14,8 @@ kernel trace. --config 1, 3, 4 run the other blocks; --config 2 the standalone i
 Printed: one JSON line with the metric, the dominant kernel's roofline, a per-kernel breakdown from an untimed
 profiled pass (kernel-bound events again, so the figures add up to less than ms_per_step), a stream-copy figure for
 the achievable HBM bandwidth, the PCIe-inclusive rate of `cm.run` on the host float input (never `value`), the step
-time of the same kernels replayed as one captured HIP graph (`hip_graph`, never `value`), and the
+time of the same kernels replayed as one captured HIP graph (`hip_graph`; `value` takes the faster of the eager and
+the replayed step, as cm.run does by default, and `launch` names it), and the
 CPU baseline: this repo's literal numpy restatement of the reference interpreter (oracle/, int64 `@`, single-threaded
 per process) on P sequences of the same batch in P processes on this host's cores (exact, as batched evaluation
 equals per-sample evaluation), scaled to tokens/s. It runs before the GPU is first touched, so the worker processes
@@ -203,7 +204,7 @@ def bench_block(args):
             e["TOPS"] = round(o_ / (us * 1e-6) / 1e12, 1)
             e["frac_mfma"] = round(e["TOPS"] / PEAK_INT8_TOPS, 4)
             if k_ == "attention":                 # MFMA work actually issued: 32-key tiles up to the diagonal
-                e["executed_ops"] = attention_executed_ops(steps[i][2])
+                e["executed_ops"] = attention_executed_ops(steps[i][2], steps[i][1].__name__ == "_call_attention_keep")
                 e["GBs"] = round(b_ / (us * 1e-6) / 1e9, 1)
             g_ops += o_
             g_us += us
@@ -492,14 +493,17 @@ def copy_calibration():
           flush=True)
 
 
-def attention_executed_ops(args):
+def attention_executed_ops(args, kept=False):
     """MFMA ops the fused attention kernel issues: per (batch, head) and 32-row query tile, the 32-key tiles up to the
-    diagonal (all of them without the causal mask), each a 32 x 32 x D QK^T and a 32 x D x 32 P.V."""
-    _, _, _, _, _, b0, b1, T, D = args[:9]
-    causal = bool(args[11].causal)
+    diagonal (all of them without the causal mask), each a 32 x 32 x D QK^T and a 32 x D x 32 P.V; the kept form
+    (anvil_attention_i8_keep, two more views in its arguments) also issues the QK^T of the tiles past the diagonal."""
+    k = 2 if kept else 0
+    b0, b1, T, D = args[5 + k:9 + k]
+    causal = bool(args[11 + k].causal)
     nt = T // 32
     tiles = nt * (nt + 1) // 2 if causal else nt * nt
-    return 2 * 2 * 32 * 32 * D * tiles * b0 * b1
+    upper = nt * nt - tiles if kept else 0
+    return (2 * 2 * tiles + 2 * upper) * 32 * 32 * D * b0 * b1
 
 
 _CPU = {}

@@ -246,6 +246,16 @@ int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const i
                        int batch1, int T, int D, const int64_t* strides, int32_t m_s, int s_s, const int32_t* lut,
                        int32_t one, int causal, int32_t m_o, int s_o, int flags);
 
+/* The same chain with its intermediate values kept (reference anvil/interp/graph.py:43-92 returns every value of the
+ * graph, the scores of anvil/semantics.py:95-103 and the probabilities of anvil/lower/graph_to_tensor.py:352-398
+ * among them): anvil_attention_i8, which also stores the whole T x T int8 score matrix into S and the probabilities
+ * into P (0 for masked keys), per (b0, b1). strides = the twelve of anvil_attention_i8, then {ss0, ss1, lds} of S
+ * and {sp0, sp1, ldp} of P, all multiples of 16, with lds, ldp >= T and 32 * lds, 32 * ldp below 2^31; S and P
+ * 16-byte aligned. Same preconditions and flags. */
+int anvil_attention_i8_keep(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const int8_t* Vt, int8_t* O, int8_t* S,
+                            int8_t* P, int batch0, int batch1, int T, int D, const int64_t* strides, int32_t m_s,
+                            int s_s, const int32_t* lut, int32_t one, int causal, int32_t m_o, int s_o, int flags);
+
 /* add_requant (reference anvil/semantics.py:106-115, golden.residual_add):
  *   out = clamp_out((a * ma + b * mb + 2^(shift-1)) >> shift), a and b ANVIL_I8 or ANVIL_I16, n elements. */
 int anvil_add_requant(anvil_ctx* ctx, const void* a, int a_dtype, const void* b, int b_dtype, int32_t ma, int32_t mb,

@@ -254,6 +254,25 @@ class FakeDevice:
         if r is not None:
             self.store(O, "i8", (b0, b1, T, D), (st[9], st[10], st[11], 1), r)
 
+    def attention_i8_keep(self, Q, K, Vt, O, S, P, b0, b1, T, D, strides, ms, ss, lut, one, causal, mo, so, flags):
+        """attention_i8 that also stores the scores and the probabilities (strides 12..17)."""
+        self.calls.append(("attention_keep", b0, b1, T, D, tuple(strides), flags))
+        st = strides
+        q = self.view(Q, "i8", (b0, b1, T, D), (st[0], st[1], st[2], 1)).astype(np.int64)
+        k = self.view(K, "i8", (b0, b1, T, D), (st[3], st[4], st[5], 1)).astype(np.int64)
+        vt = self.view(Vt, "i8", (b0, b1, D, T), (st[6], st[7], st[8], 1)).astype(np.int64)
+        lv = self.view(lut, "i32", (256,), (1,)).astype(np.int64)
+
+        def chain():
+            scores = sem.qmatmul(q, np.swapaxes(k, -1, -2), ms, ss, fast=self.fast)
+            p = sem.softmax_lut(scores, lv, one, causal)
+            return scores, p, sem.qmatmul(p, np.swapaxes(vt, -1, -2), mo, so, fast=self.fast)
+        r = self._guard(chain)
+        if r is not None:
+            self.store(S, "i8", (b0, b1, T, T), (st[12], st[13], st[14], 1), r[0])
+            self.store(P, "i8", (b0, b1, T, T), (st[15], st[16], st[17], 1), r[1])
+            self.store(O, "i8", (b0, b1, T, D), (st[9], st[10], st[11], 1), r[2])
+
     def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out, flags=0):
         self.calls.append(("rmsnorm", rows, cols, flags))
         xv = self.view(x, x_dtype, (rows, cols), (cols, 1)).astype(np.int64)

@@ -37,13 +37,16 @@ def test_planner_matches_oracle_on_config1(fake, cfg1):
     assert kinds.count("copy") == 0                                  # no layout op is materialised
     assert ("gemm_group", 3) in fake.calls                           # q, k and v: one group call
     # both residual adds run in the epilogues of the y and proj GEMMs; keep="all" still stores y and proj
-    assert kinds.count("gemm") == 6 and kinds.count("gemm_add") == 2 and kinds.count("add") == 0
+    assert kinds.count("gemm") == 4 and kinds.count("gemm_add") == 2 and kinds.count("add") == 0
     assert all(c[8] for c in fake.calls if c[0] == "gemm_add")
     gemms = [c for c in fake.calls if c[0] == "gemm"]
     assert all(c[1:4] == (1, 1, 96) for c in gemms[:2])              # q, k: batch and T fold into one M = 3 * 32
     assert gemms[2][1:6] == (1, 3, 64, 32, 64)                       # v is computed transposed, per sequence
-    # proven: unchecked (1), bounds below 2^23 allow the 24-bit requant multiply (8); P.V: causal K limit (4)
-    assert gemms[3][7] == 1 | 8 and gemms[4][7] == 1 | 4 | 8
+    # the returned scores and p come from the fused kernel's kept form: no score product, softmax or P.V launch;
+    # proven: unchecked (1), score bounds below 2^23 allow the 24-bit requant multiply (2)
+    assert kinds.count("softmax") == 0 and kinds.count("attention") == 0
+    (att,) = [c for c in fake.calls if c[0] == "attention_keep"]
+    assert att[1:5] == (3, 4, 32, 16) and att[6] == 1 | 2
 
 
 def test_keep_outputs_plan_fuses_attention(fake, cfg1):

@@ -473,6 +473,53 @@ def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
         assert np.array_equal(got, want), (seed, kind, np.argwhere(got != want)[:5])
 
 
+@pytest.mark.parametrize("B,H,T,D,pad", [(1, 2, 32, 16, 0), (2, 3, 64, 32, 16), (1, 3, 256, 64, 0),
+                                         (1, 2, 160, 128, 32), (1, 2, 1024, 64, 0), (2, 1, 512, 16, 0),
+                                         (1, 2, 992, 64, 16)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_fused_attention_keep_stores_scores_and_probabilities(dev, B, H, T, D, pad, causal):
+    """anvil_attention_i8_keep: the output as anvil_attention_i8's, and every score (the whole T x T product, past
+    the causal diagonal too) and every probability (0 for masked keys and for tiles skipped as all-zero) stored,
+    bit-exact with the oracle's scores -> softmax -> P.V chain. S and P start filled with another byte, so an
+    element the kernel leaves unwritten fails; pad > 0 gives their rows a stride of T + pad."""
+    for seed, sign, kind, one in ((0, 1, "exp", 127), (2, 1, "random", 127), (3, 1, "steep", 100), (4, 1, "self", 127),
+                                  (5, 1, "shift25", 127)):
+        q, k, v, (ms, ss, mo, so), lut, want = _attention_case(B, H, T, D, causal, seed, sign, kind, one)
+        split = lambda a: a.reshape(B, T, H, D).transpose(0, 2, 1, 3)       # noqa: E731
+        scores = sem.qmatmul(split(q), np.swapaxes(split(k), -1, -2), ms, ss, fast=True)
+        p = sem.softmax_lut(scores, lut, one, causal)
+        C, ld = H * D, T + pad
+        vt = np.ascontiguousarray(np.swapaxes(v, 1, 2))      # (B, C, T)
+        out = dev.alloc(B * T * C)
+        sb, pb = dev.alloc(B * H * T * ld), dev.alloc(B * H * T * ld)
+        for b in (sb, pb):
+            b.upload(np.full(B * H * T * ld, 0x5A, np.uint8))
+        strides = [T * C, D, C, T * C, D, C, C * T, D * T, T, T * C, D, C, H * T * ld, T * ld, ld, H * T * ld, T * ld,
+                   ld]
+        dev.attention_i8_keep(up(dev, q, "i8"), up(dev, k, "i8"), up(dev, vt, "i8"), out, sb, pb, B, H, T, D, strides,
+                              ms, ss, up(dev, lut, "i32"), one, causal, mo, so, rt.OP_UNCHECKED)
+        dev.sync()
+        got = out.download((B, T, C), np.int8).astype(np.int64)
+        assert np.array_equal(got, want), (seed, kind, np.argwhere(got != want)[:5])
+        gs = sb.download((B, H, T, ld), np.int8).astype(np.int64)
+        gp = pb.download((B, H, T, ld), np.int8).astype(np.int64)
+        assert np.array_equal(gs[..., :T], scores), (seed, kind, np.argwhere(gs[..., :T] != scores)[:5])
+        assert np.array_equal(gp[..., :T], p), (seed, kind, np.argwhere(gp[..., :T] != p)[:5])
+        assert np.all(gs[..., T:] == 0x5A) and np.all(gp[..., T:] == 0x5A)      # the row padding is untouched
+
+
+def test_fused_attention_keep_checks_its_strides(dev):
+    """The kept form refuses S / P strides that are not multiples of 16 or rows shorter than T, before any launch."""
+    B, H, T, D = 1, 1, 64, 32
+    bufs = [dev.alloc(4096) for _ in range(6)]
+    lut = up(dev, Q.exp_table(0.05, T, 127), "i32")
+    base = [T * D, T * D, D, T * D, T * D, D, D * T, D * T, T, T * D, T * D, D]
+    for tail, msg in (([T * T, T * T, T, T * T, T * T, T + 8], "multiple of 16"),
+                      ([T * T, T * T, 48, T * T, T * T, T], "out of range")):
+        with pytest.raises(ValueError, match=msg):
+            dev.attention_i8_keep(*bufs, B, H, T, D, base + tail, 1, 16, lut, 127, True, 1, 7, rt.OP_UNCHECKED)
+
+
 # add_requant multipliers: a negative one, config 5's two adds (Ma above 2^23, 128 (Ma + Mb) close to 2^31), and
 # Ma = Mb = 1 with no shift
 ADD_MULTS = [(300, -200, 9), (11157253, 4299753, 24), (7873258, 3110671, 23), (1, 1, 0)]
