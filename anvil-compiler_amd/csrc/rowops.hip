@@ -294,6 +294,17 @@ __device__ __forceinline__ int dpp_sum16(int v) {            // sum over the lan
   return v;
 }
 
+template <int L>
+__device__ __forceinline__ int lane_group_sum(int v) {                   // sum over aligned groups of L lanes
+  if constexpr (L > 1) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);    // quad_perm [1,0,3,2]
+  if constexpr (L > 2) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);    // quad_perm [2,3,0,1]
+  if constexpr (L > 4) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);   // row_half_mirror
+  if constexpr (L > 8) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);   // row_mirror
+  if constexpr (L > 16) v += __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 0x1F);           // lane ^ 16
+  if constexpr (L > 32) v += __shfl_xor(v, 32);
+  return v;
+}
+
 __device__ __forceinline__ unsigned sra_pack4v(int x0, int x1, int x2, int x3, int sh) {   // shift per lane
   unsigned d;
   asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
@@ -313,25 +324,28 @@ __device__ __forceinline__ int mad_i24v(int a, int b, int c) {
   return d;
 }
 
-template <int CH>
+// L = 16 lanes a row as described; L = 8 takes rows of 128 CH bytes, eight rows a wave, in the same way (each load or
+// store then covers 128 contiguous bytes of every row).
+template <int CH, int L = 16>
 __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
                                                              const int* __restrict__ lut, int lut_len, int mult,
                                                              int shift, long long rows, int8_t* __restrict__ out,
                                                              int kbo) {
-  constexpr int COLS = 256 * CH;
-  const int lane = threadIdx.x & 63, rr = lane >> 4, sub = lane & 15;
-  // kbo: the output K-blocked, as in rmsnorm_fast; chunk 16 c + sub of a row is in block 4 c + sub / 4
+  static_assert(L == 16 || L == 8, "16 or 8 lanes a row");
+  constexpr int COLS = 16 * L * CH, R = 64 / L;               // bytes a row, rows a wave
+  const int lane = threadIdx.x & 63, rr = lane / L, sub = lane % L;
+  // kbo: the output K-blocked, as in rmsnorm_fast; chunk L c + sub of a row is in block (L / 4) c + sub / 4
   const __amdgpu_buffer_rsrc_t wall = uniform_rsrc(out, kbo ? (int)(rows * COLS) : 0);
   const unsigned kcol = (unsigned)((sub >> 2) * kbo + 16 * (sub & 3));
   v4i wv[CH];                                                   // this lane's weights, packed (each multiply
 #pragma unroll                                                  // selects and sign-extends its byte)
-  for (int c = 0; c < CH; ++c) wv[c] = *reinterpret_cast<const v4i*>(w + 16 * (16 * c + sub));
+  for (int c = 0; c < CH; ++c) wv[c] = *reinterpret_cast<const v4i*>(w + 16 * (L * c + sub));
   unsigned off[CH];
 #pragma unroll
-  for (int c = 0; c < CH; ++c) off[c] = (unsigned)(rr * COLS + 16 * (16 * c + sub));
-  const long long step = (long long)gridDim.x * R_WAVES * 4;
-  auto group = [&](const int8_t* base, long long r0) {        // a raw buffer over rows r0 .. r0 + 3
-    const long long n = r0 < rows ? std::min<long long>(4, rows - r0) : 0;
+  for (int c = 0; c < CH; ++c) off[c] = (unsigned)(rr * COLS + 16 * (L * c + sub));
+  const long long step = (long long)gridDim.x * R_WAVES * R;
+  auto group = [&](const int8_t* base, long long r0) {        // a raw buffer over rows r0 .. r0 + R - 1
+    const long long n = r0 < rows ? std::min<long long>(R, rows - r0) : 0;
     return uniform_rsrc(base + (r0 < rows ? r0 : 0) * COLS, (int)(n * COLS));
   };
   auto load = [&](long long r0, v4i* xv) {
@@ -339,33 +353,33 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
 #pragma unroll
     for (int c = 0; c < CH; ++c) xv[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, off[c], 0, 0));
   };
-  auto pick = [&](const int* v) {                               // v[rr] of four wave-uniform values
-    return rr == 0 ? v[0] : (rr == 1 ? v[1] : (rr == 2 ? v[2] : v[3]));
-  };
   auto process = [&](const v4i* xv, long long r0) {
     int ss = 0;
 #pragma unroll
     for (int c = 0; c < CH; ++c)
 #pragma unroll
       for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[c][q], xv[c][q], ss, false);
-    ss = dpp_sum16(ss);
-    int rm_s[4], sh_s[4], rnd_s[4], lo_s[4], hi_s[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int t = __builtin_amdgcn_readlane(ss, 16 * j);
+    ss = L == 16 ? dpp_sum16(ss) : lane_group_sum<L>(ss);
+    // each row's values on the scalar unit, then the lane's row's selected (no array: an array of the rows' values
+    // indexed by the lane's row is what the compiler would otherwise make of the selects, through scratch)
+    int rm = 0, sh = 0, rnd = 0, lo = 0, hi = 0;
+    static_for<R>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      int t = __builtin_amdgcn_readlane(ss, L * j);
       int k = 0;
       while (t >= lut_len) {
         t >>= 2;
         ++k;
       }
-      const int sh = shift + k;
-      rm_s[j] = lut[t] * mult;                                  // proven below 2^23 in magnitude
-      sh_s[j] = sh;
-      rnd_s[j] = sh ? 1 << (sh - 1) : 0;
-      lo_s[j] = sh >= 24 ? INT32_MIN : -128 * (1 << sh);
-      hi_s[j] = sh >= 24 ? INT32_MAX : 128 * (1 << sh) - 1;
-    }
-    const int rm = pick(rm_s), sh = pick(sh_s), rnd = pick(rnd_s), lo = pick(lo_s), hi = pick(hi_s);
+      const int shj = shift + k;
+      const int rmj = lut[t] * mult;                            // proven below 2^23 in magnitude
+      const bool mine = rr == j;
+      rm = mine ? rmj : rm;
+      sh = mine ? shj : sh;
+      rnd = mine ? (shj ? 1 << (shj - 1) : 0) : rnd;
+      lo = mine ? (shj >= 24 ? INT32_MIN : -128 * (1 << shj)) : lo;
+      hi = mine ? (shj >= 24 ? INT32_MAX : 128 * (1 << shj) - 1) : hi;
+    });
     const __amdgpu_buffer_rsrc_t ws = group(out, r0);
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -380,12 +394,12 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
         const int y3 = med3i(mad_i24v(mul_sbytes<3>(xd, wd), rm, rnd), lo, hi);
         o[q] = (int)sra_pack4v(y0, y1, y2, y3, sh);
       }
-      const unsigned ko = r0 + rr < rows ? kcol + (unsigned)(4 * c * kbo + (r0 + rr) * 64) : OOB;
+      const unsigned ko = r0 + rr < rows ? kcol + (unsigned)((L / 4) * c * kbo + (r0 + rr) * 64) : OOB;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o),
                                              kbo ? wall : ws, kbo ? ko : off[c], 0, 0);
     }
   };
-  long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * 4;
+  long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * R;
   v4i xa[CH], xb[CH];
   load(row0, xa);
   while (row0 < rows) {
@@ -439,17 +453,6 @@ __device__ __forceinline__ int square_half(unsigned x) {                 // sext
     asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:WORD_1"
         : "=v"(d) : "v"(x));
   return d;
-}
-
-template <int L>
-__device__ __forceinline__ int lane_group_sum(int v) {                   // sum over aligned groups of L lanes
-  if constexpr (L > 1) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);    // quad_perm [1,0,3,2]
-  if constexpr (L > 2) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);    // quad_perm [2,3,0,1]
-  if constexpr (L > 4) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);   // row_half_mirror
-  if constexpr (L > 8) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);   // row_mirror
-  if constexpr (L > 16) v += __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 0x1F);           // lane ^ 16
-  if constexpr (L > 32) v += __shfl_xor(v, 32);
-  return v;
 }
 
 constexpr int WIDE_LUT_MAX = 4096;                               // table words the wide kernel stages in LDS
@@ -713,6 +716,11 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
       else if (ch == 2) launch(rmsnorm_rows16<2>);
       else if (ch == 3) launch(rmsnorm_rows16<3>);
       else launch(rmsnorm_rows16<4>);
+    } else if ((flags & ANVIL_RMS_S24) && cols == 128) {             // 8 lanes a row, 8 rows a wave
+      const long long groups8 = (rows + 7) / 8;
+      const dim3 grid8((unsigned)std::min<long long>((groups8 + R_WAVES - 1) / R_WAVES, 8ll * ctx->num_cu));
+      ANVIL_LAUNCH((rmsnorm_rows16<1, 8>), grid8, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
+                   mult, shift, (long long)rows, out, kbo);
     } else if (flags & ANVIL_RMS_S24)
       ANVIL_LAUNCH(rmsnorm_fast<true>, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
                          mult, shift, (long long)rows, cols, out, kbo);

@@ -112,11 +112,12 @@ def _rms(dev, x, xdt, w, lut, m, s, c=0, e=0, flags=0):
 
 
 @pytest.mark.parametrize("flags", [0, rt.OP_UNCHECKED, rt.OP_UNCHECKED | rt.RMS_S24])
-@pytest.mark.parametrize("d", [8, 64, 256, 512, 768, 1000, 1024])
+@pytest.mark.parametrize("d", [8, 64, 128, 256, 512, 768, 1000, 1024])
 def test_rmsnorm_i8(dev, d, flags):
     """flags=UNCHECKED selects the dot4 kernel with four rows a wave where d is a multiple of 16 up to 1024 (the
     proof's bounds hold for m = 1 and these LUTs), RMS_S24 its 24-bit multiply-add (every |lut m| < 2^23 here), on
-    16 lanes a row when d is 256, 512, 768 or 1024; results are the same bits either way."""
+    16 lanes a row when d is 256, 512, 768 or 1024 and 8 lanes a row when d is 128; results are the same bits either
+    way."""
     rng = np.random.default_rng([6, d])
     w = rng.integers(-127, 128, d)
     lut, s = Q.rsqrt_table(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
@@ -128,7 +129,7 @@ def test_rmsnorm_i8(dev, d, flags):
 
 
 @pytest.mark.parametrize("flags,d", [(rt.OP_UNCHECKED, 64), (rt.OP_UNCHECKED | rt.RMS_S24, 64),
-                                     (rt.OP_UNCHECKED | rt.RMS_S24, 768)])
+                                     (rt.OP_UNCHECKED | rt.RMS_S24, 128), (rt.OP_UNCHECKED | rt.RMS_S24, 768)])
 def test_rmsnorm_fast_walks_many_row_groups(dev, flags, d):
     """More row groups of four than the grid has waves (a cap of eight workgroups of four waves per CU): each wave
     walks several groups through both of its row buffers (three each on MI355X's 256 CUs), and the last group is
@@ -142,7 +143,7 @@ def test_rmsnorm_fast_walks_many_row_groups(dev, flags, d):
     assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s, flags=flags), want)
 
 
-@pytest.mark.parametrize("d", [64, 768])
+@pytest.mark.parametrize("d", [64, 128, 768])
 def test_rmsnorm_shift_reaching_int32_bounds(dev, d):
     """Requant shifts s + k from 20 up to 27: at 24 and above the pre-shift clamp bounds saturate to the int32 limits
     (rows with a large sum of squares take k up to 7 with a 1024-entry LUT)."""
