@@ -570,12 +570,13 @@ class CompiledModel:
     def _kblocked_values(self, keep, fused, skip, adds) -> set:
         """Values stored K-blocked in this plan: int8 results of an rmsnorm or of a plain linear product (a 2-D const
         right operand, stored unpermuted, no fused add) that are read only as the left operand of plain linear
-        products and not returned (keep="outputs"), in a proven graph, with a last dim that is a multiple of 64.
+        products and are not graph outputs, in a proven graph, with a last dim that is a multiple of 64 (keep="all"
+        reads such a value back from its blocks, View.view).
         Their readers then load whole 64-byte blocks of consecutive rows (ANVIL_GEMM_*_KBLOCK). Linear results read
         only by fused attention chains through a split into heads of 64 (q and k) are stored head-blocked too: each
         head's rows are then one contiguous block, read as a plain strided view. So is a fused attention's output
         merged back from its heads of 64 when only linear products read the merged value (om)."""
-        if keep != "outputs" or not self.proven:
+        if not self.proven:
             return set()
         fused_ops = set(fused) | skip
 

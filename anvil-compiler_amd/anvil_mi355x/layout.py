@@ -100,11 +100,18 @@ class View:
         return View(self.buf, self.dtype, (n,) + self.dims, (0,) + self.strides, self.offset, self.kb)
 
     def view(self, base: np.ndarray) -> np.ndarray:
-        """This view of `base` (the whole buffer downloaded as self.dtype), at that dtype, without a copy."""
+        """This view of `base` (the whole buffer downloaded as self.dtype), at that dtype: without a copy, or for
+        K-blocked storage a copy in the logical order (its 64-element blocks of a row are kb elements apart)."""
+        isz = self.itemsize
         if self.kb:
-            raise ValueError("K-blocked storage is planned only for values that are not read back")
+            if self.dims[-1] % 64:
+                raise ValueError("K-blocked storage holds whole 64-element blocks")
+            blocks = np.lib.stride_tricks.as_strided(
+                base[self.offset:], shape=(*self.dims[:-1], self.dims[-1] // 64, 64),
+                strides=tuple(s * isz for s in self.strides[:-1]) + (self.kb * isz, isz))
+            return blocks.reshape(self.dims)
         return np.lib.stride_tricks.as_strided(base[self.offset:], shape=self.dims,
-                                               strides=tuple(s * self.itemsize for s in self.strides))
+                                               strides=tuple(s * isz for s in self.strides))
 
     def read(self, base: np.ndarray) -> np.ndarray:
         """This view of `base` as a new int64 array."""
