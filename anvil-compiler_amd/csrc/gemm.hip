@@ -1214,6 +1214,185 @@ static bool launch_fast_group(GemmArgs* gs, const int* batch, int n, int osz, hi
   return true;
 }
 
+// Few-tile products with a long K (a handful of rows against a wide weight, as in decoding): one workgroup of four
+// groups of four waves per 64 x 64 output tile. Group grp sums the K chunks [grp S, (grp + 1) S) of the tile (S = a
+// quarter of them, chunks of 128 bytes = four MFMA steps), its four waves on 32 x 32 sub-tiles in a 2 x 2 grid; the
+// groups' partial sums meet in LDS and group 0 requantises. A group's chunk comes into LDS by direct-to-LDS loads
+// (64 rows x 128 bytes of each operand, 16-byte pieces XOR-swizzled by row so fragment reads spread over the
+// banks), two buffers a group, the next chunk loading while the current one feeds the MFMAs. Every group walks the
+// same number of chunks (pieces past its K range or past K load zeros), so the workgroup barriers line up. B rows
+// enter the MFMA in bperm order: accumulator r of lane l then holds column 16 (l / 32) + r of the lane's row l % 32,
+// 16 consecutive outputs, one 16-byte store (i8).
+constexpr int SMALL_SK = 4, SMALL_CK = 128;               // K groups a tile; K bytes a chunk
+
+template <int OSZ, bool MUL24>
+__global__ __launch_bounds__(SMALL_SK * 256) void gemm_i8_small(GemmArgs g) {
+  constexpr int TILE = 64 * SMALL_CK;                     // one operand's chunk: 64 rows of 128 bytes
+  // Each group's two buffers ([A | B] chunk) are arrays of their own, reached through a switch on the group, so the
+  // compiler sees which array every load fills and every read reads, and keeps the newer chunk's loads in flight
+  // across the older chunk's reads (with one array, or a group index into one, every read waited for every load).
+  __shared__ __attribute__((aligned(1024))) int8_t s00[2 * TILE], s01[2 * TILE], s10[2 * TILE], s11[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) int8_t s20[2 * TILE], s21[2 * TILE], s30[2 * TILE], s31[2 * TILE];
+  static_assert(SMALL_SK == 4, "four groups");
+  __shared__ int8_t lut_s[256];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int grp = wave >> 2, wq = wave & 3, wm = wq >> 1, wn = wq & 1;
+  const int l32 = lane & 31, half = lane >> 5;
+  const int tm = blockIdx.x / g.tiles_n, tn = blockIdx.x % g.tiles_n;
+  const int am0 = tm * 64, bn0 = tn * 64;
+  const int rows_a = min(g.M - am0, 64), rows_b = min(g.N - bn0, 64);
+  const __amdgpu_buffer_rsrc_t ra =
+      uniform_rsrc(g.A + (long long)am0 * g.lda, operand_bytes(rows_a, g.lda, g.kba, g.K));
+  const __amdgpu_buffer_rsrc_t rb =
+      uniform_rsrc(g.B + (long long)bn0 * g.ldb, operand_bytes(rows_b, g.ldb, g.kbb, g.K));
+  if (g.lut && t < 256) lut_s[t ^ 128] = g.lut[t];        // rotated: the entry of v at index v & 255
+  const int nck = (g.K + SMALL_CK - 1) / SMALL_CK;        // chunks of the product
+  const int S = (nck + SMALL_SK - 1) / SMALL_SK;          // chunks a group (the last group's may run past K)
+  const int kend = min(g.K, (grp + 1) * S * SMALL_CK);    // this group's K bytes end here
+  // this wave's two load instructions of each operand: rows 8 i + lane / 8 (i = wq, wq + 4), global piece
+  // (lane % 8) ^ swizzle, landing in LDS piece lane % 8 of that row
+  int pk[2];                                              // the piece's K offset in a chunk
+  unsigned rowa[2], rowb[2];                              // the row's byte offset, or OOB past the tile's rows
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 8 * (wq + 4 * j) + (lane >> 3);
+    pk[j] = 16 * swz<128>(r, lane & 7);
+    rowa[j] = r < rows_a ? (unsigned)(r * g.lda) : OOB;
+    rowb[j] = r < rows_b ? (unsigned)(r * g.ldb) : OOB;
+  }
+  // a chunk's pieces start at multiples of 16 below a 64-byte block's end, so block k >> 6 holds all 16 bytes
+  auto issue = [&](int c, int8_t* base) __attribute__((always_inline)) {   // chunk c of this group into base
+    const int k0 = (grp * S + c) * SMALL_CK;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int k = k0 + pk[j];
+      const bool kin = k < kend;
+      const unsigned ka = (unsigned)((k >> 6) * g.kba + (k & 63)), kb = (unsigned)((k >> 6) * g.kbb + (k & 63));
+      dma16(ra, base + (wq + 4 * j) * 1024, kin && rowa[j] != OOB ? rowa[j] + ka : OOB);
+      dma16(rb, base + TILE + (wq + 4 * j) * 1024, kin && rowb[j] != OOB ? rowb[j] + kb : OOB);
+    }
+  };
+  const int ar = wm * 32 + l32, br = wn * 32 + bperm(l32);
+  v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  auto compute = [&](const int8_t* base) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {                         // MFMA step j: logical pieces 2 j and 2 j + 1
+      const int q = 2 * j + half;
+      const v4i af = *reinterpret_cast<const v4i*>(base + ar * SMALL_CK + 16 * swz<128>(ar, q));
+      const v4i bf = *reinterpret_cast<const v4i*>(base + TILE + br * SMALL_CK + 16 * swz<128>(br, q));
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af, acc, 0, 0, 0);
+    }
+  };
+  // chunk c lives in buffer c % 2; chunk c + 1 loads while chunk c is read (past the group's chunks every piece is
+  // out of range: zeros). The waits leave the newer chunk's four loads of this wave in flight; the barriers (no
+  // release fence, which would wait for those loads too) make every wave's pieces visible, then free the buffer for
+  // the chunk after next.
+  auto walk = [&](int8_t* b0, int8_t* b1) __attribute__((always_inline)) {   // inlined: b0, b1 known arrays
+    issue(0, b0);
+    for (int c = 0; c < S; c += 2) {
+      issue(c + 1, b1);
+      wait_vmcnt(4);
+      stage_barrier();
+      compute(b0);
+      __builtin_amdgcn_s_waitcnt(0xC07F);                 // lgkmcnt(0): this wave's reads of b0 are done
+      stage_barrier();
+      if (c + 1 >= S) break;
+      issue(c + 2, b0);
+      wait_vmcnt(4);
+      stage_barrier();
+      compute(b1);
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      stage_barrier();
+    }
+    wait_vmcnt(0);                                        // the last (all-zero) chunk's loads land before LDS reuse
+    __syncthreads();
+    if (grp > 0) {                                        // the partial sums, into the group's first buffer (16 KiB)
+      int* pp = reinterpret_cast<int*>(b0) + (wq * 64 + lane) * 16;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<v4i*>(pp + 4 * q) = v4i{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+    }
+    __syncthreads();
+  };
+  switch (grp) {
+    case 0: walk(s00, s01); break;
+    case 1: walk(s10, s11); break;
+    case 2: walk(s20, s21); break;
+    default: walk(s30, s31); break;
+  }
+  if (grp > 0) return;
+  for (const int8_t* b : {s10, s20, s30}) {
+    const int* pp = reinterpret_cast<const int*>(b) + (wq * 64 + lane) * 16;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const v4i x = *reinterpret_cast<const v4i*>(pp + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[4 * q + e] += x[e];
+    }
+  }
+  const int m = am0 + ar, n = bn0 + wn * 32 + 16 * half;
+  if (m >= g.M || n >= g.N) return;
+  const int lo = OSZ == 1 ? -128 : -32768, hi = OSZ == 1 ? 127 : 32767;
+  int v[16];
+  auto requant = [&](auto lut) {                          // the LUT choice outside the element loop
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int x = MUL24 ? (__mul24(acc[r], g.mult) + g.rnd) : (acc[r] * g.mult + g.rnd);
+      v[r] = min(max(x >> g.shift, lo), hi);
+      if constexpr (decltype(lut)::value) v[r] = lut_s[(uint8_t)v[r]];
+    }
+  };
+  if (OSZ == 1 && g.lut)
+    requant(std::true_type{});
+  else
+    requant(std::false_type{});
+  char* c = reinterpret_cast<char*>(g.C) + cpos(g, m, n) * OSZ;
+  if (g.vec_store && n + 16 <= g.N) {
+    if (OSZ == 1) {
+      *reinterpret_cast<v4i*>(c) = v4i{(int)pack4(v[0], v[1], v[2], v[3]), (int)pack4(v[4], v[5], v[6], v[7]),
+                                       (int)pack4(v[8], v[9], v[10], v[11]), (int)pack4(v[12], v[13], v[14], v[15])};
+    } else {
+      v4i w0, w1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        w0[q] = (int)__builtin_amdgcn_perm((unsigned)v[2 * q + 1], (unsigned)v[2 * q], 0x05040100u);
+        w1[q] = (int)__builtin_amdgcn_perm((unsigned)v[2 * q + 9], (unsigned)v[2 * q + 8], 0x05040100u);
+      }
+      *reinterpret_cast<v4i*>(c) = w0;
+      *reinterpret_cast<v4i*>(c + 16) = w1;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      if (n + e >= g.N) break;
+      if (OSZ == 1)
+        reinterpret_cast<int8_t*>(g.C)[cpos(g, m, n + e)] = (int8_t)v[e];
+      else
+        reinterpret_cast<int16_t*>(g.C)[cpos(g, m, n + e)] = (int16_t)v[e];
+    }
+  }
+}
+
+template <bool MUL24>
+static void launch_small(GemmArgs& g, int osz, hipStream_t s) {
+  g.tiles_m = (g.M + 63) / 64;
+  g.tiles_n = (g.N + 63) / 64;
+  const dim3 grid(g.tiles_m * g.tiles_n);
+  if (osz == 1)
+    ANVIL_LAUNCH((gemm_i8_small<1, MUL24>), grid, dim3(SMALL_SK * 256), 0, s, g);
+  else
+    ANVIL_LAUNCH((gemm_i8_small<2, MUL24>), grid, dim3(SMALL_SK * 256), 0, s, g);
+}
+
+// Whether a fast-path product takes gemm_i8_small: one product (batch 1, no causal mode, no fused add) whose 128 x 128
+// tiles fill at most a quarter of the CUs, with K >= 512.
+static bool small_plan(const GemmArgs& g, int batch, int num_cu) {
+  if (batch != 1 || g.causal != 0 || g.res || g.K < 512) return false;
+  const long long tiles = (long long)((g.M + 127) / 128) * ((g.N + 127) / 128);
+  return tiles * 4 <= num_cu;
+}
+
 constexpr int SPLITK_MAX = 4;                             // K chunks of one product (partial tiles kept per tile)
 
 // Split-K on 128 x 128 tiles (three LDS stages, three workgroups per CU): grid (tiles, splits) storing partial
@@ -1556,6 +1735,13 @@ static int gemm_launch(anvil_ctx* ctx, Prepared& p, bool noalloc = false) {
     return ANVIL_OK;
   }
   int splits = 0, kchunk = 0;
+  if (!p.force_split && !ctx->gemm_cfg && small_plan(p.g, p.batch, ctx->num_cu)) {
+    if (p.mul24)
+      launch_small<true>(p.g, p.osz, ctx->stream);
+    else
+      launch_small<false>(p.g, p.osz, ctx->stream);
+    return ANVIL_OK;
+  }
   if (splitk_plan(p.g, p.batch, ctx->num_cu, p.force_split, splits, kchunk)) {
     const long long tiles = (long long)((p.g.M + 127) / 128) * ((p.g.N + 127) / 128);
     const long long sums = tiles * splits * 128 * 128;   // one int32 partial tile per (tile, chunk)
