@@ -391,7 +391,8 @@ class CompiledModel:
     def _attention_chains(self, keep) -> dict:
         """{P.V matmul: (scores matmul, softmax)} for every chain qmatmul -> softmax_lut -> qmatmul whose scores and
         probabilities are read by nothing else, in a proven graph with int8 values throughout, a square (T x T)
-        score matrix with T a multiple of 32 up to 1024 and one head dim of 16, 32, 64 or 128: the chains
+        score matrix with T a multiple of 32 up to 1024 and one head dim of 16, 32, 64 or 128, or T = 16 and a head
+        dim of 16 or 32: the chains
         anvil_attention_i8 evaluates without materialising scores or p, or, when the run returns them (keep="all",
         or graph outputs), anvil_attention_i8_keep, which also stores them (_kept_chain)."""
         if not self.proven:
@@ -411,7 +412,8 @@ class CompiledModel:
                 continue
             sd, od = g.qt(s_op.result).dims, g.qt(o_op.result).dims
             T, D = sd[-1], g.qt(s_op.a).dims[-1]
-            if sd[-2] != T or T % 32 or T > 1024 or D not in (16, 32, 64, 128) or od[-1] != D or od[-2] != T:
+            if (sd[-2] != T or (T % 32 and T != 16) or T > 1024 or D not in (16, 32, 64, 128) or (T == 16 and D > 32)
+                    or od[-1] != D or od[-2] != T):
                 continue
             found[o_op] = (s_op, sm)
         return found

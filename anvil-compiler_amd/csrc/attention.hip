@@ -503,6 +503,112 @@ static void launch_attention_nt(const AttnArgs& a, int D, unsigned grid, hipStre
     launch_attention<8, S24, KEEP>(a, D, grid, s);
 }
 
+
+// ------------------------------------------------------------------------------------------------ T = 16
+// The same chain for sequences of 16 tokens (the reference's frozen models: T 16, heads of 16), where a 32 x 32 tile
+// is mostly empty: one lane a query row, so a wave holds four (batch, head) pairs whole and nothing crosses waves.
+// Lane 16 h + i of a wave takes row i of its head h. Its q row (DC 16-byte chunks) loads into registers; its k row
+// and its V^T rows (V^T row d = the 16 keys' values of dim d: rows i and 16 + i at D = 32) go to LDS, from where every
+// lane of the head reads all 16 (same address across the 16 lanes: a broadcast). Then per row, in registers:
+//   s_j = clamp((q . k_j) M_s + rnd) >> s_s for the 16 keys (v_dot4 on 4-byte pieces);
+//   m = max(-128, max of the kept s_j) (key j kept iff j <= i when causal); e_j = lut[s_j - m + 255] (kept, else 0);
+//   S = sum e_j; p_j = (e_j one + S // 2) // S exactly, as y = fma(e_j, A, B) with A = fl(one / S) and
+//   B = fl((S // 2) / S + 2^-40) - 1/2, rounded by adding 1.5 2^52 (the quotient bound and error argument of the
+//   long kernel's p tables, which hold for every n < 2^31 and quotient < 128);
+//   o_d = clamp((p . V^T_d) M_o + rnd) >> s_o, p packed as 16 bytes (p >= 0, so the signed v_dot4 is exact).
+// The kept form also stores the row's 16 scores and 16 probabilities (16-byte stores).
+template <int DC, bool S24, bool KEEP>
+__global__ __launch_bounds__(A_THREADS) void attention_t16(AttnArgs a, int nheads) {
+  constexpr int W = A_THREADS / 64;
+  __shared__ int lut_s[256];
+  __shared__ __attribute__((aligned(16))) v4i kst[W][64][DC];   // lane l's k row, chunk c
+  __shared__ __attribute__((aligned(16))) v4i vst[W][64][DC];   // lane l's V^T rows i + 16 c (one 16-byte row each)
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int hl = lane >> 4, i = lane & 15;
+  const long long hh = ((long long)blockIdx.x * W + w) * 4 + hl;          // (batch, head) of this lane
+  const bool live = hh < nheads;
+  const int b0 = live ? (int)(hh / a.batch1) : 0, b1 = live ? (int)(hh % a.batch1) : 0;
+  lut_s[t] = a.lut[t];
+  v4i qv[DC];
+  const int8_t* Qr = a.Q + b0 * a.sq0 + b1 * a.sq1 + (long long)i * a.ldq;
+  const int8_t* Kr = a.K + b0 * a.sk0 + b1 * a.sk1 + (long long)i * a.ldk;
+  const int8_t* Vr = a.V + b0 * a.sv0 + b1 * a.sv1 + (long long)i * a.ldv;
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    qv[c] = live ? *reinterpret_cast<const v4i*>(Qr + 16 * c) : v4i{0, 0, 0, 0};
+    kst[w][lane][c] = live ? *reinterpret_cast<const v4i*>(Kr + 16 * c) : v4i{0, 0, 0, 0};
+    vst[w][lane][c] = live ? *reinterpret_cast<const v4i*>(Vr + 16 * c * a.ldv) : v4i{0, 0, 0, 0};
+  }
+  __syncthreads();
+  // scores of the row, clamped in the pre-shift domain, and the row max over the kept keys
+  int sc[16];
+  int mx = -128;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    int acc = 0;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      const v4i kj = kst[w][16 * hl + j][c];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_sdot4(qv[c][q], kj[q], acc, false);
+    }
+    const int y = S24 ? __mul24(acc, a.ms) + a.rnds : acc * a.ms + a.rnds;
+    sc[j] = med3i(y, a.clo, a.chi) >> a.ss;
+    if (!a.causal || j <= i) mx = max(mx, sc[j]);
+  }
+  int e[16];
+  int S = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {                   // a kept score lies in [-128, mx], so its index in [0, 255]
+    const bool kept = !a.causal || j <= i;
+    e[j] = lut_s[kept ? sc[j] - mx + 255 : 0];
+    e[j] = kept ? e[j] : 0;
+    S += e[j];
+  }
+  S = max(S, 1);                                   // S >= lut[255] >= 1 for a live row (the entry's precondition)
+  const double Sd = (double)S;
+  const double qa = (double)a.one / Sd;
+  const double qb = (double)(S >> 1) / Sd + 0x1p-40 - 0.5;
+  int p[16];                                       // a masked key's e_j = 0 gives (S // 2) // S = 0, as it must
+#pragma unroll
+  for (int j = 0; j < 16; ++j) p[j] = __double2loint(__builtin_fma((double)e[j], qa, qb) + 0x1.8p52);
+  v4i pp;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) pp[g] = (int)pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
+  // O row: 16 DC dims, each the dot of p with V^T row d (lane 16 hl + (d % 16)'s chunk d / 16)
+  int ov[16 * DC];
+#pragma unroll
+  for (int d = 0; d < 16 * DC; ++d) {
+    const v4i vd = vst[w][16 * hl + (d & 15)][d >> 4];
+    int acc = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_sdot4(pp[q], vd[q], acc, false);
+    const int y = a.mo24 ? __mul24(acc, a.mo) + a.rndo : acc * a.mo + a.rndo;
+    ov[d] = med3i(y, a.clo_o, a.chi_o);
+  }
+  if (!live) return;
+  int8_t* Or = a.O + b0 * a.so0 + b1 * a.so1 + (long long)i * a.ldo;
+#pragma unroll
+  for (int d = 0; d < 16 * DC; d += 4)
+    *reinterpret_cast<unsigned*>(Or + d) = sra_pack4(ov[d], ov[d + 1], ov[d + 2], ov[d + 3], a.so);
+  if constexpr (KEEP) {
+    v4i sv;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sv[g] = (int)pack4(sc[4 * g], sc[4 * g + 1], sc[4 * g + 2], sc[4 * g + 3]);
+    *reinterpret_cast<v4i*>(a.Sc + b0 * a.sc0 + b1 * a.sc1 + (long long)i * a.ldsc) = sv;
+    *reinterpret_cast<v4i*>(a.Pr + b0 * a.pr0 + b1 * a.pr1 + (long long)i * a.ldpr) = pp;
+  }
+}
+
+template <bool S24, bool KEEP>
+static void launch_attention_t16(const AttnArgs& a, int D, long long nheads, hipStream_t s) {
+  const unsigned grid = (unsigned)((nheads + 4 * (A_THREADS / 64) - 1) / (4 * (A_THREADS / 64)));
+  if (D == 16)
+    ANVIL_LAUNCH((attention_t16<1, S24, KEEP>), dim3(grid), dim3(A_THREADS), 0, s, a, (int)nheads);
+  else
+    ANVIL_LAUNCH((attention_t16<2, S24, KEEP>), dim3(grid), dim3(A_THREADS), 0, s, a, (int)nheads);
+}
+
 }  // namespace anvil
 
 using namespace anvil;
@@ -518,10 +624,12 @@ static int attention_entry(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, con
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: null pointer");
   if (!(flags & ANVIL_OP_UNCHECKED) || (flags & ~(ANVIL_OP_UNCHECKED | ANVIL_ATTN_S24)))
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: flags must hold ANVIL_OP_UNCHECKED (a proven graph)");
-  if (batch0 < 1 || batch1 < 1 || T < 32 || T % 32 || T > 1024)
-    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: T=%d must be a multiple of 32 in [32, 1024]", T);
+  if (batch0 < 1 || batch1 < 1 || (T != 16 && (T < 32 || T % 32 || T > 1024)))
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: T=%d must be 16 or a multiple of 32 in [32, 1024]", T);
   if (D != 16 && D != 32 && D != 64 && D != 128)
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: head dim %d not in {16, 32, 64, 128}", D);
+  if (T == 16 && D > 32)
+    return set_error(ANVIL_E_VALUE, "anvil_attention_i8: T=16 takes head dims 16 and 32, not %d", D);
   if (s_s < 0 || s_s > 31 || s_o < 0 || s_o > 31) return set_error(ANVIL_E_VALUE, "shift outside [0, 31]");
   if (one < 1 || one > 127) return set_error(ANVIL_E_VALUE, "one=%d does not fit int8", one);
   if ((flags & ANVIL_ATTN_S24) && (m_s >= (1 << 23) || m_s <= -(1 << 23)))
@@ -533,7 +641,7 @@ static int attention_entry(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, con
                        (long long)st[i], i < 9 ? 16 : 4);
   if (!al(Q, 16) || !al(K, 16) || !al(Vt, 16) || !al(O, 4))
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: operand not aligned");
-  if ((long long)batch0 * batch1 * (T / 32) > (1ll << 31) - 1)
+  if ((long long)batch0 * batch1 * std::max(1, T / 32) > (1ll << 31) - 1)
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: too many heads");
   // K and V^T are read through 32-bit buffer offsets over one head: T key rows of stride ldk (each at least D
   // bytes apart), D rows of V^T of stride ldv (each at least T keys)
@@ -582,7 +690,7 @@ static int attention_entry(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, con
     while ((1 << k) < d) ++k;
     m = ((1ull << (32 + k)) + d - 1) / d;
   };
-  magic(a.nqt, a.mq, a.kq);
+  magic(std::max(1, a.nqt), a.mq, a.kq);
   magic(batch1, a.mb, a.kb);
   magic(one, a.mone, a.kone);
   a.Sc = S;
@@ -596,8 +704,17 @@ static int attention_entry(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, con
     a.sc0 = a.sc1 = a.ldsc = a.pr0 = a.pr1 = a.ldpr = 0;
     a.ldsc32 = a.ldpr32 = a.scbytes = a.prbytes = 0;
   }
-  const unsigned grid = (unsigned)((long long)batch0 * batch1 * a.nqt);
   const bool s24 = flags & ANVIL_ATTN_S24;
+  if (T == 16) {
+    const long long nh = (long long)batch0 * batch1;
+    if (keep)
+      s24 ? launch_attention_t16<true, true>(a, D, nh, ctx->stream) : launch_attention_t16<false, true>(a, D, nh, ctx->stream);
+    else
+      s24 ? launch_attention_t16<true, false>(a, D, nh, ctx->stream) : launch_attention_t16<false, false>(a, D, nh, ctx->stream);
+    ANVIL_LAUNCHED();
+    return ANVIL_OK;
+  }
+  const unsigned grid = (unsigned)((long long)batch0 * batch1 * a.nqt);
   if (keep)
     s24 ? launch_attention_nt<true, true>(a, D, grid, ctx->stream) : launch_attention_nt<false, true>(a, D, grid, ctx->stream);
   else
