@@ -413,6 +413,73 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
   }
 }
 
+// rmsnorm_int over short int8 rows (16 L bytes, L = 1, 2 or 4 lanes a row, 64 / L rows a wave: the reference's
+// frozen models have rows of 32), the S24 form. With so many rows a wave, the per-row values are each lane's own:
+// the row sum is reduced over the row's L lanes, then every lane forms its row's table index, multiplier, shift and
+// clamp bounds (the table staged in LDS, as in rmsnorm_wide_fast), and the element math is rmsnorm_rows16's.
+template <int L>
+__global__ __launch_bounds__(R_THREADS) void rmsnorm_narrow(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
+                                                             const int* __restrict__ lut, int lut_len, int mult,
+                                                             int shift, long long rows, int8_t* __restrict__ out,
+                                                             int kbo) {
+  constexpr int COLS = 16 * L, R = 64 / L;
+  extern __shared__ int narrow_lut[];
+  for (int i0 = threadIdx.x; i0 < lut_len; i0 += R_THREADS) narrow_lut[i0] = lut[i0];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, rr = lane / L, sub = lane % L;
+  const __amdgpu_buffer_rsrc_t wall = uniform_rsrc(out, kbo ? (int)(rows * COLS) : 0);
+  const unsigned kcol = (unsigned)(16 * sub);                  // K-blocked output (COLS = 64): one block a row
+  const v4i wv = *reinterpret_cast<const v4i*>(w + 16 * sub);
+  const unsigned off = (unsigned)(rr * COLS + 16 * sub);
+  const long long step = (long long)gridDim.x * R_WAVES * R;
+  auto group = [&](const int8_t* base, long long r0) {        // a raw buffer over rows r0 .. r0 + R - 1
+    const long long n = r0 < rows ? std::min<long long>(R, rows - r0) : 0;
+    return uniform_rsrc(base + (r0 < rows ? r0 : 0) * COLS, (int)(n * COLS));
+  };
+  auto load = [&](long long r0) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(group(x, r0), off, 0, 0));
+  };
+  auto process = [&](v4i xv, long long r0) {
+    int ss = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[q], xv[q], ss, false);
+    int t = lane_group_sum<L>(ss);
+    int k = 0;
+    while (t >= lut_len) {
+      t >>= 2;
+      ++k;
+    }
+    const int sh = shift + k;
+    const int rm = narrow_lut[t] * mult;                        // proven below 2^23 in magnitude
+    const int rnd = sh ? 1 << (sh - 1) : 0;
+    const int lo = sh >= 24 ? INT32_MIN : -128 * (1 << sh), hi = sh >= 24 ? INT32_MAX : 128 * (1 << sh) - 1;
+    v4i o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const unsigned xd = (unsigned)xv[q], wd = (unsigned)wv[q];
+      const int y0 = med3i(mad_i24v(mul_sbytes<0>(xd, wd), rm, rnd), lo, hi);
+      const int y1 = med3i(mad_i24v(mul_sbytes<1>(xd, wd), rm, rnd), lo, hi);
+      const int y2 = med3i(mad_i24v(mul_sbytes<2>(xd, wd), rm, rnd), lo, hi);
+      const int y3 = med3i(mad_i24v(mul_sbytes<3>(xd, wd), rm, rnd), lo, hi);
+      o[q] = (int)sra_pack4v(y0, y1, y2, y3, sh);
+    }
+    const unsigned ko = r0 + rr < rows ? kcol + (unsigned)((r0 + rr) * 64) : OOB;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o),
+                                           kbo ? wall : group(out, r0), kbo ? ko : off, 0, 0);
+  };
+  long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * R;
+  v4i xa = load(row0), xb;
+  while (row0 < rows) {
+    xb = load(row0 + step);
+    process(xa, row0);
+    row0 += step;
+    if (row0 >= rows) break;
+    xa = load(row0 + step);
+    process(xb, row0);
+    row0 += step;
+  }
+}
+
 // ------------------------------------------------------------------------------- fast rmsnorm_int, int16 rows
 // The proven form of a wide (int16) row: ss = e + sum((x^2 + 2^(c-1)) >> c), out = requant(x w lut[i], M, s + k).
 // A row of cols = 8 n entries is n chunks of 16 bytes (8 entries); L lanes (the power of two >= n, at most 64)
@@ -716,6 +783,17 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
       else if (ch == 2) launch(rmsnorm_rows16<2>);
       else if (ch == 3) launch(rmsnorm_rows16<3>);
       else launch(rmsnorm_rows16<4>);
+    } else if ((flags & ANVIL_RMS_S24) && (cols == 16 || cols == 32 || cols == 64) && lut_len <= WIDE_LUT_MAX) {
+      const int L = cols / 16;                                         // lanes a row, 64 / L rows a wave
+      const long long groupsn = (rows + 64 / L - 1) / (64 / L);
+      const dim3 gridn((unsigned)std::min<long long>((groupsn + R_WAVES - 1) / R_WAVES, 8ll * ctx->num_cu));
+      auto launch = [&](auto kernel) {
+        ANVIL_LAUNCH(kernel, gridn, dim3(R_THREADS), lut_len * sizeof(int), ctx->stream, (const int8_t*)x, w, lut,
+                     lut_len, mult, shift, (long long)rows, out, kbo);
+      };
+      if (L == 1) launch(rmsnorm_narrow<1>);
+      else if (L == 2) launch(rmsnorm_narrow<2>);
+      else launch(rmsnorm_narrow<4>);
     } else if ((flags & ANVIL_RMS_S24) && cols == 128) {             // 8 lanes a row, 8 rows a wave
       const long long groups8 = (rows + 7) / 8;
       const dim3 grid8((unsigned)std::min<long long>((groups8 + R_WAVES - 1) / R_WAVES, 8ll * ctx->num_cu));

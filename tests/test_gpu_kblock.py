@@ -156,13 +156,13 @@ def test_kblocked_batched_and_grouped(dev):
 
 
 @pytest.mark.parametrize("xdt,d,flags", [("i8", 768, rt.OP_UNCHECKED | rt.RMS_S24), ("i8", 256, rt.OP_UNCHECKED | rt.RMS_S24),
-                                         ("i8", 128, rt.OP_UNCHECKED | rt.RMS_S24),
+                                         ("i8", 128, rt.OP_UNCHECKED | rt.RMS_S24), ("i8", 64, rt.OP_UNCHECKED | rt.RMS_S24),
                                          ("i8", 320, rt.OP_UNCHECKED | rt.RMS_S24), ("i8", 768, rt.OP_UNCHECKED),
                                          ("i8", 192, 0), ("i16", 64, rt.OP_UNCHECKED), ("i16", 768, rt.OP_UNCHECKED),
                                          ("i16", 128, 0)])
 @pytest.mark.parametrize("rows", [203, 8 * 4 * 256 * 4 * 2 + 3])
 def test_rmsnorm_kblocked_result(dev, xdt, d, flags, rows):
-    """ANVIL_RMS_OUT_KBLOCK on every rmsnorm kernel (16 or 8 lanes a row, four rows a wave, the wide int16 form and
+    """ANVIL_RMS_OUT_KBLOCK on every rmsnorm kernel (16, 8 or 4 lanes a row, four rows a wave, the wide int16 form and
     the checked one): the result K-blocked, block stride rows * 64, equal to the oracle's rows; ragged row counts, and
     more row groups than the grid has waves."""
     from anvil_mi355x import quantize as Q

@@ -112,12 +112,12 @@ def _rms(dev, x, xdt, w, lut, m, s, c=0, e=0, flags=0):
 
 
 @pytest.mark.parametrize("flags", [0, rt.OP_UNCHECKED, rt.OP_UNCHECKED | rt.RMS_S24])
-@pytest.mark.parametrize("d", [8, 64, 128, 256, 512, 768, 1000, 1024])
+@pytest.mark.parametrize("d", [8, 16, 32, 64, 128, 256, 512, 768, 1000, 1024])
 def test_rmsnorm_i8(dev, d, flags):
     """flags=UNCHECKED selects the dot4 kernel with four rows a wave where d is a multiple of 16 up to 1024 (the
     proof's bounds hold for m = 1 and these LUTs), RMS_S24 its 24-bit multiply-add (every |lut m| < 2^23 here), on
-    16 lanes a row when d is 256, 512, 768 or 1024 and 8 lanes a row when d is 128; results are the same bits either
-    way."""
+    16 lanes a row when d is 256, 512, 768 or 1024, 8 lanes a row when d is 128, and 1, 2 or 4 lanes a row with
+    per-lane row values when d is 16, 32 or 64; results are the same bits either way."""
     rng = np.random.default_rng([6, d])
     w = rng.integers(-127, 128, d)
     lut, s = Q.rsqrt_table(0.03, 0.01, 0.02, int(np.abs(w).max()), d, 1e-5)
@@ -129,7 +129,8 @@ def test_rmsnorm_i8(dev, d, flags):
 
 
 @pytest.mark.parametrize("flags,d", [(rt.OP_UNCHECKED, 64), (rt.OP_UNCHECKED | rt.RMS_S24, 64),
-                                     (rt.OP_UNCHECKED | rt.RMS_S24, 128), (rt.OP_UNCHECKED | rt.RMS_S24, 768)])
+                                     (rt.OP_UNCHECKED | rt.RMS_S24, 32), (rt.OP_UNCHECKED | rt.RMS_S24, 128),
+                                     (rt.OP_UNCHECKED | rt.RMS_S24, 768)])
 def test_rmsnorm_fast_walks_many_row_groups(dev, flags, d):
     """More row groups of four than the grid has waves (a cap of eight workgroups of four waves per CU): each wave
     walks several groups through both of its row buffers (three each on MI355X's 256 CUs), and the last group is
@@ -143,7 +144,7 @@ def test_rmsnorm_fast_walks_many_row_groups(dev, flags, d):
     assert np.array_equal(_rms(dev, x, "i8", w, lut, 1, s, flags=flags), want)
 
 
-@pytest.mark.parametrize("d", [64, 128, 768])
+@pytest.mark.parametrize("d", [32, 64, 128, 768])
 def test_rmsnorm_shift_reaching_int32_bounds(dev, d):
     """Requant shifts s + k from 20 up to 27: at 24 and above the pre-shift clamp bounds saturate to the int32 limits
     (rows with a large sum of squares take k up to 7 with a 1024-entry LUT)."""
@@ -449,13 +450,14 @@ def _attention_case(B, H, T, D, causal, seed, ms_sign=1, lut_kind="exp", one=127
 
 @pytest.mark.parametrize("B,H,T,D", [(1, 2, 32, 16), (2, 3, 64, 32), (1, 2, 96, 64), (2, 2, 128, 32),
                                      (1, 3, 256, 64), (1, 2, 160, 128), (1, 2, 1024, 64), (2, 1, 512, 16),
-                                     (1, 1, 1024, 128), (1, 2, 1024, 32), (1, 2, 992, 64)])
+                                     (1, 1, 1024, 128), (1, 2, 1024, 32), (1, 2, 992, 64), (5, 2, 16, 16),
+                                     (3, 3, 16, 32), (300, 2, 16, 16)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
     """anvil_attention_i8 over q, k (B, T, H D), v^T (B, H D, T) and o (B, T, H D), as the planner lays them out,
     bit-exact with the oracle's scores -> softmax -> P.V chain, for the quantizer's exp table, a table with a zero run,
     a non-monotone one and rows peaked on the diagonal (tiles whose p are all zero are skipped), and one = 127 or
-    100."""
+    100. T = 16 runs the one-lane-a-row kernel (four heads a wave; 300 x 2 heads leave the last wave part empty)."""
     for seed, sign, kind, one in ((0, 1, "exp", 127), (1, -1, "exp", 127), (2, 1, "random", 127), (3, 1, "steep", 100),
                                   (4, 1, "self", 127), (5, 1, "shift25", 127)):
         q, k, v, (ms, ss, mo, so), lut, want = _attention_case(B, H, T, D, causal, seed, sign, kind, one)
@@ -476,7 +478,7 @@ def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
 
 @pytest.mark.parametrize("B,H,T,D,pad", [(1, 2, 32, 16, 0), (2, 3, 64, 32, 16), (1, 3, 256, 64, 0),
                                          (1, 2, 160, 128, 32), (1, 2, 1024, 64, 0), (2, 1, 512, 16, 0),
-                                         (1, 2, 992, 64, 16)])
+                                         (1, 2, 992, 64, 16), (7, 2, 16, 16, 0), (3, 3, 16, 32, 16)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_fused_attention_keep_stores_scores_and_probabilities(dev, B, H, T, D, pad, causal):
     """anvil_attention_i8_keep: the output as anvil_attention_i8's, and every score (the whole T x T product, past
