@@ -191,10 +191,40 @@ class CompiledModel:
                 phys[op.result] = p
         for op in self.ops:
             if isinstance(op, (g.QMatmulOp, g.QLinearOp)):
+                if self._t16_chain(op):           # the T = 16 attention reads V's rows as they are
+                    continue
                 root = self._transposed_producer(op.b, phys)
                 if root is not None:
                     phys[root] = _swap_last2(len(g.qt(root).dims))
         return phys
+
+    def _chain_of(self, o_op):
+        """(scores matmul, softmax) when o_op is the P.V product of a chain the fused attention evaluates (the
+        structure only: proven, int8 throughout, scores and p read by nothing else, square scores with T a multiple
+        of 32 up to 1024 and a head dim of 16, 32, 64 or 128, or T = 16 and a head dim of 16 or 32), else None."""
+        if not self.proven or not isinstance(o_op, g.QMatmulOp) or o_op.lut is not None:
+            return None
+        if g.qt(o_op.result).dtype != "i8":
+            return None
+        sm = o_op.a.owner
+        if not isinstance(sm, g.SoftmaxLutOp) or g.qt(sm.result).dtype != "i8" or not 1 <= int(sm.one) <= 127:
+            return None
+        s_op = sm.x.owner
+        if (not isinstance(s_op, g.QMatmulOp) or s_op.lut is not None or g.qt(s_op.result).dtype != "i8"
+                or not self._softmax_lut_ok(sm)):
+            return None
+        if any(v in self.is_const or self.users.get(v, []) != [u] for v, u in ((s_op.result, sm), (sm.result, o_op))):
+            return None
+        sd, od = g.qt(s_op.result).dims, g.qt(o_op.result).dims
+        T, D = sd[-1], g.qt(s_op.a).dims[-1]
+        if (sd[-2] != T or (T % 32 and T != 16) or T > 1024 or D not in (16, 32, 64, 128) or (T == 16 and D > 32)
+                or od[-1] != D or od[-2] != T):
+            return None
+        return s_op, sm
+
+    def _t16_chain(self, o_op) -> bool:
+        chain = self._chain_of(o_op)
+        return chain is not None and g.qt(chain[0].result).dims[-1] == 16
 
     def _const_array(self, v):
         """The int64 values of a graph const, None for a computed value."""
@@ -399,23 +429,9 @@ class CompiledModel:
             return {}
         found = {}
         for o_op in self.ops:
-            if not isinstance(o_op, g.QMatmulOp) or o_op.lut is not None or g.qt(o_op.result).dtype != "i8":
-                continue
-            sm = o_op.a.owner
-            if not isinstance(sm, g.SoftmaxLutOp) or g.qt(sm.result).dtype != "i8" or not 1 <= int(sm.one) <= 127:
-                continue
-            s_op = sm.x.owner
-            if (not isinstance(s_op, g.QMatmulOp) or s_op.lut is not None or g.qt(s_op.result).dtype != "i8"
-                    or not self._softmax_lut_ok(sm)):
-                continue
-            if any(v in self.is_const or self.users.get(v, []) != [u] for v, u in ((s_op.result, sm), (sm.result, o_op))):
-                continue
-            sd, od = g.qt(s_op.result).dims, g.qt(o_op.result).dims
-            T, D = sd[-1], g.qt(s_op.a).dims[-1]
-            if (sd[-2] != T or (T % 32 and T != 16) or T > 1024 or D not in (16, 32, 64, 128) or (T == 16 and D > 32)
-                    or od[-1] != D or od[-2] != T):
-                continue
-            found[o_op] = (s_op, sm)
+            chain = self._chain_of(o_op)
+            if chain is not None:
+                found[o_op] = chain
         return found
 
     def _kept_chain(self, s_op, sm, keep) -> bool:
@@ -430,6 +446,10 @@ class CompiledModel:
         qa = views[s_op.a]
         kb = views[s_op.b].permute(_swap_last2(n))           # key rows (..., T, d)
         vb = views[o_op.b].permute(_swap_last2(n))           # V^T rows (..., d, T)
+        T0 = g.qt(s_op.result).dims[-1]
+        vrows = T0 == 16 and vb.strides[-1] != 1 and views[o_op.b].strides[-1] == 1
+        if vrows:                                           # the T = 16 kernel takes V's own rows (..., T, d)
+            vb = views[o_op.b]
         om = self._merged_heads(o_op)
         if om is not None and om in P.kb_values:
             # o written head-blocked: om's K-blocked storage (block = head), split into heads and permuted back to
@@ -458,10 +478,11 @@ class CompiledModel:
             T, D = qa.dims[-2], qa.dims[-1]
             # K and V^T go through 32-bit buffer offsets over one head: rows at least D (keys) / T (V^T) apart; O's
             # 32-row tiles through 32-bit offsets too
+            vrow_len, vrows_n = (D, T) if vrows else (T, D)   # V rows (T of D keys' values) or V^T rows
             fits = (all(st % 16 == 0 for st in strides[:9]) and all(st % 4 == 0 for st in strides[9:12])
                     and all(o % 16 == 0 for o in offs[:3]) and offs[3] % 4 == 0
-                    and strides[5] >= D and strides[8] >= T and T * strides[5] < 1 << 31 and D * strides[8] < 1 << 31
-                    and strides[11] >= D and 32 * strides[11] < 1 << 31)
+                    and strides[5] >= D and strides[8] >= vrow_len and T * strides[5] < 1 << 31
+                    and vrows_n * strides[8] < 1 << 31 and strides[11] >= D and 32 * strides[11] < 1 << 31)
             if kept:                     # S and P: 16-byte stores into 32-row tiles through 32-bit offsets
                 fits = (fits and all(st % 16 == 0 for st in strides[12:]) and all(o % 16 == 0 for o in offs[4:])
                         and all(T <= st and 32 * st < 1 << 31 for st in (strides[14], strides[17])))
@@ -475,7 +496,7 @@ class CompiledModel:
                                      out=out)
         b0, b1 = [1 if i is None else lead[i] for i in idx]
         T, D = qa.dims[-2], qa.dims[-1]
-        flags = rt.OP_UNCHECKED
+        flags = rt.OP_UNCHECKED | (rt.ATTN_V_ROWS if vrows else 0)
         if self.acc_bounds.get(s_op.result, 1 << 31) < (1 << 23) and abs(int(s_op.M)) < (1 << 23):
             flags |= rt.ATTN_S24
         if kept:

@@ -32,7 +32,7 @@ _ERRORS = {1: ValueError, 2: OverflowError, 3: ZeroDivisionError, 4: RuntimeErro
 GEMM_UNCHECKED, GEMM_CAUSAL_SKIP, GEMM_CAUSAL_K, GEMM_MUL24, GEMM_SPLITK = 1, 2, 4, 8, 16
 GEMM_A_KBLOCK, GEMM_B_KBLOCK, GEMM_C_KBLOCK = 32, 64, 128
 # anvil_rmsnorm_int_ex / anvil_softmax_lut_ex / anvil_attention_i8 flags
-OP_UNCHECKED, ATTN_S24, RMS_S24, RMS_OUT_KBLOCK = 1, 2, 2, 4
+OP_UNCHECKED, ATTN_S24, RMS_S24, RMS_OUT_KBLOCK, ATTN_V_ROWS = 1, 2, 2, 4, 4
 
 _p, _i, _i64, _i32, _sz, _f64 = C.c_void_p, C.c_int, C.c_int64, C.c_int32, C.c_size_t, C.c_double
 # symbol -> argtypes (restype int for all but anvil_last_error), in include/anvil_mi355x.h order

@@ -66,6 +66,7 @@ struct AttnArgs {
   int8_t* Pr;
   long long sc0, sc1, ldsc, pr0, pr1, ldpr;
   int ldsc32, ldpr32, scbytes, prbytes;
+  int vrows;           // T = 16 only: V given as its (T, D) rows (strides sv0, sv1, ldv) instead of V^T
 };
 
 // n / d for a uniform n < 2^32 by one 64-bit multiply-high (scalar ALU): with m = ceil(2^(32+k) / d) and 2^k >= d,
@@ -522,7 +523,8 @@ __global__ __launch_bounds__(A_THREADS) void attention_t16(AttnArgs a, int nhead
   constexpr int W = A_THREADS / 64;
   __shared__ int lut_s[256];
   __shared__ __attribute__((aligned(16))) v4i kst[W][64][DC];   // lane l's k row, chunk c
-  __shared__ __attribute__((aligned(16))) v4i vst[W][64][DC];   // lane l's V^T rows i + 16 c (one 16-byte row each)
+  // V^T of the wave's four heads: row d of head h (the 16 keys' values of dim d) at vst[w][h][d]
+  __shared__ __attribute__((aligned(16))) int8_t vst[W][4][16 * DC][16];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int hl = lane >> 4, i = lane & 15;
   const long long hh = ((long long)blockIdx.x * W + w) * 4 + hl;          // (batch, head) of this lane
@@ -537,7 +539,19 @@ __global__ __launch_bounds__(A_THREADS) void attention_t16(AttnArgs a, int nhead
   for (int c = 0; c < DC; ++c) {
     qv[c] = live ? *reinterpret_cast<const v4i*>(Qr + 16 * c) : v4i{0, 0, 0, 0};
     kst[w][lane][c] = live ? *reinterpret_cast<const v4i*>(Kr + 16 * c) : v4i{0, 0, 0, 0};
-    vst[w][lane][c] = live ? *reinterpret_cast<const v4i*>(Vr + 16 * c * a.ldv) : v4i{0, 0, 0, 0};
+  }
+  if (a.vrows) {                                   // lane i holds V row i (key i): its D bytes go to column i
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      const v4i vr = live ? *reinterpret_cast<const v4i*>(Vr + 16 * c) : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int b = 0; b < 16; ++b) vst[w][hl][16 * c + b][i] = (int8_t)(vr[b >> 2] >> (8 * (b & 3)));
+    }
+  } else {                                         // lane i holds V^T rows i and 16 + i
+#pragma unroll
+    for (int c = 0; c < DC; ++c)
+      *reinterpret_cast<v4i*>(vst[w][hl][i + 16 * c]) =
+          live ? *reinterpret_cast<const v4i*>(Vr + 16 * c * a.ldv) : v4i{0, 0, 0, 0};
   }
   __syncthreads();
   // scores of the row, clamped in the pre-shift domain, and the row max over the kept keys
@@ -575,11 +589,11 @@ __global__ __launch_bounds__(A_THREADS) void attention_t16(AttnArgs a, int nhead
   v4i pp;
 #pragma unroll
   for (int g = 0; g < 4; ++g) pp[g] = (int)pack4(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]);
-  // O row: 16 DC dims, each the dot of p with V^T row d (lane 16 hl + (d % 16)'s chunk d / 16)
+  // O row: 16 DC dims, each the dot of p with V^T row d
   int ov[16 * DC];
 #pragma unroll
   for (int d = 0; d < 16 * DC; ++d) {
-    const v4i vd = vst[w][16 * hl + (d & 15)][d >> 4];
+    const v4i vd = *reinterpret_cast<const v4i*>(vst[w][hl][d]);
     int acc = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_sdot4(pp[q], vd[q], acc, false);
@@ -622,8 +636,10 @@ static int attention_entry(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, con
                            int flags) {
   if (!Q || !K || !Vt || !O || !strides || !lut || (keep && (!S || !P)))
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: null pointer");
-  if (!(flags & ANVIL_OP_UNCHECKED) || (flags & ~(ANVIL_OP_UNCHECKED | ANVIL_ATTN_S24)))
+  if (!(flags & ANVIL_OP_UNCHECKED) || (flags & ~(ANVIL_OP_UNCHECKED | ANVIL_ATTN_S24 | ANVIL_ATTN_V_ROWS)))
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: flags must hold ANVIL_OP_UNCHECKED (a proven graph)");
+  const bool vrows = flags & ANVIL_ATTN_V_ROWS;
+  if (vrows && T != 16) return set_error(ANVIL_E_VALUE, "anvil_attention_i8: ANVIL_ATTN_V_ROWS needs T = 16");
   if (batch0 < 1 || batch1 < 1 || (T != 16 && (T < 32 || T % 32 || T > 1024)))
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: T=%d must be 16 or a multiple of 32 in [32, 1024]", T);
   if (D != 16 && D != 32 && D != 64 && D != 128)
@@ -645,7 +661,8 @@ static int attention_entry(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, con
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: too many heads");
   // K and V^T are read through 32-bit buffer offsets over one head: T key rows of stride ldk (each at least D
   // bytes apart), D rows of V^T of stride ldv (each at least T keys)
-  if (st[5] < D || st[8] < T || (long long)T * st[5] >= (1ll << 31) || (long long)D * st[8] >= (1ll << 31))
+  if (st[5] < D || st[8] < (vrows ? D : T) || (long long)T * st[5] >= (1ll << 31) ||
+      (long long)(vrows ? T : D) * st[8] >= (1ll << 31))
     return set_error(ANVIL_E_VALUE, "anvil_attention_i8: K row stride %lld / V^T row stride %lld out of range",
                      (long long)st[5], (long long)st[8]);
   if (st[11] < D || 32 * st[11] >= (1ll << 31))   // a 32-row output tile is stored through 32-bit offsets
@@ -693,6 +710,7 @@ static int attention_entry(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, con
   magic(std::max(1, a.nqt), a.mq, a.kq);
   magic(batch1, a.mb, a.kb);
   magic(one, a.mone, a.kone);
+  a.vrows = vrows ? 1 : 0;
   a.Sc = S;
   a.Pr = P;
   if (keep) {

@@ -239,9 +239,11 @@ int anvil_softmax_lut_ex(anvil_ctx* ctx, const int8_t* x, const int32_t* lut, in
  * T * ldk, D * ldv, 32 * ldo below 2^31 (one head of K and of Vt is read, and 32 rows of O are written, through
  * 32-bit offsets). T a multiple of 32 in [32, 1024];
  * D in {16, 32, 64, 128}; 1 <= one <= 127; lut int32[256] with every entry >= 0 and lut[255] >= 1.
+ * T may also be 16, with D 16 or 32 (one lane a query row); then ANVIL_ATTN_V_ROWS passes V itself, (T, D) rows of
+ * stride ldv >= D, in place of V^T.
  * flags must hold ANVIL_OP_UNCHECKED: the caller has proven every int32 intermediate of the three ops in range;
  * ANVIL_ATTN_S24 adds that every |Q K^T| and |m_s| is below 2^23 (the score requant multiply is then 24-bit). */
-enum anvil_attn_flags { ANVIL_ATTN_S24 = 2 };
+enum anvil_attn_flags { ANVIL_ATTN_S24 = 2, ANVIL_ATTN_V_ROWS = 4 };
 int anvil_attention_i8(anvil_ctx* ctx, const int8_t* Q, const int8_t* K, const int8_t* Vt, int8_t* O, int batch0,
                        int batch1, int T, int D, const int64_t* strides, int32_t m_s, int s_s, const int32_t* lut,
                        int32_t one, int causal, int32_t m_o, int s_o, int flags);

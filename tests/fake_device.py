@@ -237,13 +237,21 @@ class FakeDevice:
                 self._store_result(Cp, dt, b0, b1, M, N, (sc0, sc1, ldc), flags & rt.GEMM_C_KBLOCK, out[0])
             self.store(D, dt, (b0, b1, M, N), (sd0, sd1, ldd, 1), out[1])
 
+    def _vt(self, Vt, b0, b1, T, D, st, flags):
+        """The attention's V^T operand: given as V^T rows, or (ATTN_V_ROWS, T = 16 only) as V's own rows."""
+        if flags & rt.ATTN_V_ROWS:
+            assert T == 16, "V rows are for the T = 16 kernel"
+            v = self.view(Vt, "i8", (b0, b1, T, D), (st[6], st[7], st[8], 1)).astype(np.int64)
+            return np.swapaxes(v, -1, -2)
+        return self.view(Vt, "i8", (b0, b1, D, T), (st[6], st[7], st[8], 1)).astype(np.int64)
+
     def attention_i8(self, Q, K, Vt, O, b0, b1, T, D, strides, ms, ss, lut, one, causal, mo, so, flags):
         """The three ops the fused kernel replaces, over the same strided operands."""
         self.calls.append(("attention", b0, b1, T, D, tuple(strides), flags))
         st = strides
         q = self.view(Q, "i8", (b0, b1, T, D), (st[0], st[1], st[2], 1)).astype(np.int64)
         k = self.view(K, "i8", (b0, b1, T, D), (st[3], st[4], st[5], 1)).astype(np.int64)
-        vt = self.view(Vt, "i8", (b0, b1, D, T), (st[6], st[7], st[8], 1)).astype(np.int64)
+        vt = self._vt(Vt, b0, b1, T, D, st, flags)
         lv = self.view(lut, "i32", (256,), (1,)).astype(np.int64)
 
         def chain():
@@ -260,7 +268,7 @@ class FakeDevice:
         st = strides
         q = self.view(Q, "i8", (b0, b1, T, D), (st[0], st[1], st[2], 1)).astype(np.int64)
         k = self.view(K, "i8", (b0, b1, T, D), (st[3], st[4], st[5], 1)).astype(np.int64)
-        vt = self.view(Vt, "i8", (b0, b1, D, T), (st[6], st[7], st[8], 1)).astype(np.int64)
+        vt = self._vt(Vt, b0, b1, T, D, st, flags)
         lv = self.view(lut, "i32", (256,), (1,)).astype(np.int64)
 
         def chain():

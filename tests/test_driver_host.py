@@ -334,6 +334,10 @@ def test_wide_frozen_model_fuses_its_i16_residual_adds(fake, keep):
     assert kinds.count("add") == 0 and len(adds) == n_add and all(c[-1] == "i16" for c in adds)
     # the products' own i16 results are stored only when they are returned
     assert all(c[8] == (keep == "all") for c in adds)
+    # T = 16: the fused attention reads v's own rows, so v is one plain product grouped with q and k
+    att = [c for c in fake.calls if c[0] in ("attention", "attention_keep")]
+    assert len(att) == 2 and all(c[3] == 16 and c[-1] & rt.ATTN_V_ROWS for c in att)
+    assert kinds.count("gemm_group") == 4 and ("gemm_group", 3) in fake.calls
 
 
 def test_gemm_operands_are_planned_kblocked(fake, cfg1):

@@ -474,6 +474,13 @@ def test_fused_attention_matches_the_three_ops(dev, B, H, T, D, causal):
         dev.sync()
         got = out.download((B, T, C), np.int8).astype(np.int64)
         assert np.array_equal(got, want), (seed, kind, np.argwhere(got != want)[:5])
+        if T == 16:                                         # V's own rows (ATTN_V_ROWS) in place of V^T
+            out2 = dev.alloc(B * T * C)
+            strides_v = strides[:6] + [T * C, D, C] + strides[9:]
+            dev.attention_i8(up(dev, q, "i8"), up(dev, k, "i8"), up(dev, v, "i8"), out2, B, H, T, D, strides_v, ms, ss,
+                             up(dev, lut, "i32"), one, causal, mo, so, rt.OP_UNCHECKED | rt.ATTN_V_ROWS)
+            dev.sync()
+            assert np.array_equal(out2.download((B, T, C), np.int8).astype(np.int64), want), (seed, kind, "V rows")
 
 
 @pytest.mark.parametrize("B,H,T,D,pad", [(1, 2, 32, 16, 0), (2, 3, 64, 32, 16), (1, 3, 256, 64, 0),
