@@ -1385,6 +1385,188 @@ static void launch_small(GemmArgs& g, int osz, hipStream_t s) {
     ANVIL_LAUNCH((gemm_i8_small<2, MUL24>), grid, dim3(SMALL_SK * 256), 0, s, g);
 }
 
+// Narrow products over many rows: K and N each 32 or 64 (the reference's frozen models, C = 32: q, k, v, y with
+// its residual add, gate, up, down), where a 128-row tile leaves most of every MFMA and of its operand loads unused.
+// One wave takes a block of 32 rows at a time (walking blocks grid-stride, the next block's rows loading during
+// this one's epilogue): its A rows load as MFMA fragments (lane l: row l % 32, 16 K bytes at 16 (l / 32) + 32 k,
+// 1 KiB contiguous for a dense 32-byte row), the weights' fragments stay in registers for the whole walk, and up to
+// four products that share A (q, k and v of one input) run in the same pass. B rows enter the MFMA in bperm order,
+// so a lane's 16 accumulators are 16 consecutive columns of its row: one 16-byte store (i8), or two (i16).
+// RES: the fused add_requant of anvil_gemm_i8_add (one member): D = clamp((R ma + y mb + rnd2) >> shift2) in the
+// result's dtype, y stored when store_y.
+struct SkinnyArgs {
+  GemmArgs g[GEMM_GROUP_MAX];
+  int n;                  // members, sharing A, M and K
+  int nblocks;            // blocks of 32 rows
+};
+
+template <int NT, int KS, int OSZ, bool MUL24, bool RES>
+__global__ __launch_bounds__(G_THREADS) void gemm_i8_skinny(SkinnyArgs sa) {
+  __shared__ int8_t lut_s[GEMM_GROUP_MAX][256];
+  const int t = threadIdx.x, lane = t & 63;
+  const int l32 = lane & 31, half = lane >> 5;
+  const GemmArgs& g0 = sa.g[0];
+#pragma unroll
+  for (int j = 0; j < GEMM_GROUP_MAX; ++j)
+    if (j < sa.n && sa.g[j].lut) lut_s[j][t ^ 128] = sa.g[j].lut[t];   // rotated: entry of v at index v & 255
+  __syncthreads();
+  // the members' weight fragments: B row 32 nt + bperm(l32), K bytes 32 ks + 16 half
+  v4i bf[GEMM_GROUP_MAX][NT][KS];
+#pragma unroll
+  for (int j = 0; j < GEMM_GROUP_MAX; ++j)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const GemmArgs& g = sa.g[j < sa.n ? j : 0];
+        const int r = 32 * nt + bperm(l32), k = 32 * ks + 16 * half;
+        bf[j][nt][ks] = j < sa.n && r < g.N && k < g.K
+                            ? *reinterpret_cast<const v4i*>(g.B + (long long)r * g.ldb + (k >> 6) * g.kbb + (k & 63))
+                            : v4i{0, 0, 0, 0};
+      }
+  const __amdgpu_buffer_rsrc_t ra = uniform_rsrc(g0.A, operand_bytes(g0.M, g0.lda, g0.kba, g0.K));
+  auto aoff = [&](int blk, int ks) -> unsigned {        // this lane's A fragment of block blk, or out of range
+    const int m = 32 * blk + l32, k = 32 * ks + 16 * half;
+    return blk < sa.nblocks && m < g0.M && k < g0.K ? (unsigned)(m * g0.lda + (k >> 6) * g0.kba + (k & 63)) : OOB;
+  };
+  const int wave = blockIdx.x * (G_THREADS / 64) + (t >> 6), nwaves = gridDim.x * (G_THREADS / 64);
+  v4i af[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    af[ks] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff(wave, ks), 0, 0));
+  constexpr int LO = OSZ == 1 ? -128 : -32768, HI = OSZ == 1 ? 127 : 32767;
+  for (int blk = wave; blk < sa.nblocks; blk += nwaves) {
+    v4i an[KS];                                          // the next block's rows load during this block's work
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      an[ks] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff(blk + nwaves, ks), 0, 0));
+    const int m = 32 * blk + l32;
+#pragma unroll
+    for (int j = 0; j < GEMM_GROUP_MAX; ++j) {
+      if (j >= sa.n) break;
+      const GemmArgs& g = sa.g[j];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j][nt][ks], af[ks], acc, 0, 0, 0);
+        const int n = 32 * nt + 16 * half;
+        if (m >= g0.M || n >= g.N) continue;
+        int v[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int x = MUL24 ? (__mul24(acc[r], g.mult) + g.rnd) : (acc[r] * g.mult + g.rnd);
+          v[r] = min(max(x >> g.shift, LO), HI);
+        }
+        if (OSZ == 1 && g.lut) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) v[r] = lut_s[j][(uint8_t)v[r]];
+        }
+        const bool whole = n + 16 <= g.N;
+        if constexpr (RES) {                             // D = clamp((R ma + y mb + rnd2) >> shift2), proven in int32
+          int o[16];
+          if constexpr (OSZ == 1) {
+            const int8_t* rp = g.R + (long long)m * g.ldr + n;
+            v4i rv = {0, 0, 0, 0};
+            if (whole && g.vec_res) rv = *reinterpret_cast<const v4i*>(rp);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int r = whole && g.vec_res ? (int)(int8_t)((unsigned)rv[e >> 2] >> (8 * (e & 3)))
+                                               : (n + e < g.N ? (int)rp[e] : 0);
+              o[e] = min(max((r * g.ma + v[e] * g.mb + g.rnd2) >> g.shift2, LO), HI);
+            }
+          } else {
+            const int16_t* rp = reinterpret_cast<const int16_t*>(g.R) + (long long)m * g.ldr + n;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int r = n + e < g.N ? (int)rp[e] : 0;
+              o[e] = min(max((r * g.ma + v[e] * g.mb + g.rnd2) >> g.shift2, LO), HI);
+            }
+          }
+          char* dp = reinterpret_cast<char*>(g.D) + ((long long)m * g.ldd + n) * OSZ;
+          if (whole && g.vec_res) {
+            if (OSZ == 1) {
+              *reinterpret_cast<v4i*>(dp) = v4i{(int)pack4(o[0], o[1], o[2], o[3]), (int)pack4(o[4], o[5], o[6], o[7]),
+                                                (int)pack4(o[8], o[9], o[10], o[11]),
+                                                (int)pack4(o[12], o[13], o[14], o[15])};
+            } else {
+              v4i w0, w1;
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                w0[q] = (int)__builtin_amdgcn_perm((unsigned)o[2 * q + 1], (unsigned)o[2 * q], 0x05040100u);
+                w1[q] = (int)__builtin_amdgcn_perm((unsigned)o[2 * q + 9], (unsigned)o[2 * q + 8], 0x05040100u);
+              }
+              *reinterpret_cast<v4i*>(dp) = w0;
+              *reinterpret_cast<v4i*>(dp + 16) = w1;
+            }
+          } else {
+            for (int e = 0; e < 16 && n + e < g.N; ++e) {
+              if (OSZ == 1)
+                reinterpret_cast<int8_t*>(dp)[e] = (int8_t)o[e];
+              else
+                reinterpret_cast<int16_t*>(dp)[e] = (int16_t)o[e];
+            }
+          }
+          if (!g.store_y) continue;
+        }
+        char* c = reinterpret_cast<char*>(g.C) + cpos(g, m, n) * OSZ;
+        if (whole && g.vec_store) {
+          if (OSZ == 1) {
+            *reinterpret_cast<v4i*>(c) = v4i{(int)pack4(v[0], v[1], v[2], v[3]), (int)pack4(v[4], v[5], v[6], v[7]),
+                                             (int)pack4(v[8], v[9], v[10], v[11]),
+                                             (int)pack4(v[12], v[13], v[14], v[15])};
+          } else {
+            v4i w0, w1;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              w0[q] = (int)__builtin_amdgcn_perm((unsigned)v[2 * q + 1], (unsigned)v[2 * q], 0x05040100u);
+              w1[q] = (int)__builtin_amdgcn_perm((unsigned)v[2 * q + 9], (unsigned)v[2 * q + 8], 0x05040100u);
+            }
+            *reinterpret_cast<v4i*>(c) = w0;
+            *reinterpret_cast<v4i*>(c + 16) = w1;
+          }
+        } else {
+          for (int e = 0; e < 16 && n + e < g.N; ++e) {
+            if (OSZ == 1)
+              reinterpret_cast<int8_t*>(g.C)[cpos(g, m, n + e)] = (int8_t)v[e];
+            else
+              reinterpret_cast<int16_t*>(g.C)[cpos(g, m, n + e)] = (int16_t)v[e];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) af[ks] = an[ks];
+  }
+}
+
+// Whether a fast-path product (one member of a group, or the product of a fused add) takes gemm_i8_skinny: batch 1, no
+// causal mode or split, K and N each 32 or 64, at least 4096 rows.
+static bool skinny_ok(const GemmArgs& g, int batch) {
+  return batch == 1 && g.causal == 0 && (g.K == 32 || g.K == 64) && (g.N == 32 || g.N == 64) && g.M >= 4096 &&
+         (long long)g.M * g.lda < (1ll << 31);
+}
+
+template <bool MUL24>
+static void launch_skinny(const GemmArgs* gs, int n, int osz, int num_cu, hipStream_t s) {
+  SkinnyArgs sa;
+  for (int i = 0; i < n; ++i) sa.g[i] = gs[i];
+  for (int i = n; i < GEMM_GROUP_MAX; ++i) sa.g[i] = gs[0];
+  sa.n = n;
+  sa.nblocks = (gs[0].M + 31) / 32;
+  const int nt = (gs[0].N + 31) / 32, ks = (gs[0].K + 31) / 32;
+  const bool res = gs[0].res != 0;
+  const dim3 grid((unsigned)std::min<long long>((sa.nblocks + 3) / 4, 8ll * num_cu));
+  auto go = [&](auto kernel) { ANVIL_LAUNCH(kernel, grid, dim3(G_THREADS), 0, s, sa); };
+#define ANVIL_SKINNY(NT, KS, OSZ, RES) \
+  if (nt == NT && ks == KS && osz == OSZ && res == RES) return go(gemm_i8_skinny<NT, KS, OSZ, MUL24, RES>);
+  ANVIL_SKINNY(1, 1, 1, false) ANVIL_SKINNY(1, 2, 1, false) ANVIL_SKINNY(2, 1, 1, false) ANVIL_SKINNY(2, 2, 1, false)
+  ANVIL_SKINNY(1, 1, 2, false) ANVIL_SKINNY(1, 2, 2, false) ANVIL_SKINNY(2, 1, 2, false) ANVIL_SKINNY(2, 2, 2, false)
+  ANVIL_SKINNY(1, 1, 1, true) ANVIL_SKINNY(1, 2, 1, true) ANVIL_SKINNY(2, 1, 1, true) ANVIL_SKINNY(2, 2, 1, true)
+  ANVIL_SKINNY(1, 1, 2, true) ANVIL_SKINNY(1, 2, 2, true) ANVIL_SKINNY(2, 1, 2, true) ANVIL_SKINNY(2, 2, 2, true)
+#undef ANVIL_SKINNY
+}
+
 // Whether a fast-path product takes gemm_i8_small: one product (batch 1, no causal mode, no fused add) whose 128 x 128
 // tiles fill at most a quarter of the CUs, with K >= 512.
 static bool small_plan(const GemmArgs& g, int batch, int num_cu) {
@@ -1735,6 +1917,13 @@ static int gemm_launch(anvil_ctx* ctx, Prepared& p, bool noalloc = false) {
     return ANVIL_OK;
   }
   int splits = 0, kchunk = 0;
+  if (!p.force_split && !ctx->gemm_cfg && skinny_ok(p.g, p.batch)) {
+    if (p.mul24)
+      launch_skinny<true>(&p.g, 1, p.osz, ctx->num_cu, ctx->stream);
+    else
+      launch_skinny<false>(&p.g, 1, p.osz, ctx->num_cu, ctx->stream);
+    return ANVIL_OK;
+  }
   if (!p.force_split && !ctx->gemm_cfg && small_plan(p.g, p.batch, ctx->num_cu)) {
     if (p.mul24)
       launch_small<true>(p.g, p.osz, ctx->stream);
@@ -1799,6 +1988,22 @@ extern "C" int anvil_gemm_i8_group(anvil_ctx* ctx, const anvil_gemm_desc* d, int
     if (int r = gemm_prepare(ctx, d[i].A, d[i].Bt, d[i].C, d[i].batch0, d[i].batch1, d[i].M, d[i].N, d[i].K,
                              d[i].strides, d[i].mult, d[i].shift, d[i].lut, d[i].out_dtype, d[i].flags, nullptr, p[i]))
       return r;
+  // narrow products sharing their left operand (the frozen models' q, k and v; gate and up): one gemm_i8_skinny pass
+  bool skinny = count > 1 && !ctx->gemm_cfg;
+  for (int i = 0; i < count && skinny; ++i)
+    skinny = p[i].fast && !p[i].force_split && skinny_ok(p[i].g, p[i].batch) && p[i].osz == p[0].osz &&
+             p[i].mul24 == p[0].mul24 && p[i].g.A == p[0].g.A && p[i].g.lda == p[0].g.lda &&
+             p[i].g.kba == p[0].g.kba && p[i].g.M == p[0].g.M && p[i].g.K == p[0].g.K && p[i].g.N == p[0].g.N;
+  if (skinny) {
+    GemmArgs gs[GEMM_GROUP_MAX];
+    for (int i = 0; i < count; ++i) gs[i] = p[i].g;
+    if (p[0].mul24)
+      launch_skinny<true>(gs, count, p[0].osz, ctx->num_cu, ctx->stream);
+    else
+      launch_skinny<false>(gs, count, p[0].osz, ctx->num_cu, ctx->stream);
+    ANVIL_LAUNCHED();
+    return ANVIL_OK;
+  }
   // one launch when every member takes the same one-tile-per-workgroup kernel: 256 x 128 tiles, or 128 x 128 tiles
   // for smaller products (config 3's q, k and v, 256 tiles each), none of them splitting K
   int shape = 0;

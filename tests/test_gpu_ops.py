@@ -663,6 +663,44 @@ def _check_sampled_gemm(dev, M, N, K, dtype, lut, add, seed, mults=(300, -200, 9
         assert np.array_equal(d.download((M, N), np.int8)[rows].astype(np.int64), want)
 
 
+@pytest.mark.parametrize("M,N,K", [(262144, 32, 32), (4096 + 37, 64, 32), (20000 + 5, 32, 64), (8192, 64, 64)])
+@pytest.mark.parametrize("dtype,lut,add", [("i8", False, False), ("i8", True, False), ("i16", False, False),
+                                           ("i8", False, True)])
+def test_narrow_products_take_the_skinny_kernel(dev, M, N, K, dtype, lut, add):
+    """K and N each 32 or 64 with at least 4096 rows (the frozen models' layers): one wave per 32-row block, weight
+    fragments in registers; ragged row counts, the LUT epilogue, i16 results and the fused i8 residual add, checked
+    on sampled rows (the first and last 256 among them)."""
+    _check_sampled_gemm(dev, M, N, K, dtype, lut, add, 43)
+
+
+@pytest.mark.parametrize("N,K,n", [(32, 32, 3), (64, 32, 2), (32, 64, 4)])
+def test_narrow_group_shares_its_left_operand(dev, N, K, n):
+    """anvil_gemm_i8_group of narrow products reading one left operand (q, k and v of one input; gate and up): one
+    pass of the skinny kernel, every member bit-exact with the oracle, each with its own requant and one with a LUT."""
+    M = 16384 * 16 + 7
+    rng = np.random.default_rng([44, N, K, n])
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    rows = np.unique(np.concatenate([np.arange(256), np.arange(M - 256, M), rng.integers(0, M, 512)]))
+    A = up(dev, a, "i8")
+    calls, wants, outs = [], [], []
+    for j in range(n):
+        w = rng.integers(-128, 128, (K, N), dtype=np.int8)
+        acc = sem.matmul_i8(a[rows].astype(np.int64), w.astype(np.int64), fast=True)
+        s = 18 + j
+        m = int(min(((1 << 31) - 1 - (1 << (s - 1))) // int(np.abs(acc).max() * 2), (1 << 23) - 1))
+        L = rng.integers(-128, 128, 256) if j == 1 else None
+        wants.append(sem.qmatmul(a[rows].astype(np.int64), w.astype(np.int64), m, s, L, fast=True))
+        c = dev.alloc(M * N)
+        outs.append(c)
+        calls.append((A, up(dev, np.ascontiguousarray(w.T), "i8"), c, 1, 1, M, N, K, [0, 0, K, 0, 0, K, 0, 0, N], m, s,
+                      None if L is None else up(dev, L, "i8"), "i8", rt.GEMM_UNCHECKED | rt.GEMM_MUL24))
+    dev.gemm_i8_group(calls)
+    dev.sync()
+    for j in range(n):
+        got = outs[j].download((M, N), np.int8)[rows].astype(np.int64)
+        assert np.array_equal(got, wants[j]), (j, np.argwhere(got != wants[j])[:5])
+
+
 # members (M, N, K, batch, A shared by the batch entries, LUT): q / k / v of the block (v computed transposed, per
 # sequence, with the weight as the shared left operand), ragged rows and columns, tile counts that are not multiples
 # of 8 (padding workgroups between members), and a group whose members take different kernels (one launch each)
