@@ -238,6 +238,7 @@ def bench_block(args):
                            "times below; the fused attention kernel's time, softmax included, counts as GEMM time"},
         "roofline": roof,
         "roofline_next": roof2,
+        "hbm_stream": stream,
         "launch": {"mode": mode, "eager_ms_per_step": round(eager_ms, 4),
                    "graph_ms_per_step": graph["ms_per_step"], "steps": K,
                    "covers": "value and ms_per_step: the faster of the two timed regions, each K steps between device "
