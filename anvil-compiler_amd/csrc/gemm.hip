@@ -356,12 +356,21 @@ __device__ __forceinline__ unsigned sra_byte(int x, int sh) {
   return d;
 }
 
-// requant (+ LUT) of one lane's 16 accumulators into 16 results. With a LUT (int8 results, the table staged rotated
-// so that the entry of v sits at index v & 255) the clamp runs before the shift, with bounds [-128, 127] << shift
-// saturated to int32, and one SDWA shift gives the lookup index.
-template <int OSZ, bool MUL24, bool LUT>
+// requant (+ LUT) of one lane's 16 accumulators into 16 results. With the rotated LUT (LUT 1: int8 results, the
+// table staged so that the entry of v sits at index v & 255) the clamp runs before the shift, with bounds
+// [-128, 127] << shift saturated to int32, and one SDWA shift gives the lookup index. The widened table (LUT 2, entry
+// u = lut[clamp(u - 2^(31 - shift), -128, 127) + 128]) is indexed by (x + 2^31) >> shift, unsigned.
+template <int OSZ, bool MUL24, int LUT>
 __device__ __forceinline__ void requant16(const v16i& a, int mult, int rnd, int shift, const int8_t* lut_s, int v[16]) {
-  if constexpr (LUT) {
+  if constexpr (LUT == 2) {
+    static_assert(OSZ == 1, "a LUT epilogue has int8 results");
+    const unsigned rndw = (unsigned)rnd ^ 0x80000000u;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const unsigned u = (unsigned)(MUL24 ? __mul24(a[e], mult) : a[e] * mult) + rndw;
+      v[e] = lut_s[u >> shift];
+    }
+  } else if constexpr (LUT == 1) {
     static_assert(OSZ == 1, "a LUT epilogue has int8 results");
     const int clo = (int)max(-128ll << shift, (long long)INT32_MIN);
     const int chi = (int)min((128ll << shift) - 1, (long long)INT32_MAX);
@@ -385,7 +394,7 @@ __device__ __forceinline__ void requant16(const v16i& a, int mult, int rnd, int 
 // issue every residual load first, then requantize and store 16 bytes a lane; edge tiles store element by element.
 template <int BM, int BN, int WM, int WN, int TM, int TN, int OSZ, bool MUL24>
 __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&acc)[TN][TM], const int8_t* lut_s,
-                                                int mrow, int ncol, int m0, int n0, int b0, int b1) {
+                                                bool wide, int mrow, int ncol, int m0, int n0, int b0, int b1) {
   char* Cb = reinterpret_cast<char*>(g.C) + (b0 * g.sc0 + b1 * g.sc1) * OSZ;
   const bool res = OSZ == 1 && g.res;
   const int8_t* Rb = g.R + b0 * g.sr0 + b1 * g.sr1;
@@ -394,7 +403,8 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
                         (res ? (g.vec_res != 0 && (!g.store_y || g.vec_store != 0)) : g.vec_store != 0);
   const int mult = g.mult, rnd = g.rnd, shift = g.shift;
   auto run = [&](auto lut_c, auto full_c) {
-    constexpr bool LUT = decltype(lut_c)::value, FULL = decltype(full_c)::value;
+    constexpr int LUT = decltype(lut_c)::value;
+    constexpr bool FULL = decltype(full_c)::value;
     v4i rv[TM][TN];
     if (FULL && res) {
 #pragma unroll
@@ -469,11 +479,68 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
   const bool lut = OSZ == 1 && g.lut;
   auto pick = [&](auto full_c) {
     if constexpr (OSZ == 1) {
-      if (lut) return run(std::true_type{}, full_c);
+      if (lut && wide) return run(std::integral_constant<int, 2>{}, full_c);
+      if (lut) return run(std::integral_constant<int, 1>{}, full_c);
     }
-    run(std::false_type{}, full_c);
+    run(std::integral_constant<int, 0>{}, full_c);
   };
   if (interior) pick(std::true_type{}); else pick(std::false_type{});
+}
+
+// Bytes of the persistent kernel's lookup table: the largest power of two up to 32 KiB that fits beside `stages`
+// bytes of pipeline stages in the 160 KiB of LDS.
+constexpr int table_bytes(int stages) {
+  int b = 32768;
+  while (b > 256 && stages + b > 160 * 1024) b >>= 1;
+  return b;
+}
+
+// The register epilogue of an interior tile with int8 results and no fused add, one group at a time: requant (+ LUT)
+// and one 16-byte store a group at p + the group's offset. A LUT widened to the whole range of x >> shift (WIDE,
+// the table's entry u holding lut[clamp(u - 2^(31 - shift), -128, 127)]) takes its index as (x + 2^31) >> shift,
+// unsigned: the 2^31 rides in the rounding constant, and no clamp is needed, as the proof keeps x inside int32.
+// Without a LUT the clamp runs before the shift and one SDWA shift writes each byte of the packed dword.
+template <int TM, int TN, bool MUL24, int MODE>   // MODE 0: no LUT, 1: the rotated 256-entry LUT, 2: WIDE
+__device__ __forceinline__ void plain_epilogue(const GemmArgs& g, const v16i (&acc)[TN][TM], const uint8_t* tab,
+                                               int8_t* p) {
+  const int mult = g.mult, shift = g.shift;
+  const int clo = (int)max(-128ll << shift, (long long)INT32_MIN);
+  const int chi = (int)min((128ll << shift) - 1, (long long)INT32_MAX);
+  const unsigned rndw = (unsigned)g.rnd ^ 0x80000000u;
+#pragma unroll
+  for (int j = 0; j < TM; ++j)
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+      const v16i& a = acc[i][j];
+      v4i w;
+      if constexpr (MODE == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          int x[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            x[e] = med3i(MUL24 ? __mul24(a[4 * q + e], mult) + g.rnd : a[4 * q + e] * mult + g.rnd, clo, chi);
+          w[q] = (int)sra_pack4(x[0], x[1], x[2], x[3], shift);
+        }
+      } else {
+        int v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if constexpr (MODE == 2) {
+            const unsigned u = (unsigned)(MUL24 ? __mul24(a[e], mult) : a[e] * mult) + rndw;
+            v[e] = tab[u >> shift];
+          } else {
+            const int x = MUL24 ? (__mul24(a[e], mult) + g.rnd) : (a[e] * mult + g.rnd);
+            v[e] = tab[sra_byte(med3i(x, clo, chi), shift)];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w[q] = (int)pack4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+      }
+      // group (i, j): row + 32 j, column + 32 i; a wave's columns start at a multiple of 64 (+ 16 for the upper
+      // half-wave), so column + 32 i lies in 64-column block i / 2 at offset 32 (i % 2)
+      *reinterpret_cast<v4i*>(p + 32 * j * g.ldc + (i >> 1) * g.kbc + 32 * (i & 1)) = w;
+    }
 }
 
 // One output tile of the fast kernel: logical tile pid of batch entry bz (the XCD remap below assumes pid and the
@@ -982,8 +1049,10 @@ __global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) voi
   static_assert(IA % NW == 0 && IB % NW == 0, "each wave issues an equal share of a stage");
   constexpr int JA = IA / NW, JB = IB / NW, G = JA + JB;
   constexpr int STAGE = (BM + BN) * BK;
-  // the LUT first, at a low LDS address that a lookup's offset field can hold (past the stages it would not fit)
-  __shared__ __attribute__((aligned(2048))) int8_t lut_s[256];
+  // the LUT first, at LDS address 0 (an alignment above the stages' puts it first), so that a lookup's address is
+  // its index: the 256-entry table rotated, or widened to TAB entries (plain_epilogue)
+  constexpr int TAB = table_bytes(NS * STAGE);
+  __shared__ __attribute__((aligned(2048))) int8_t lut_s[TAB];
   __shared__ __attribute__((aligned(1024))) int8_t L0[STAGE];
   __shared__ __attribute__((aligned(1024))) int8_t L1[STAGE];
   __shared__ __attribute__((aligned(1024))) int8_t L2[NS > 2 ? STAGE : 16];
@@ -1040,7 +1109,14 @@ __global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) voi
 
   Tile cur = tile_of(0);
   if (!cur.valid) return;
-  if (g.lut && t < 256) lut_s[t ^ 128] = g.lut[t];   // rotated: the entry of v at index v & 255
+  // a table of 2^(32 - shift) entries fits: widened, entry u = lut[clamp(u - 2^(31 - shift), -128, 127) + 128]
+  const bool wide = OSZ == 1 && g.lut && g.shift >= 1 && g.shift <= 31 && (1ll << (32 - g.shift)) <= TAB;
+  if (wide) {
+    const int n = 1 << (32 - g.shift), mid = 1 << (31 - g.shift);
+    for (int u = t; u < n; u += NW * 64) lut_s[u] = g.lut[min(max(u - mid, -128), 127) + 128];
+  } else if (g.lut && t < 256) {
+    lut_s[t ^ 128] = g.lut[t];   // rotated: the entry of v at index v & 255
+  }
 
   unsigned offa[JA], offb[JB];
   int ka[JA], kb[JB];
@@ -1136,8 +1212,19 @@ __global__ __launch_bounds__(NW * 64, (persist_occupancy<BM, BN, BK, NS>())) voi
              ran, rbn);
       });
     }
-    direct_epilogue<BM, BN, WM, WN, TM, TN, OSZ, MUL24>(g, acc, lut_s, cur.m0 + wm * WM + l32,
-                                                        cur.n0 + wn * WN + 16 * half, cur.m0, cur.n0, cur.b0, cur.b1);
+    const int mrow = cur.m0 + wm * WM + l32, ncol = cur.n0 + wn * WN + 16 * half;
+    if (OSZ == 1 && !g.res && g.vec_store != 0 && cur.m0 + BM <= g.M && cur.n0 + BN <= g.N) {
+      if constexpr (OSZ == 1) {
+        int8_t* p = reinterpret_cast<int8_t*>(g.C) + cur.b0 * g.sc0 + cur.b1 * g.sc1 + cpos(g, mrow, ncol);
+        const uint8_t* tab = reinterpret_cast<const uint8_t*>(lut_s);
+        if (wide) plain_epilogue<TM, TN, MUL24, 2>(g, acc, tab, p);
+        else if (g.lut) plain_epilogue<TM, TN, MUL24, 1>(g, acc, tab, p);
+        else plain_epilogue<TM, TN, MUL24, 0>(g, acc, tab, p);
+      }
+    } else {
+      direct_epilogue<BM, BN, WM, WN, TM, TN, OSZ, MUL24>(g, acc, lut_s, wide, mrow, ncol, cur.m0, cur.n0, cur.b0,
+                                                          cur.b1);
+    }
     if (!nt.valid) break;
     cur = nt;
     ra = ran;

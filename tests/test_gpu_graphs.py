@@ -224,11 +224,8 @@ def _workspace_sums(dev) -> int:
     return int(out.value)
 
 
-def test_hip_graph_of_a_split_k_plan_survives_a_larger_workspace():
-    """A one-sequence plan of a long-K, few-tile qlinear splits K into the context's workspace, and its captured HIP
-    graph records that workspace's address. A 32-sequence run of the same graph then needs a larger workspace (64
-    tiles of 128 x 128 instead of 1), which replaces the buffer. Replays of the first graph afterwards still write
-    correct outputs: the outgrown buffer is kept alive for graphs that hold it (every output against the oracle)."""
+def split_k_graph_case():
+    """The body of the split-K graph test, run in a child process whose context plans split-K products."""
     from anvil_mi355x import quantize as Q
     from anvil_mi355x.ir import GraphBuilder
     from oracle import semantics as sem
@@ -258,3 +255,27 @@ def test_hip_graph_of_a_split_k_plan_survives_a_larger_workspace():
     for _ in range(3):
         check(1, True)                     # replays of the graph captured before the growth
     assert cm.plan(1).graph is not None
+
+
+@pytest.mark.timeout(300)
+def test_hip_graph_of_a_split_k_plan_survives_a_larger_workspace():
+    """A one-sequence plan of a long-K, few-tile qlinear splits K into the context's workspace, and its captured HIP
+    graph records that workspace's address. A 32-sequence run of the same graph then needs a larger workspace (64
+    tiles of 128 x 128 instead of 1), which replaces the buffer. Replays of the first graph afterwards still write
+    correct outputs: the outgrown buffer is kept alive for graphs that hold it (every output against the oracle).
+
+    By default such few-tile products take the one-launch small-product kernel, which needs no workspace; the case
+    runs in a child process whose context is created with the benchmarking override ANVIL_GEMM_CFG set to a value no
+    product takes, which turns that kernel off and leaves the split-K rule in force."""
+    import os
+    import subprocess
+    import sys
+
+    child = "import test_gpu_graphs as t; t.split_k_graph_case(); print('split-K graph case ok')"
+    env = dict(os.environ, ANVIL_GEMM_CFG="99",
+               PYTHONPATH=os.pathsep.join(str(p) for p in (helpers.ROOT / "anvil-compiler_amd", helpers.ROOT,
+                                                           helpers.ROOT / "tests")))
+    print("split-K graph child: T 128, K 2048, N 256, 1 and 32 sequences, ANVIL_GEMM_CFG=99", flush=True)
+    out = subprocess.run([sys.executable, "-c", child], capture_output=True, text=True, timeout=280, env=env)
+    assert out.returncode == 0, (out.stdout[-2000:], out.stderr[-2000:])
+    assert "split-K graph case ok" in out.stdout

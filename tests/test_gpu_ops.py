@@ -634,12 +634,23 @@ def test_gemm_fused_add_block_multipliers(dev, M, N, K, ma, mb, s2):
     _check_sampled_gemm(dev, M, N, K, "i8", False, True, 45, (ma, mb, s2))
 
 
-def _check_sampled_gemm(dev, M, N, K, dtype, lut, add, seed, mults=(300, -200, 9)):
+@pytest.mark.parametrize("M,N,K,s", [(32768, 3072, 768, 12), (32768, 3072, 768, 16), (32768, 3072, 768, 17),
+                                     (32768, 3072, 768, 27), (32768 + 37, 3072 + 40, 768, 18),
+                                     (32768, 768, 3072, 17), (32768, 768, 3072, 18)])
+def test_gemm_persistent_lut_table_forms(dev, M, N, K, s):
+    """The persistent kernels' LUT epilogue at shifts on both sides of the widened table's limit: a table of
+    2^(32 - s) entries that fits beside the LDS stages (32 KiB for the 256 x 256 kernel, s >= 17; 16 KiB for the
+    256 x 128 one with 128-byte K blocks, s >= 18) is indexed by (x + 2^31) >> s with the clamp folded into its entries, otherwise the
+    rotated 256-entry table follows a clamp. The multiplier spreads the accumulators over the whole int32 range, so
+    both clamp ends and every table region are hit; ragged edges take the per-element path."""
+    _check_sampled_gemm(dev, M, N, K, "i8", True, False, 49, s=s)
+
+
+def _check_sampled_gemm(dev, M, N, K, dtype, lut, add, seed, mults=(300, -200, 9), s=20):
     rng = np.random.default_rng([seed, M, N, K])
     a, w = rng.integers(-128, 128, (M, K), dtype=np.int8), rng.integers(-128, 128, (K, N), dtype=np.int8)
     rows = np.unique(np.concatenate([np.arange(256), np.arange(M - 256, M), rng.integers(0, M, 512)]))
     acc = sem.matmul_i8(a[rows].astype(np.int64), w.astype(np.int64), fast=True)   # float64 BLAS, exact here
-    s = 20
     m = int(min(((1 << 31) - 1 - (1 << (s - 1))) // int(np.abs(acc).max() * 2), (1 << 23) - 1))
     L = rng.integers(-128, 128, 256) if lut else None
     flags = rt.GEMM_UNCHECKED | rt.GEMM_MUL24
