@@ -139,6 +139,59 @@ __device__ __forceinline__ unsigned sra_pack4(int x0, int x1, int x2, int x3, in
 // median of three: clamp(x, lo, hi) for runtime bounds lo <= hi, written in the form that selects v_med3_i32
 __device__ __forceinline__ int med3i(int x, int lo, int hi) { return max(min(x, lo), min(max(x, lo), hi)); }
 
+// a * (byte B of x, zero-extended), a < 2^24: one full-rate SDWA multiply (a 32-bit v_mul_lo_u32 runs at a quarter
+// of the rate)
+template <int B>
+__device__ __forceinline__ unsigned mul_u24_byte(unsigned a, unsigned x) {
+  static_assert(B >= 0 && B < 4, "byte lane");
+  unsigned d;
+  if constexpr (B == 0)
+    asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(d) : "s"(a), "v"(x));
+  else if constexpr (B == 1)
+    asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+        : "=v"(d) : "s"(a), "v"(x));
+  else if constexpr (B == 2)
+    asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+        : "=v"(d) : "s"(a), "v"(x));
+  else
+    asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=v"(d) : "s"(a), "v"(x));
+  return d;
+}
+
+// add_requant of packed int8 operands with multipliers below 2^24 in magnitude, r * m + y * n + rnd as
+// u * |m| + v * |n| + c: u = r + 128 (the byte of r ^ 0x80) when m >= 0, else 127 - r (the byte of r ^ 0x7F), so that
+// r * m = u * |m| - 128 m or u * |m| + 127 m; likewise v for y and n; c = rnd plus both corrections. Every product
+// is below 2^32 and the sum is taken modulo 2^32, so it equals the true sum whenever that lies inside int32, as the
+// proof of the add ensures.
+struct PackedAdd {
+  unsigned am, an, xr, xy, c;
+  int clo, chi, sh;
+  __device__ static bool applies(int m, int n) { return m > -(1 << 24) && m < (1 << 24) && n > -(1 << 24) && n < (1 << 24); }
+  __device__ PackedAdd(int m, int n, int rnd, int shift) {
+    am = m >= 0 ? (unsigned)m : (unsigned)-m;
+    an = n >= 0 ? (unsigned)n : (unsigned)-n;
+    xr = m >= 0 ? 0x80808080u : 0x7F7F7F7Fu;
+    xy = n >= 0 ? 0x80808080u : 0x7F7F7F7Fu;
+    c = (unsigned)rnd + (m >= 0 ? 0u - 128u * (unsigned)m : 127u * (unsigned)m) +
+        (n >= 0 ? 0u - 128u * (unsigned)n : 127u * (unsigned)n);
+    clo = (int)max(-128ll << shift, (long long)INT32_MIN);
+    chi = (int)min((128ll << shift) - 1, (long long)INT32_MAX);
+    sh = shift;
+  }
+  // four int8 results clamp((r * m + y * n + rnd) >> shift) of the bytes of r and y, packed (clamp before the shift,
+  // then one SDWA shift into each byte lane)
+  __device__ __forceinline__ unsigned operator()(unsigned r, unsigned y) const {
+    const unsigned ur = r ^ xr, uy = y ^ xy;
+    const int o0 = med3i((int)(mul_u24_byte<0>(am, ur) + mul_u24_byte<0>(an, uy) + c), clo, chi);
+    const int o1 = med3i((int)(mul_u24_byte<1>(am, ur) + mul_u24_byte<1>(an, uy) + c), clo, chi);
+    const int o2 = med3i((int)(mul_u24_byte<2>(am, ur) + mul_u24_byte<2>(an, uy) + c), clo, chi);
+    const int o3 = med3i((int)(mul_u24_byte<3>(am, ur) + mul_u24_byte<3>(an, uy) + c), clo, chi);
+    return sra_pack4(o0, o1, o2, o3, sh);
+  }
+};
+
 constexpr long long I32_MIN = -(1ll << 31);
 constexpr long long I32_MAX = (1ll << 31) - 1;
 

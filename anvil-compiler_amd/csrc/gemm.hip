@@ -554,7 +554,7 @@ __device__ void splitk_finish(const GemmArgs& g, const v16i (&acc)[TN][TM], cons
 // add). A stage at or past K is issued only to keep each stage's load count fixed and is never read: its offsets
 // reach the next rows' bytes inside the buffer resource, or zeros past it. With three stages KFULL also means
 // whole rotations (K a multiple of 192), which the launches check.
-template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool SPLIT = false, bool KFULL = false>
+template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool SPLIT = false, bool KFULL = false, bool RES = true>
 __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int bz) {
   constexpr int BK = 64, CPR = BK / 16;
   constexpr int WGN = 4 / WGM;
@@ -733,7 +733,7 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
   auto rr_of = [&](int pass) { return (t + pass * G_THREADS) / CH_ROW; };
   auto cf_of = [&](int pass) { return (t + pass * G_THREADS) % CH_ROW * 16 / OSZ; };   // first column
   const int cols_valid = min(BN, g.N - n0);
-  const bool res = g.res != 0;
+  const bool res = RES && g.res != 0;   // RES false: no fused add, its code compiled out
   // interior tile: every chunk is read from LDS (and the residual from memory) before the first store, so the
   // reads' latencies overlap instead of serialising pass by pass
   const bool full = m0 + BM <= g.M && cols_valid == BN && (res ? g.vec_res != 0 : g.vec_store != 0) &&
@@ -743,7 +743,7 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
   // without a residual): they are then the newest NR loads, and waiting for all but those retires the pipeline's
   // last (zero-filling) stage loads before the staging overwrites their arrays. An i16 result (twice the chunks,
   // whose registers the staging needs) loads its residual chunks in the store phase, and the wait is for all.
-  constexpr int NR = OSZ == 1 ? PASSES : 0;
+  constexpr int NR = OSZ == 1 && RES ? PASSES : 0;
   const bool res_full = res && full;
   const int8_t* Rb = g.R + (b0 * g.sr0 + b1 * g.sr1 + (long long)m0 * g.ldr + n0) * OSZ;
   const __amdgpu_buffer_rsrc_t rres = uniform_rsrc(res_full ? Rb : g.A, res_full ? (int)(BM * g.ldr * OSZ) : 0);
@@ -833,6 +833,22 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
       constexpr long long LO = OSZ == 1 ? -128 : -32768, HI = OSZ == 1 ? 127 : 32767;
       const int clo2 = (int)max(LO << sh2, (long long)INT32_MIN);
       const int chi2 = (int)min(((HI + 1) << sh2) - 1, (long long)INT32_MAX);
+      if (OSZ == 1 && PackedAdd::applies(ma, mb)) {
+        // multipliers below 2^24: full-rate byte multiplies (PackedAdd) instead of 32-bit ones
+        const PackedAdd add(ma, mb, rnd2, sh2);
+#pragma unroll
+        for (int pass = 0; pass < PASSES; ++pass) {
+          v4i ov;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ov[q] = (int)add((unsigned)rv[pass][q], (unsigned)ch[pass][q]);
+          *reinterpret_cast<v4i*>(Db + ((long long)rr_of(pass) * g.ldd + cf_of(pass)) * OSZ) = ov;
+        }
+        if (!g.store_y) return;
+#pragma unroll
+        for (int pass = 0; pass < PASSES; ++pass)
+          *reinterpret_cast<v4i*>(Cb + cpos(g, m0 + rr_of(pass), n0 + cf_of(pass)) * OSZ) = ch[pass];
+        return;
+      }
 #pragma unroll
       for (int pass = 0; pass < PASSES; ++pass) {
         v4i ov, r16 = {0, 0, 0, 0};
@@ -875,7 +891,7 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
     const int m = m0 + rr;
     if (m >= g.M) break;                                 // rows grow with the pass
     const int8_t* src = srow(rr) + cfirst * OSZ;
-    if (OSZ == 2 && g.res) {
+    if (OSZ == 2 && res) {
       // the fused add_requant on i16 values, element by element over the chunk's 8 columns
       const int16_t* rp = reinterpret_cast<const int16_t*>(g.R) + b0 * g.sr0 + b1 * g.sr1 + (long long)m * g.ldr + n0 +
                           cfirst;
@@ -887,7 +903,7 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
         }
       if (!g.store_y) continue;
     }
-    if (OSZ == 1 && g.res) {
+    if (OSZ == 1 && res) {
       // the fused add_requant: 16 results from the staged y chunk and the residual chunk at the same position
       const int8_t* rp = g.R + b0 * g.sr0 + b1 * g.sr1 + (long long)m * g.ldr + n0 + cfirst;
       int8_t* dp = g.D + b0 * g.sd0 + b1 * g.sd1 + (long long)m * g.ldd + n0 + cfirst;
@@ -994,12 +1010,13 @@ __global__ __launch_bounds__(G_THREADS) void splitk_reduce(GemmArgs g) {
 
 template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool KFULL>
 __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8_splitk(GemmArgs g) {
-  fast_tile<BM, BN, WGM, NS, OSZ, MUL24, true, KFULL>(g, blockIdx.x, blockIdx.y);
+  fast_tile<BM, BN, WGM, NS, OSZ, MUL24, true, KFULL, false>(g, blockIdx.x, blockIdx.y);
 }
 
-template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool KFULL = false>
+// RES: the product may carry a fused residual add (a kernel without one has none of its code)
+template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool KFULL = false, bool RES = true>
 __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8_fast(GemmArgs g) {
-  fast_tile<BM, BN, WGM, NS, OSZ, MUL24, false, KFULL>(g, blockIdx.x, blockIdx.y);
+  fast_tile<BM, BN, WGM, NS, OSZ, MUL24, false, KFULL, RES>(g, blockIdx.x, blockIdx.y);
 }
 
 // Up to GEMM_GROUP_MAX independent products in one launch (q, k and v of one input, say): member i owns the
@@ -1023,7 +1040,7 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
   const int ntiles = g.tiles_m * g.tiles_n, local = w - a.first[i];
   const int bz = local / ntiles;
   if (bz >= g.nbatch) return;                            // padding up to the next member's multiple of 8
-  fast_tile<BM, BN, WGM, NS, OSZ, MUL24, false, KFULL>(g, local - bz * ntiles, bz);
+  fast_tile<BM, BN, WGM, NS, OSZ, MUL24, false, KFULL, false>(g, local - bz * ntiles, bz);   // no member has an add
 }
 
 // Persistent kernel with a register epilogue. Bt rows are loaded into LDS permuted within each 32-row group (LDS row c
@@ -1263,14 +1280,18 @@ static void launch_fast(GemmArgs& g, int osz, int batch, hipStream_t s) {
   g.tiles_n = (g.N + BN - 1) / BN;
   dim3 grid(g.tiles_m * g.tiles_n, batch);
   const bool kfull = KF && g.K % (64 * NS) == 0 && g.causal != 2;
-  if (osz == 1 && kfull)
-    ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 1, MUL24, KF>), grid, dim3(G_THREADS), 0, s, g);
-  else if (osz == 1)
-    ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 1, MUL24, false>), grid, dim3(G_THREADS), 0, s, g);
-  else if (kfull)
-    ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 2, MUL24, KF>), grid, dim3(G_THREADS), 0, s, g);
-  else
-    ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 2, MUL24, false>), grid, dim3(G_THREADS), 0, s, g);
+  auto go = [&](auto res_c) {
+    constexpr bool R = decltype(res_c)::value;
+    if (osz == 1 && kfull)
+      ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 1, MUL24, KF, R>), grid, dim3(G_THREADS), 0, s, g);
+    else if (osz == 1)
+      ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 1, MUL24, false, R>), grid, dim3(G_THREADS), 0, s, g);
+    else if (kfull)
+      ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 2, MUL24, KF, R>), grid, dim3(G_THREADS), 0, s, g);
+    else
+      ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 2, MUL24, false, R>), grid, dim3(G_THREADS), 0, s, g);
+  };
+  if (g.res) go(std::true_type{}); else go(std::false_type{});
 }
 
 template <int BM, int BN, int WGM, int NS, bool MUL24>

@@ -532,7 +532,10 @@ def test_fused_attention_keep_checks_its_strides(dev):
 
 # add_requant multipliers: a negative one, config 5's two adds (Ma above 2^23, 128 (Ma + Mb) close to 2^31), and
 # Ma = Mb = 1 with no shift
-ADD_MULTS = [(300, -200, 9), (11157253, 4299753, 24), (7873258, 3110671, 23), (1, 1, 0)]
+# multipliers of every sign, at and above 2^23 (the 24-bit byte-multiply form covers magnitudes below 2^24; the
+# worst-case sum still inside int32)
+ADD_MULTS = [(300, -200, 9), (11157253, 4299753, 24), (7873258, 3110671, 23), (1, 1, 0), (-12000000, 4000000, 24),
+             (16000000, -700000, 24), (-8388608, -8000000, 24)]
 
 
 @pytest.mark.parametrize("M,K,N", [(256, 768, 768), (300, 64, 200), (33, 48, 72), (1024, 256, 384)])
