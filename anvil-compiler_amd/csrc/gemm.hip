@@ -424,19 +424,27 @@ __device__ __forceinline__ void direct_epilogue(const GemmArgs& g, const v16i (&
         if (FULL) {
           if (res) {
             const int ma = g.ma, mb = g.mb, rnd2 = g.rnd2, sh2 = g.shift2;
-            // clamp before the shift, then one SDWA shift into each byte lane
-            const int clo2 = (int)max(-128ll << sh2, (long long)INT32_MIN);
-            const int chi2 = (int)min((128ll << sh2) - 1, (long long)INT32_MAX);
             v4i ov;
+            if (PackedAdd::applies(ma, mb)) {
+              // multipliers below 2^24: y packed, then full-rate byte multiplies (PackedAdd)
+              const PackedAdd add(ma, mb, rnd2, sh2);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              int o[4];
+              for (int q = 0; q < 4; ++q)
+                ov[q] = (int)add((unsigned)rv[j][i][q], pack4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]));
+            } else {
+              // clamp before the shift, then one SDWA shift into each byte lane
+              const int clo2 = (int)max(-128ll << sh2, (long long)INT32_MIN);
+              const int chi2 = (int)min((128ll << sh2) - 1, (long long)INT32_MAX);
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int r = (int)(int8_t)((unsigned)rv[j][i][q] >> (8 * e));
-                o[e] = med3i(r * ma + v[4 * q + e] * mb + rnd2, clo2, chi2);   // proven inside int32
+              for (int q = 0; q < 4; ++q) {
+                int o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const int r = (int)(int8_t)((unsigned)rv[j][i][q] >> (8 * e));
+                  o[e] = med3i(r * ma + v[4 * q + e] * mb + rnd2, clo2, chi2);   // proven inside int32
+                }
+                ov[q] = (int)sra_pack4(o[0], o[1], o[2], o[3], sh2);
               }
-              ov[q] = (int)sra_pack4(o[0], o[1], o[2], o[3], sh2);
             }
             *reinterpret_cast<v4i*>(Db + (long long)m * g.ldd + n) = ov;
             if (!g.store_y) continue;
