@@ -6,6 +6,9 @@ fl(y + 1.5 2^52), i.e. y rounded to the nearest integer: floor(y + 1/2). Here fm
 rational e A + B' rounded once to the nearest double, which Python's float(Fraction) does), the addition is an IEEE
 double addition, and the result is compared with integer floor division on the cases where a floating-point quotient
 is most fragile: exact multiples n = k S and their neighbours, the largest divisors, and random draws.
+
+The GEMM epilogues' fused add on byte multiplies (PackedAdd) and their widened LUT index are checked at the end of
+the file, on every int8 operand pair and on int32 values at both ends of the range.
 """
 import struct
 from fractions import Fraction
@@ -94,3 +97,64 @@ def test_every_quotient_of_a_small_range(S):
     for e in range(top + 1):
         if in_domain(e, one, S):
             assert kernel_quot(e, one, S) == (e * one + h) // S, (e, S)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# The GEMM epilogues' byte-multiply add and widened LUT index (csrc/common.h PackedAdd, csrc/gemm.hip plain_epilogue),
+# emulated with the hardware's operations: a 24 x 24 -> 32-bit unsigned multiply of a byte, and 32-bit wrapping adds.
+
+M32 = (1 << 32) - 1
+
+
+def packed_add_sum(r, y, m, n, rnd):
+    """r * m + y * n + rnd as the kernel forms it: u * |m| + v * |n| + c modulo 2^32, read as int32; u is the byte of
+    r ^ 0x80 (m >= 0) or r ^ 0x7F (m < 0), likewise v for y."""
+    def term(x, mult):
+        u = (x & 0xFF) ^ (0x80 if mult >= 0 else 0x7F)
+        assert 0 <= u <= 255 and abs(mult) < 1 << 24
+        return (u * abs(mult)) & M32, ((-128 * mult) if mult >= 0 else (127 * mult)) & M32
+    tr, cr = term(r, m)
+    ty, cy = term(y, n)
+    s = (tr + ty + ((rnd + cr + cy) & M32)) & M32
+    return s - (1 << 32) if s >= 1 << 31 else s
+
+
+@pytest.mark.parametrize("m,n", [(0, 0), (1, 1), (300, -200), (11157253, 4299753), (-12000000, 4000000),
+                                 (16000000, -700000), (-8388608, -8000000), ((1 << 24) - 1, 0), (-(1 << 24) + 1, 0),
+                                 (1 << 23, -(1 << 23)), (-1, 1)])
+def test_packed_add_is_the_add_inside_int32(m, n):
+    """Every pair of int8 operands: the byte-multiply form equals r m + y n + rnd whenever that lies inside int32 (the
+    add's proof); planted: the 127 correction of a negative multiplier replaced by 128 fails."""
+    r = np.arange(-128, 128, dtype=np.int64)[:, None]
+    y = np.arange(-128, 128, dtype=np.int64)[None, :]
+    rnd = 1 << 23
+    want = r * m + y * n + rnd
+    inside = (want >= -(1 << 31)) & (want < 1 << 31)
+    got = np.vectorize(lambda a, b: packed_add_sum(int(a), int(b), m, n, rnd))(r, y)
+    assert np.array_equal(got[inside], want[inside])
+    if m < 0:   # a plausible slip: the same correction for both signs
+        bad = np.vectorize(lambda a, b: (((a & 0xFF) ^ 0x7F) * -m - 128 * m + b * n + rnd))(r, y)
+        assert not np.array_equal(bad[inside], want[inside])
+
+
+def wide_lut_index(x, s):
+    """(x + 2^31) >> s, unsigned, with x + 2^31 formed modulo 2^32 (the kernel adds 2^31 through the rounding
+    constant)."""
+    return ((x + (1 << 31)) & M32) >> s
+
+
+@pytest.mark.parametrize("s", [1, 2, 12, 16, 17, 18, 24, 30, 31])
+def test_wide_lut_index_is_the_shift_plus_an_offset(s):
+    """For every int32 x, (x + 2^31) >> s (unsigned) equals floor(x / 2^s) + 2^(31 - s), in [0, 2^(32 - s)): the
+    widened table's entry u = lut[clamp(u - 2^(31 - s), -128, 127) + 128] is then the clamped requant's LUT value."""
+    rng = np.random.default_rng(s)
+    x = np.concatenate([np.arange(-(1 << 31), -(1 << 31) + 4096), np.arange(-4096, 4096),
+                        np.arange((1 << 31) - 4096, 1 << 31), rng.integers(-(1 << 31), 1 << 31, 100000)])
+    x = x.astype(np.int64)
+    u = wide_lut_index(x, s)
+    assert np.array_equal(u, (x >> s) + (1 << (31 - s)))
+    assert u.min() >= 0 and u.max() < 1 << (32 - s)
+    lut = np.random.default_rng(1).integers(-128, 128, 256)
+    table = lut[np.clip(np.arange(1 << (32 - s)) - (1 << (31 - s)), -128, 127) + 128] if s >= 12 else None
+    if table is not None:
+        assert np.array_equal(table[u], lut[np.clip(x >> s, -128, 127) + 128])
