@@ -106,6 +106,8 @@ class _Plan:
         self.steps: list = []          # (label, fn, args)
         self.works: list = []          # per step: (kind, algorithmic int ops, algorithmic HBM bytes)
         self.fused_adds: set = set()   # add_requant ops computed in a GEMM epilogue
+        self.norm_of: dict = {}        # fused add_requant -> the rmsnorm_int of its sum that may share its epilogue
+        self.fused_norms: set = set()  # rmsnorm_int ops computed in a GEMM epilogue
         self.stage: dict = {}          # device staging buffers of float inputs and token ids
         self.host_stage: dict = {}     # page-locked host buffers the read-back downloads into, by device buffer
         self.graph = None              # the steps captured as one HIP graph (run(..., graph=True))
@@ -318,9 +320,10 @@ class CompiledModel:
         fused = self._attention_chains(keep)
         skip = {o for s_op, sm in fused.values() for o in (s_op, sm)}
         adds = self._residual_fusions(keep)
+        P.norm_of = self._norm_fusions(adds)
         P.kb_values = self._kblocked_values(keep, fused, skip, adds)
         for op in self.ops:
-            if op in skip or op in P.fused_adds:
+            if op in skip or op in P.fused_adds or op in P.fused_norms:
                 continue
             r = op.results[0]
             t = g.qt(r)
@@ -691,6 +694,32 @@ class CompiledModel:
                 break
         return found
 
+    def _norm_fusions(self, adds) -> dict:
+        """{add_requant: rmsnorm_int} for fused adds (_residual_fusions) whose int8 sum feeds a plain int8 rmsnorm
+        (ss_shift = ss_init = 0, const weights and a const non-negative table with |table x M| < 2^23) over rows
+        of 128, with add multipliers below 2^24: the rmsnorm can then run in the same epilogue
+        (anvil_gemm_i8_add_norm), which _plan_fused_add takes when the rows allow it. At C = 128 (config 4) these are
+        each block's h2 = rmsnorm(r1), the next layer's h1 and the final norm: 0.1042 -> 0.0972 ms a step. The entry
+        point also takes rows of 256 (64 x 256 tiles), but at config 3 that measured level with the two launches
+        (0.0736 against 0.0737 ms), so the planner leaves those unfused."""
+        found = {}
+        for add in adds.values():
+            t = g.qt(add.result)
+            if t.dtype != "i8" or t.dims[-1] != 128 or max(abs(int(add.Ma)), abs(int(add.Mb))) >= 1 << 24:
+                continue
+            for u in self.users.get(add.result, []):
+                if (not isinstance(u, g.RmsNormIntOp) or u.x is not add.result or u.ss_shift_int
+                        or u.ss_init_int or g.qt(u.w).dtype != "i8"):
+                    continue
+                w, lut = self._const_array(u.w), self._const_array(u.lut)
+                if w is None or lut is None or lut.size < 1 or int(lut.min()) < 0:
+                    continue
+                if int(np.abs(lut).max()) * abs(int(u.M)) >= 1 << 23 or not 0 <= int(u.s) <= 31:
+                    continue
+                found[add] = u
+                break
+        return found
+
     def _plan_matmul(self, P, op, views, out_dims, label, dense, step, keep, out=None, add=None):
         t = g.qt(op.result)
         M, N = out_dims[-2], out_dims[-1]
@@ -785,8 +814,22 @@ class CompiledModel:
         rstrides = [0, 0, rv.strides[0], 0, 0, d.strides[0]]
         a2, bt = self._kblock_weight(op, a2, bt, strides, K, False)
         strides, flags = self._kb_call(a2, bt, c2 if store_y else None, strides, flags)
-        step(label, _call_gemm_add, self.dev, a2, bt, c2 if store_y else None, rows, N, K, strides, op, lut, rv, ma,
-             mb, int(add.s), d, rstrides, flags, dt)
+        norm = P.norm_of.get(add)
+        if norm is not None and dt == "i8" and rows % 128 == 0 and N == 128 and ok16(rv.offset):
+            # the sum's rmsnorm in the same epilogue: each 128 x N tile spans its rows
+            hdims = tuple(views[other].dims)
+            h = (P.kblocked(hdims, "i8", norm.sym_str or "norm") if norm.result in P.kb_values
+                 else P.dense(hdims, "i8", norm.sym_str or "norm"))
+            nw = self._const_views[norm.w]
+            nlut = self._const_views[norm.lut]
+            step(f"{label}+{norm.sym_str or 'norm'}", _call_gemm_add_norm, self.dev, a2, bt, c2 if store_y else None,
+                 rows, N, K, strides, op, lut, rv, ma, mb, int(add.s), d, rstrides, nw, nlut, norm, h,
+                 flags | rt.GEMM_NORM_S24)
+            views[norm.result] = h
+            P.fused_norms.add(norm)
+        else:
+            step(label, _call_gemm_add, self.dev, a2, bt, c2 if store_y else None, rows, N, K, strides, op, lut, rv,
+                 ma, mb, int(add.s), d, rstrides, flags, dt)
         views[add.result] = d.reshape(tuple(views[other].dims))
         P.fused_adds.add(add)
         return True
@@ -1138,6 +1181,10 @@ def _work(fn, args):
         _, a, bt, c, M, N, K = args[:7]
         osz = isz[args[-1]] if len(args) > 17 else 1
         return "gemm", 2 * M * N * K, M * K + N * K + M * N * osz * (3 if c is not None else 2)
+    if fn is _call_gemm_add_norm:                 # also reads the norm's weights and table and writes H
+        _, a, bt, c, M, N, K = args[:7]
+        nw, nlut = args[16], args[17]
+        return "gemm", 2 * M * N * K, M * K + N * K + M * N * (4 if c is not None else 3) + N + 4 * nlut.size
     if fn is _call_attention:
         _, q, k, v, o, b0, b1, T, D = args[:9]
         nb = b0 * b1
@@ -1227,6 +1274,13 @@ def _call_gemm_add(dev, a: View, bt: View, c, M, N, K, strides, op, lut, r: View
                    flags, out_dtype="i8"):
     dev.gemm_i8_add(a.ptr, bt.ptr, None if c is None else c.ptr, 1, 1, M, N, K, strides, int(op.M), int(op.s),
                     None if lut is None else lut.ptr, r.ptr, ma, mb, shift2, d.ptr, rstrides, flags, out_dtype)
+
+
+def _call_gemm_add_norm(dev, a: View, bt: View, c, M, N, K, strides, op, lut, r: View, ma, mb, shift2, d: View,
+                        rstrides, nw: View, nlut: View, norm, h: View, flags):
+    dev.gemm_i8_add_norm(a.ptr, bt.ptr, None if c is None else c.ptr, M, N, K, strides, int(op.M), int(op.s),
+                         None if lut is None else lut.ptr, r.ptr, ma, mb, shift2, d.ptr, rstrides, nw.ptr, nlut.ptr,
+                         nlut.size, int(norm.M), int(norm.s), h.ptr, 64 if h.kb else h.strides[-2], h.kb, flags)
 
 
 def _swap_last2(n):

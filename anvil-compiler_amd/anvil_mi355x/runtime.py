@@ -31,6 +31,7 @@ _ERRORS = {1: ValueError, 2: OverflowError, 3: ZeroDivisionError, 4: RuntimeErro
 # anvil_gemm_i8_ex flags (include/anvil_mi355x.h)
 GEMM_UNCHECKED, GEMM_CAUSAL_SKIP, GEMM_CAUSAL_K, GEMM_MUL24, GEMM_SPLITK = 1, 2, 4, 8, 16
 GEMM_A_KBLOCK, GEMM_B_KBLOCK, GEMM_C_KBLOCK = 32, 64, 128
+GEMM_NORM_S24 = 256                          # anvil_gemm_i8_add_norm: |rsqrt table entry x mult| < 2^23
 # anvil_rmsnorm_int_ex / anvil_softmax_lut_ex / anvil_attention_i8 flags
 OP_UNCHECKED, ATTN_S24, RMS_S24, RMS_OUT_KBLOCK, ATTN_V_ROWS = 1, 2, 2, 4, 4
 
@@ -64,6 +65,7 @@ SIGNATURES = {
     "anvil_gemm_i8_add": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _p, _i32, _i32, _i, _p, _p, _i],
     "anvil_gemm_i8_add_ex": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i32, _i, _p, _i, _p, _i32, _i32, _i, _p, _p,
                              _i],
+    "anvil_gemm_i8_add_norm": [_p, _p, _p, _p, _i, _i, _i, _p, _i32, _i, _p, _p, _i32, _i32, _i, _p, _p, _p, _i],
     "anvil_rmsnorm_int": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p],
     "anvil_rmsnorm_int_ex": [_p, _p, _i, _p, _p, _i, _i32, _i, _i, _i32, _i64, _i, _p, _i],
     "anvil_softmax_lut": [_p, _p, _p, _i32, _i, _i64, _i, _i, _p, _i],
@@ -87,6 +89,12 @@ class GemmDesc(C.Structure):
     _fields_ = [("A", _p), ("Bt", _p), ("C", _p), ("lut", _p), ("strides", _i64 * 9), ("batch0", _i32),
                 ("batch1", _i32), ("M", _i32), ("N", _i32), ("K", _i32), ("mult", _i32), ("shift", _i32),
                 ("out_dtype", _i32), ("flags", _i32)]
+
+
+class NormEpilogue(C.Structure):
+    """anvil_norm_epilogue: the rmsnorm fused after anvil_gemm_i8_add_norm's add."""
+    _fields_ = [("w", _p), ("lut", _p), ("lut_len", _i32), ("mult", _i32), ("shift", _i32), ("out", _p),
+                ("ld", _i64), ("kb", _i64)]
 
 
 GEMM_GROUP_MAX = 4
@@ -331,6 +339,19 @@ class Device:
                       C.c_void_p(_ptr(Cp) if Cp is not None else 0), batch0, batch1, M, N, K, st, int(mult), shift,
                       C.c_void_p(_ptr(lut) if lut is not None else 0), DTYPE_CODE[out_dtype], C.c_void_p(_ptr(R)),
                       int(ma), int(mb), shift2, C.c_void_p(_ptr(D)), rs, int(flags))
+
+    def gemm_i8_add_norm(self, A, Bt, Cp, M, N, K, strides, mult, shift, lut, R, ma, mb, shift2, D, rstrides,
+                         nw, nlut, nlut_len, nmult, nshift, H, ld, kb, flags):
+        """anvil_gemm_i8_add_norm: gemm_i8_add (batch 1, int8) whose sum D also feeds rmsnorm_int(D, nw, nlut, nmult,
+        nshift) into H (row stride ld, or K-blocked with block stride kb and ld 64), all in one epilogue."""
+        st = (C.c_int64 * 9)(*[int(s) for s in strides])
+        rs = (C.c_int64 * 6)(*[int(s) for s in rstrides])
+        norm = NormEpilogue(C.c_void_p(_ptr(nw)), C.c_void_p(_ptr(nlut)), int(nlut_len), int(nmult), int(nshift),
+                            C.c_void_p(_ptr(H)), int(ld), int(kb))
+        self.lib.call("anvil_gemm_i8_add_norm", self.ctx, C.c_void_p(_ptr(A)), C.c_void_p(_ptr(Bt)),
+                      C.c_void_p(_ptr(Cp) if Cp is not None else 0), M, N, K, st, int(mult), shift,
+                      C.c_void_p(_ptr(lut) if lut is not None else 0), C.c_void_p(_ptr(R)), int(ma), int(mb), shift2,
+                      C.c_void_p(_ptr(D)), rs, C.byref(norm), int(flags))
 
     def rmsnorm_int(self, x, x_dtype, w, lut, lut_len, mult, shift, ss_shift, ss_init, rows, cols, out, flags=0):
         self.lib.call("anvil_rmsnorm_int_ex", self.ctx, C.c_void_p(_ptr(x)), DTYPE_CODE[x_dtype], C.c_void_p(_ptr(w)),

@@ -64,6 +64,13 @@ struct GemmArgs {
   // as partial tile (tile, z) of ws; splitk_reduce adds the partial tiles up
   int* ws;
   int kchunk, splits;
+  // fused rmsnorm of D (gemm_i8_fast with NORM, one tile spanning D's rows): H = rmsnorm_int(D, nw, nlut, nmult,
+  // nshift), H row-major (row stride ldh) or K-blocked (block stride kbh); nbits = the bit length of nlut_len
+  const int8_t* nw;
+  const int* nlut;
+  int8_t* H;
+  long long ldh, kbh;
+  int nlut_len, nbits, nmult, nshift;
 };
 
 constexpr int G_THREADS = 256;
@@ -562,7 +569,8 @@ __device__ void splitk_finish(const GemmArgs& g, const v16i (&acc)[TN][TM], cons
 // add). A stage at or past K is issued only to keep each stage's load count fixed and is never read: its offsets
 // reach the next rows' bytes inside the buffer resource, or zeros past it. With three stages KFULL also means
 // whole rotations (K a multiple of 192), which the launches check.
-template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool SPLIT = false, bool KFULL = false, bool RES = true>
+template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool SPLIT = false, bool KFULL = false, bool RES = true,
+          bool NORM = false>
 __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int bz) {
   constexpr int BK = 64, CPR = BK / 16;
   constexpr int WGN = 4 / WGM;
@@ -844,12 +852,47 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
       if (OSZ == 1 && PackedAdd::applies(ma, mb)) {
         // multipliers below 2^24: full-rate byte multiplies (PackedAdd) instead of 32-bit ones
         const PackedAdd add(ma, mb, rnd2, sh2);
+        // NORM: H = rmsnorm_int(D) row by row (anvil/semantics.py:164-182 with ss_shift = ss_init = 0): the tile
+        // spans D's rows, CH_ROW consecutive lanes hold one row's chunks, and a lane's columns are the same in every
+        // pass (CH_ROW divides the thread count), so its 16 weights load once
+        static_assert(!NORM || (OSZ == 1 && RES && G_THREADS % CH_ROW == 0), "a fused rmsnorm of int8 D rows");
+        v4i nwv = {0, 0, 0, 0};
+        if constexpr (NORM) nwv = *reinterpret_cast<const v4i*>(g.nw + cf_of(0));
+        auto norm_chunk = [&](const v4i& d, int rr, int cf) {
+          int ss = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(d[q], d[q], ss, false);
+          ss = lane_group_sum<CH_ROW>(ss);
+          // (idx, k) = rsqrt_index(ss, n), the fewest k with ss >> 2k below n: with b and c the bit lengths of ss
+          // and n, k is k0 = max(0, floor((b - c + 1) / 2)) or k0 + 1
+          const int b = ss == 0 ? 0 : 32 - __builtin_clz((unsigned)ss);
+          const int k0 = max(0, (b - g.nbits + 1) >> 1);
+          const int k = k0 + ((ss >> (2 * k0)) >= g.nlut_len ? 1 : 0);
+          const int rm = g.nlut[ss >> (2 * k)] * g.nmult;            // proven below 2^23 in magnitude
+          const int sh = g.nshift + k;
+          const int rnd = sh ? 1 << (sh - 1) : 0;
+          const int lo = sh >= 24 ? INT32_MIN : -128 * (1 << sh), hi = sh >= 24 ? INT32_MAX : 128 * (1 << sh) - 1;
+          v4i h;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const unsigned xd = (unsigned)d[q], wd = (unsigned)nwv[q];
+            // proven: x w r M + rnd inside int32, |x w| and |r M| below 2^23
+            const int y0 = med3i(mad_i24v(mul_sbytes<0>(xd, wd), rm, rnd), lo, hi);
+            const int y1 = med3i(mad_i24v(mul_sbytes<1>(xd, wd), rm, rnd), lo, hi);
+            const int y2 = med3i(mad_i24v(mul_sbytes<2>(xd, wd), rm, rnd), lo, hi);
+            const int y3 = med3i(mad_i24v(mul_sbytes<3>(xd, wd), rm, rnd), lo, hi);
+            h[q] = (int)sra_pack4v(y0, y1, y2, y3, sh);
+          }
+          const long long m = m0 + rr;
+          *reinterpret_cast<v4i*>(g.H + (g.kbh ? m * 64 + (cf >> 6) * g.kbh + (cf & 63) : m * g.ldh + cf)) = h;
+        };
 #pragma unroll
         for (int pass = 0; pass < PASSES; ++pass) {
           v4i ov;
 #pragma unroll
           for (int q = 0; q < 4; ++q) ov[q] = (int)add((unsigned)rv[pass][q], (unsigned)ch[pass][q]);
           *reinterpret_cast<v4i*>(Db + ((long long)rr_of(pass) * g.ldd + cf_of(pass)) * OSZ) = ov;
+          if constexpr (NORM) norm_chunk(ov, rr_of(pass), cf_of(pass));
         }
         if (!g.store_y) return;
 #pragma unroll
@@ -1021,10 +1064,11 @@ __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8
   fast_tile<BM, BN, WGM, NS, OSZ, MUL24, true, KFULL, false>(g, blockIdx.x, blockIdx.y);
 }
 
-// RES: the product may carry a fused residual add (a kernel without one has none of its code)
-template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool KFULL = false, bool RES = true>
+// RES: the product may carry a fused residual add (a kernel without one has none of its code); NORM: and a fused
+// rmsnorm of its sum
+template <int BM, int BN, int WGM, int NS, int OSZ, bool MUL24, bool KFULL = false, bool RES = true, bool NORM = false>
 __global__ __launch_bounds__(G_THREADS, (fast_occupancy<BM, BN>())) void gemm_i8_fast(GemmArgs g) {
-  fast_tile<BM, BN, WGM, NS, OSZ, MUL24, false, KFULL, RES>(g, blockIdx.x, blockIdx.y);
+  fast_tile<BM, BN, WGM, NS, OSZ, MUL24, false, KFULL, RES, NORM>(g, blockIdx.x, blockIdx.y);
 }
 
 // Up to GEMM_GROUP_MAX independent products in one launch (q, k and v of one input, say): member i owns the
@@ -1300,6 +1344,18 @@ static void launch_fast(GemmArgs& g, int osz, int batch, hipStream_t s) {
       ANVIL_LAUNCH((gemm_i8_fast<BM, BN, WGM, NS, 2, MUL24, false, R>), grid, dim3(G_THREADS), 0, s, g);
   };
   if (g.res) go(std::true_type{}); else go(std::false_type{});
+}
+
+// The fused add + rmsnorm product (anvil_gemm_i8_add_norm): BM x BN tiles, BN = N, so each tile spans its rows
+template <int BM, int BN>
+static void launch_fast_norm(GemmArgs& g, bool mul24, hipStream_t s) {
+  g.tiles_m = (g.M + BM - 1) / BM;
+  g.tiles_n = 1;
+  const dim3 grid(g.tiles_m, 1);
+  if (mul24)
+    ANVIL_LAUNCH((gemm_i8_fast<BM, BN, 2, 3, 1, true, false, true, true>), grid, dim3(G_THREADS), 0, s, g);
+  else
+    ANVIL_LAUNCH((gemm_i8_fast<BM, BN, 2, 3, 1, false, false, true, true>), grid, dim3(G_THREADS), 0, s, g);
 }
 
 template <int BM, int BN, int WGM, int NS, bool MUL24>
@@ -2182,6 +2238,51 @@ extern "C" int anvil_gemm_i8_add_ex(anvil_ctx* ctx, const int8_t* A, const int8_
                                     int shift2, void* D, const int64_t* rstrides, int flags) {
   const AddEpilogue add{static_cast<const int8_t*>(R), static_cast<int8_t*>(D), rstrides, ma, mb, shift2};
   return gemm_entry(ctx, A, Bt, C, batch0, batch1, M, N, K, strides, mult, shift, lut, out_dtype, flags, &add);
+}
+
+extern "C" int anvil_gemm_i8_add_norm(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, int8_t* C, int M, int N, int K,
+                                      const int64_t* strides, int32_t mult, int shift, const int8_t* lut,
+                                      const int8_t* R, int32_t ma, int32_t mb, int shift2, int8_t* D,
+                                      const int64_t* rstrides, const anvil_norm_epilogue* norm, int flags) {
+  if (!norm || !norm->w || !norm->lut || !norm->out)
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_add_norm: null rmsnorm weights, table or result");
+  if (!(flags & ANVIL_GEMM_UNCHECKED) || !(flags & ANVIL_GEMM_NORM_S24) || (flags & (ANVIL_GEMM_SPLITK | ANVIL_GEMM_CAUSAL_SKIP | ANVIL_GEMM_CAUSAL_K)))
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_add_norm: flags must hold ANVIL_GEMM_UNCHECKED and "
+                                    "ANVIL_GEMM_NORM_S24, without a causal mode or split-K");
+  if ((N != 128 && N != 256) || M % 128 != 0)
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_add_norm: needs N of 128 or 256 (one tile a row band) and M a "
+                                    "multiple of 128 (M %d, N %d)", M, N);
+  if (!PackedAdd::applies(ma, mb))
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_add_norm: add multipliers must be below 2^24 in magnitude");
+  if (norm->lut_len < 1 || norm->shift < 0 || norm->shift > 31)
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_add_norm: rsqrt table of %d entries, shift %d", norm->lut_len,
+                     norm->shift);
+  const bool kb = norm->kb != 0;
+  if (!aligned16(norm->out) || !aligned16(norm->w) || (kb ? norm->ld != 64 || norm->kb % 16 || (long long)M * 64 > norm->kb
+                                                          : norm->ld < N || norm->ld % 16))
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_add_norm: the result H and the weights must be 16-byte aligned, "
+                                    "H row-major with a row stride >= N and a multiple of 16, or K-blocked");
+  const AddEpilogue add{R, D, rstrides, ma, mb, shift2};
+  Prepared p;
+  if (int r = gemm_prepare(ctx, A, Bt, C, 1, 1, M, N, K, strides, mult, shift, lut, ANVIL_I8, flags & ~ANVIL_GEMM_NORM_S24,
+                           &add, p))
+    return r;
+  if (!p.fast || p.osz != 1 || !p.g.vec_res || (C && !p.g.vec_store) || 128ll * p.g.ldr >= (1ll << 31))
+    return set_error(ANVIL_E_VALUE, "anvil_gemm_i8_add_norm: needs the fast path with 16-byte aligned operands, "
+                                    "results and row strides");
+  p.g.nw = norm->w;
+  p.g.nlut = norm->lut;
+  p.g.nlut_len = norm->lut_len;
+  p.g.nbits = 32 - __builtin_clz((unsigned)norm->lut_len);
+  p.g.nmult = norm->mult;
+  p.g.nshift = norm->shift;
+  p.g.H = norm->out;
+  p.g.ldh = kb ? 64 : norm->ld;
+  p.g.kbh = kb ? norm->kb : 0;
+  if (N == 128) launch_fast_norm<128, 128>(p.g, p.mul24, ctx->stream);
+  else launch_fast_norm<64, 256>(p.g, p.mul24, ctx->stream);     // twice the workgroups of 128 x 256 tiles
+  ANVIL_LAUNCHED();
+  return ANVIL_OK;
 }
 
 extern "C" int anvil_gemm_i8(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1,

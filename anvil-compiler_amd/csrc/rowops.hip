@@ -61,24 +61,6 @@ __device__ __forceinline__ int mul_sbyte(unsigned x, int w) {
   return d;
 }
 
-// signed byte B of x times signed byte B of w, both selected and sign-extended by the SDWA operands
-template <int B>
-__device__ __forceinline__ int mul_sbytes(unsigned x, unsigned w) {
-  int d;
-  if constexpr (B == 0)
-    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:BYTE_0"
-        : "=v"(d) : "v"(x), "v"(w));
-  else if constexpr (B == 1)
-    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:BYTE_1"
-        : "=v"(d) : "v"(x), "v"(w));
-  else if constexpr (B == 2)
-    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:BYTE_2"
-        : "=v"(d) : "v"(x), "v"(w));
-  else
-    asm("v_mul_i32_i24_sdwa %0, sext(%1), sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:BYTE_3"
-        : "=v"(d) : "v"(x), "v"(w));
-  return d;
-}
 
 __device__ __forceinline__ int mad_i24(int a, int b, int c) {
   int d;
@@ -286,43 +268,9 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
 // store instruction covers 256 contiguous bytes of every row. The row sums are reduced within each 16-lane DPP row,
 // read out as four scalars, and the per-row values (requant multiplier, shift, clamp bounds) return to the lanes by
 // selection on the lane's row.
-__device__ __forceinline__ int dpp_sum16(int v) {            // sum over the lane's 16-lane row, in every lane
-  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
-  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
-  v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false);  // row_ror:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
-  return v;
-}
 
-template <int L>
-__device__ __forceinline__ int lane_group_sum(int v) {                   // sum over aligned groups of L lanes
-  if constexpr (L > 1) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);    // quad_perm [1,0,3,2]
-  if constexpr (L > 2) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);    // quad_perm [2,3,0,1]
-  if constexpr (L > 4) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);   // row_half_mirror
-  if constexpr (L > 8) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);   // row_mirror
-  if constexpr (L > 16) v += __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 0x1F);           // lane ^ 16
-  if constexpr (L > 32) v += __shfl_xor(v, 32);
-  return v;
-}
 
-__device__ __forceinline__ unsigned sra_pack4v(int x0, int x1, int x2, int x3, int sh) {   // shift per lane
-  unsigned d;
-  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
-      : "=v"(d) : "v"(sh), "v"(x0));
-  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-      : "+v"(d) : "v"(sh), "v"(x1));
-  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-      : "+v"(d) : "v"(sh), "v"(x2));
-  asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-      : "+v"(d) : "v"(sh), "v"(x3));
-  return d;
-}
 
-__device__ __forceinline__ int mad_i24v(int a, int b, int c) {
-  int d;
-  asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
-}
 
 // L = 16 lanes a row as described; L = 8 takes rows of 128 CH bytes, eight rows a wave, in the same way (each load or
 // store then covers 128 contiguous bytes of every row).

@@ -133,7 +133,8 @@ enum anvil_gemm_flags {
   ANVIL_GEMM_SPLITK = 16,
   ANVIL_GEMM_A_KBLOCK = 32,
   ANVIL_GEMM_B_KBLOCK = 64,
-  ANVIL_GEMM_C_KBLOCK = 128
+  ANVIL_GEMM_C_KBLOCK = 128,
+  ANVIL_GEMM_NORM_S24 = 256     /* anvil_gemm_i8_add_norm only: |rsqrt table entry x norm mult| < 2^23 */
 };
 int anvil_gemm_i8_ex(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, void* C, int batch0, int batch1, int M,
                      int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut, int out_dtype,
@@ -173,6 +174,20 @@ typedef struct anvil_gemm_desc {
  * each. No member may write memory that another member reads or writes. */
 int anvil_gemm_i8_group(anvil_ctx* ctx, const anvil_gemm_desc* descs, int count);
 
+/* The rmsnorm that follows a fused add (below), fused too (anvil_gemm_i8_add_norm): H = rmsnorm_int(D, w, lut, mult,
+ * shift) over D's rows (reference anvil/semantics.py:164-182 with ss_shift = ss_init = 0). H is M x N int8, row-major
+ * with row stride ld (kb = 0), or K-blocked (ld = 64, kb the 64-column block stride, kb >= 64 M). */
+typedef struct anvil_norm_epilogue {
+  const int8_t* w;        /* N weights */
+  const int32_t* lut;     /* lut_len entries, >= 0 */
+  int lut_len;
+  int32_t mult;
+  int shift;
+  int8_t* out;
+  int64_t ld;
+  int64_t kb;
+} anvil_norm_epilogue;
+
 /* A qlinear / qmatmul whose int8 result y feeds an add_requant with an int8 residual R, fused in the GEMM's
  * epilogue (reference anvil/semantics.py:95-103, then add_requant :106-115):
  *   y = clamp_i8((acc * mult + 2^(shift-1)) >> shift) [-> lut];  D = clamp_i8((R * ma + y * mb + 2^(shift2-1)) >> shift2)
@@ -183,6 +198,18 @@ int anvil_gemm_i8_add(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, int8_t*
                       int N, int K, const int64_t* strides, int32_t mult, int shift, const int8_t* lut,
                       const int8_t* R, int32_t ma, int32_t mb, int shift2, int8_t* D, const int64_t* rstrides,
                       int flags);
+
+/* anvil_gemm_i8_add (batch 1) whose sum D also feeds an rmsnorm_int (the block's h2 = rmsnorm(r1); reference
+ * anvil/semantics.py:95-103, then add_requant :106-115, then rmsnorm_int :164-182), fused in the same epilogue: D and
+ * H = rmsnorm_int(D) are written, y too unless C is NULL. Each workgroup's 128 x N tile spans whole rows, so N must be
+ * 128 or 256 and M a multiple of 128. flags: ANVIL_GEMM_UNCHECKED (every intermediate of the three ops proven in
+ * int32) and ANVIL_GEMM_NORM_S24 (|lut[i] x norm->mult| < 2^23 for every entry), ANVIL_GEMM_MUL24 and the K-block
+ * flags allowed, no causal mode or split-K; |ma|, |mb| < 2^24; operands, results and their row strides 16-byte
+ * aligned. One launch in place of the product's and the rmsnorm's. */
+int anvil_gemm_i8_add_norm(anvil_ctx* ctx, const int8_t* A, const int8_t* Bt, int8_t* C, int M, int N, int K,
+                           const int64_t* strides, int32_t mult, int shift, const int8_t* lut, const int8_t* R,
+                           int32_t ma, int32_t mb, int shift2, int8_t* D, const int64_t* rstrides,
+                           const anvil_norm_epilogue* norm, int flags);
 
 /* anvil_gemm_i8_add with the result dtype as an argument (ADR-004's wide residual stream, reference
  * docs/decisions/ADR-004-small-inputs.md:59-82 and anvil/semantics.py:106-115): y, R and D are all out_dtype, ANVIL_I8

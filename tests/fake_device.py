@@ -237,6 +237,23 @@ class FakeDevice:
                 self._store_result(Cp, dt, b0, b1, M, N, (sc0, sc1, ldc), flags & rt.GEMM_C_KBLOCK, out[0])
             self.store(D, dt, (b0, b1, M, N), (sd0, sd1, ldd, 1), out[1])
 
+    def gemm_i8_add_norm(self, A, Bt, Cp, M, N, K, strides, mult, shift, lut, R, ma, mb, shift2, D, rstrides, nw, nlut,
+                         nlut_len, nmult, nshift, H, ld, kb, flags):
+        """gemm_i8_add (batch 1, int8), then H = rmsnorm_int(D): the preconditions of the fused entry point, then the
+        three ops."""
+        self.calls.append(("gemm_add_norm", M, N, K, tuple(strides), flags, Cp is not None, ld, kb))
+        assert N in (128, 256) and M % 128 == 0 and flags & rt.GEMM_NORM_S24 and flags & rt.GEMM_UNCHECKED
+        assert max(abs(ma), abs(mb)) < 1 << 24 and (ld == 64 if kb else ld >= N)
+        self.gemm_i8_add(A, Bt, Cp, 1, 1, M, N, K, strides, mult, shift, lut, R, ma, mb, shift2, D, rstrides,
+                         flags & ~rt.GEMM_NORM_S24)
+        d = self.view(D, "i8", (M, N), (rstrides[5], 1)).astype(np.int64)
+        w = self.view(nw, "i8", (N,), (1,)).astype(np.int64)
+        lt = self.view(nlut, "i32", (nlut_len,), (1,)).astype(np.int64)
+        assert int(np.abs(lt).max()) * abs(nmult) < 1 << 23
+        h = self._guard(lambda: sem.rmsnorm_int(d, w, lt, nmult, nshift))
+        if h is not None:
+            self._store_result(H, "i8", 1, 1, M, N, (0, 0, kb if kb else ld), bool(kb), h.reshape(1, 1, M, N))
+
     def _vt(self, Vt, b0, b1, T, D, st, flags):
         """The attention's V^T operand: given as V^T rows, or (ATTN_V_ROWS, T = 16 only) as V's own rows."""
         if flags & rt.ATTN_V_ROWS:

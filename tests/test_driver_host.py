@@ -532,3 +532,29 @@ def test_gemm_operand_ranges_stay_inside_their_allocations(monkeypatch, n, keep)
     else:
         res = cm.run(x, "mi355x", batch=True, keep=keep)
     assert res.ints and any(c[0] in ("gemm", "gemm_add", "gemm_group") for c in dev.calls)
+
+
+@pytest.mark.parametrize("keep", ["outputs", "all"])
+def test_rmsnorm_after_a_fused_add_joins_its_epilogue(fake, cfg4, keep):
+    """At C = 128 (config 4) each block's h2 = rmsnorm(r1), the second layer's h1 and the final norm hf run in the
+    epilogue of the GEMM whose residual add makes their input (anvil_gemm_i8_add_norm): four such launches and one
+    stand-alone rmsnorm (the first h1, whose input comes from outside). Every value against the oracle. At C = 256
+    (config 3) the planner leaves the rmsnorm on its own."""
+    cm = anvil_mi355x.compile(cfg4)
+    x = models.eval_inputs(cfg4.spec, 2, 11)
+    xf = models.to_float_input(cfg4.spec, cfg4.params, x)
+    xq = cm.quantize_input(xf)
+    fake.calls.clear()
+    res = cm.run(xq, quantized=True, batch=True, keep=keep)
+    kinds = [c[0] for c in fake.calls]
+    assert kinds.count("gemm_add_norm") == 4 and kinds.count("rmsnorm") == 1, kinds
+    assert all(c[1] % 128 == 0 and c[2] == 128 for c in fake.calls if c[0] == "gemm_add_norm")
+    want = interp.run(cfg4.module, {"x": xq}, cfg4.consts, batch=True)
+    names = want.values.keys() if keep == "all" else res.ints.keys()
+    for k in names:
+        if k in cfg4.consts:
+            continue
+        assert np.array_equal(res.ints[k], want.values[k]), k
+    cm3 = anvil_mi355x.compile(models.config(3)[0])
+    cm3._ensure_device()
+    assert not any(lab.endswith("+h2") for lab, _, _ in cm3._plan(2, "outputs").steps)

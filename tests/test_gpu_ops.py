@@ -4,6 +4,8 @@ Config 2 (the standalone int8 linear + requant sweep: M in {256, 4096, 16384}, K
 int8 in [-127, 127]) runs at its full sizes; the edge cases cover odd shapes (the byte-load path), i16 results,
 LUT epilogues, negative multipliers, head-batched strided operands and the device-side int32 contract flags.
 """
+import re
+
 import numpy as np
 import pytest
 
@@ -594,6 +596,78 @@ def test_gemm_with_fused_i16_residual_add(dev, M, K, N, store_y):
     assert np.array_equal(got, want), np.argwhere(got != want)[:5]
     if store_y:
         assert np.array_equal(c.download((M, N), np.int16)[rows].astype(np.int64), y)
+
+
+def _add_norm_case(M, N, K, seed, wide_shift=False):
+    """Operands of a fused qlinear + add_requant + rmsnorm_int and the oracle's three results (y, D, H)."""
+    rng = np.random.default_rng([33, M, N, K, seed])
+    a, w = rng.integers(-128, 128, (M, K)), rng.integers(-128, 128, (K, N))
+    r = rng.integers(-128, 128, (M, N))
+    acc = sem.matmul_i8(a[:256], w, fast=True)
+    (m,), s = Q.choose_shift([127 / (1.5 * max(1, int(np.abs(acc).max())))], [128 * int(np.abs(w).sum(axis=0).max())])
+    ma, mb, s2 = [(7873258, 3110671, 23), (-12000000, 4000000, 24), (300, -200, 9)][seed % 3]
+    nw = rng.integers(-127, 128, N)
+    if wide_shift:       # shifts s + k from 20 up past 24 (the clamp bounds at the int32 limits)
+        nlut, ns = rng.integers(1, 1 << 14, 1024), 20
+    else:
+        nlut, ns = Q.rsqrt_table(0.03, 0.01, 0.02, int(np.abs(nw).max()), N, 1e-5)
+    y = sem.qmatmul(a, w, m, s, None, fast=True)
+    d = sem.add_requant(r, y, ma, mb, s2)
+    h = sem.rmsnorm_int(d, nw, nlut, 1, ns)
+    return a, w, r, m, s, ma, mb, s2, nw, nlut, ns, y, d, h
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (1024, 128, 128), (16384, 128, 512), (256, 256, 256),
+                                   (16384, 256, 256), (384, 256, 1024)])
+@pytest.mark.parametrize("store_y,kb", [(True, False), (False, True), (False, False)])
+def test_gemm_add_norm(dev, M, N, K, store_y, kb):
+    """anvil_gemm_i8_add_norm: y = qlinear(a, w), D = add_requant(r, y) and H = rmsnorm_int(D) in one launch, each
+    128 x N tile spanning its rows (the blocks' C = 128 and 256): D, H (row-major or K-blocked) and y bit-exact
+    against the three ops, with add multipliers of both signs and at 2^23."""
+    a, w, r, m, s, ma, mb, s2, nw, nlut, ns, y, d, h = _add_norm_case(M, N, K, M + K + int(store_y) + 2 * int(kb))
+    C_ = dev.alloc(M * N) if store_y else None
+    D_, H_ = dev.alloc(M * N), dev.alloc(M * N)
+    flags = rt.GEMM_UNCHECKED | rt.GEMM_NORM_S24 | (rt.GEMM_MUL24 if K * 128 * 128 < (1 << 23) and m < (1 << 23) else 0)
+    dev.gemm_i8_add_norm(up(dev, a, "i8"), up(dev, np.ascontiguousarray(w.T), "i8"), C_, M, N, K,
+                         [0, 0, K, 0, 0, K, 0, 0, N], m, s, None, up(dev, r, "i8"), ma, mb, s2, D_, [0, 0, N, 0, 0, N],
+                         up(dev, nw, "i8"), up(dev, nlut, "i32"), len(nlut), 1, ns, H_, 64 if kb else N,
+                         M * 64 if kb else 0, flags)
+    dev.sync()
+    assert np.array_equal(D_.download((M, N), np.int8).astype(np.int64), d)
+    got_h = H_.download((M * N,), np.int8).astype(np.int64)
+    got_h = got_h.reshape(N // 64, M, 64).transpose(1, 0, 2).reshape(M, N) if kb else got_h.reshape(M, N)
+    assert np.array_equal(got_h, h), np.argwhere(got_h != h)[:5]
+    if store_y:
+        assert np.array_equal(C_.download((M, N), np.int8).astype(np.int64), y)
+
+
+@pytest.mark.parametrize("N", [128, 256])
+def test_gemm_add_norm_shifts_reaching_int32_bounds(dev, N):
+    """The fused rmsnorm with a 1024-entry table and s = 20: rows with large sums take k up to 7, so s + k passes
+    24, where the pre-shift clamp bounds saturate to the int32 limits (as in the stand-alone kernel's test)."""
+    M, K = 1024, 256
+    a, w, r, m, s, ma, mb, s2, nw, nlut, ns, y, d, h = _add_norm_case(M, N, K, 5, wide_shift=True)
+    D_, H_ = dev.alloc(M * N), dev.alloc(M * N)
+    dev.gemm_i8_add_norm(up(dev, a, "i8"), up(dev, np.ascontiguousarray(w.T), "i8"), None, M, N, K,
+                         [0, 0, K, 0, 0, K, 0, 0, N], m, s, None, up(dev, r, "i8"), ma, mb, s2, D_, [0, 0, N, 0, 0, N],
+                         up(dev, nw, "i8"), up(dev, nlut, "i32"), len(nlut), 1, ns, H_, N, 0,
+                         rt.GEMM_UNCHECKED | rt.GEMM_NORM_S24)
+    dev.sync()
+    assert np.array_equal(H_.download((M, N), np.int8).astype(np.int64), h)
+    assert np.abs(h).max() > 0
+
+
+@pytest.mark.parametrize("M,N,ma,flags,what", [(200, 128, 300, None, "multiple of 128"), (128, 192, 300, None, "128 or 256"),
+                                               (128, 128, 1 << 24, None, "below 2^24"),
+                                               (128, 128, 300, rt.GEMM_UNCHECKED, "NORM_S24")])
+def test_gemm_add_norm_rejects(dev, M, N, ma, flags, what):
+    """The fused entry point's preconditions, each refused with a ValueError before any launch."""
+    K = 64
+    flags = rt.GEMM_UNCHECKED | rt.GEMM_NORM_S24 if flags is None else flags
+    buf = dev.alloc(max(M, 256) * max(N, 256) * 4)
+    with pytest.raises(ValueError, match=re.escape(what)):
+        dev.gemm_i8_add_norm(buf, buf, None, M, N, K, [0, 0, K, 0, 0, K, 0, 0, N], 1, 8, None, buf, ma, 1, 8, buf,
+                             [0, 0, N, 0, 0, N], buf, buf, 1024, 1, 8, buf, N, 0, flags)
 
 
 @pytest.mark.parametrize("M,N,K,dtype,lut,add", [(32768, 3072, 768, "i8", True, False),

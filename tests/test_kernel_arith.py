@@ -8,7 +8,8 @@ double addition, and the result is compared with integer floor division on the c
 is most fragile: exact multiples n = k S and their neighbours, the largest divisors, and random draws.
 
 The GEMM epilogues' fused add on byte multiplies (PackedAdd) and their widened LUT index are checked at the end of
-the file, on every int8 operand pair and on int32 values at both ends of the range.
+the file, on every int8 operand pair and on int32 values at both ends of the range, and so is the closed form of the
+rsqrt table index that the fused rmsnorm epilogue uses in place of the reference's shift loop.
 """
 import struct
 from fractions import Fraction
@@ -158,3 +159,27 @@ def test_wide_lut_index_is_the_shift_plus_an_offset(s):
     table = lut[np.clip(np.arange(1 << (32 - s)) - (1 << (31 - s)), -128, 127) + 128] if s >= 12 else None
     if table is not None:
         assert np.array_equal(table[u], lut[np.clip(x >> s, -128, 127) + 128])
+
+
+def rsqrt_index_closed(ss, n):
+    """The fused rmsnorm epilogue's (idx, k) (csrc/gemm.hip norm_chunk): with b and c the bit lengths of ss and n,
+    k = k0 or k0 + 1, k0 = max(0, floor((b - c + 1) / 2)), whichever first brings ss >> 2k below n."""
+    b = int(ss).bit_length()
+    c = int(n).bit_length()
+    k0 = max(0, (b - c + 1) >> 1)
+    k = k0 + (1 if (ss >> (2 * k0)) >= n else 0)
+    return ss >> (2 * k), k
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 255, 256, 257, 1000, 1023, 1024, 1025, 4096, 12345])
+def test_rsqrt_index_closed_form(n):
+    """The closed form equals the reference loop (shift right by 2 until below n) for sums of squares across the
+    int32 range: every value up to 2^16, powers of two and their neighbours, and random draws."""
+    from oracle import semantics as sem
+    rng = np.random.default_rng(n)
+    ss = np.unique(np.concatenate([np.arange(1 << 16), [(1 << p) + d for p in range(31) for d in (-1, 0, 1)],
+                                   rng.integers(0, (1 << 31) - 1, 20000)]))
+    ss = ss[(ss >= 0) & (ss < 1 << 31)]
+    idx, k = sem.rsqrt_index(ss, n)
+    got = np.array([rsqrt_index_closed(int(v), n) for v in ss])
+    assert np.array_equal(got[:, 0], idx) and np.array_equal(got[:, 1], k)
