@@ -277,4 +277,15 @@ __device__ __forceinline__ int mad_i24v(int a, int b, int c) {
   return d;
 }
 
+
+// The shift count of the reference's rsqrt_index (shift the sum of squares right by 2 until it is below the table's
+// length n, counting the steps): the fewest k >= 0 with ss >> 2k below n, for 0 <= ss < 2^31, nbits the bit length of
+// n. With b the bit length of ss, n 4^k <= ss for k <= (b - 1 - nbits) / 2 and n 4^k > ss for k >= (b - nbits + 1) / 2,
+// so k is k0 = max(0, floor((b - nbits + 1) / 2)) or k0 + 1: two compares in place of a loop of up to 15 steps.
+__device__ __forceinline__ int rsqrt_shift(int ss, int n, int nbits) {
+  const int b = ss == 0 ? 0 : 32 - __builtin_clz((unsigned)ss);
+  const int k0 = max(0, (b - nbits + 1) >> 1);
+  return k0 + ((ss >> (2 * k0)) >= n ? 1 : 0);
+}
+
 }  // namespace anvil

@@ -863,11 +863,7 @@ __device__ __forceinline__ void fast_tile(const GemmArgs& g, int pid, const int 
 #pragma unroll
           for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(d[q], d[q], ss, false);
           ss = lane_group_sum<CH_ROW>(ss);
-          // (idx, k) = rsqrt_index(ss, n), the fewest k with ss >> 2k below n: with b and c the bit lengths of ss
-          // and n, k is k0 = max(0, floor((b - c + 1) / 2)) or k0 + 1
-          const int b = ss == 0 ? 0 : 32 - __builtin_clz((unsigned)ss);
-          const int k0 = max(0, (b - g.nbits + 1) >> 1);
-          const int k = k0 + ((ss >> (2 * k0)) >= g.nlut_len ? 1 : 0);
+          const int k = rsqrt_shift(ss, g.nlut_len, g.nbits);       // (idx, k) = rsqrt_index(ss, n)
           const int rm = g.nlut[ss >> (2 * k)] * g.nmult;            // proven below 2^23 in magnitude
           const int sh = g.nshift + k;
           const int rnd = sh ? 1 << (sh - 1) : 0;

@@ -206,12 +206,8 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
 #pragma unroll
       for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[j][q], xv[j][q], ss, false);
       ss = __builtin_amdgcn_readfirstlane(wave_sum32(ss));     // every lane holds the same sum
-      int k = 0;
-      while (ss >= lut_len) {
-        ss >>= 2;
-        ++k;
-      }
-      idx[j] = ss;
+      const int k = rsqrt_shift(ss, lut_len, 32 - __builtin_clz((unsigned)lut_len));
+      idx[j] = ss >> (2 * k);
       sh[j] = shift + k;
     }
     int r[RMS_ROWS];
@@ -314,11 +310,8 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
     static_for<R>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       int t = __builtin_amdgcn_readlane(ss, L * j);
-      int k = 0;
-      while (t >= lut_len) {
-        t >>= 2;
-        ++k;
-      }
+      const int k = rsqrt_shift(t, lut_len, 32 - __builtin_clz((unsigned)lut_len));
+      t >>= 2 * k;
       const int shj = shift + k;
       const int rmj = lut[t] * mult;                            // proven below 2^23 in magnitude
       const bool mine = rr == j;
@@ -392,11 +385,8 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_narrow(const int8_t* __rest
 #pragma unroll
     for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[q], xv[q], ss, false);
     int t = lane_group_sum<L>(ss);
-    int k = 0;
-    while (t >= lut_len) {
-      t >>= 2;
-      ++k;
-    }
+    const int k = rsqrt_shift(t, lut_len, 32 - __builtin_clz((unsigned)lut_len));   // per lane: its row's sum
+    t >>= 2 * k;
     const int sh = shift + k;
     const int rm = narrow_lut[t] * mult;                        // proven below 2^23 in magnitude
     const int rnd = sh ? 1 << (sh - 1) : 0;
@@ -527,11 +517,8 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_wide_fast(const int16_t* __
         ss += (unsigned)(square_half<1>(xd) + rc) >> c;
       }
     int t = lane_group_sum<L>(ss) + e;
-    int kk = 0;
-    while (t >= lut_len) {
-      t >>= 2;
-      ++kk;
-    }
+    const int kk = rsqrt_shift(t, lut_len, 32 - __builtin_clz((unsigned)lut_len));  // per lane: its row's sum
+    t >>= 2 * kk;
     const int sh = shift + kk;                                   // proven at most 31
     const int rm = wide_lut[t] * mult;                           // wraps unless s24; the products stay exact
     const int rnd = sh ? 1 << (sh - 1) : 0;
