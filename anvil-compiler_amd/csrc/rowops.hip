@@ -8,6 +8,19 @@
 namespace anvil {
 
 constexpr int R_THREADS = 256, R_WAVES = R_THREADS / 64;
+constexpr int ROWS_LUT_MAX = 4 * R_THREADS;   // table words rmsnorm_rows16 stages in LDS: four reads a thread
+
+// A row kernel's table into LDS (dst: lut_len words), four reads in flight a lane; the caller synchronises.
+__device__ __forceinline__ void stage_lut(int* dst, const int* __restrict__ lut, int lut_len) {
+  for (int i0 = threadIdx.x; i0 < lut_len; i0 += 4 * R_THREADS) {
+    int v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = i0 + j * R_THREADS < lut_len ? lut[i0 + j * R_THREADS] : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (i0 + j * R_THREADS < lut_len) dst[i0 + j * R_THREADS] = v[j];
+  }
+}
 
 __device__ __forceinline__ long long wave_sum(long long v) {
 #pragma unroll
@@ -262,12 +275,12 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_fast(const int8_t* __restri
 // rmsnorm_int over rows of 256·CH bytes (the S24 form of rmsnorm_fast, every lane busy): a wave holds four rows,
 // 16 lanes a row, and lane sub of row rr reads and writes chunks c·16 + sub (16 bytes each, c < CH), so each load or
 // store instruction covers 256 contiguous bytes of every row. The row sums are reduced within each 16-lane DPP row,
-// read out as four scalars, and the per-row values (requant multiplier, shift, clamp bounds) return to the lanes by
-// selection on the lane's row.
-
-
-
-
+// which leaves the row's sum in each of its lanes, and every lane forms its row's table index, requant multiplier,
+// shift and clamp bounds itself, reading the table from LDS (at most ROWS_LUT_MAX words, staged once per workgroup
+// while the first row group loads), so the reads do not wait behind the next group's row loads. (Formed on the
+// scalar unit, read out row by row and returned to the lanes by selection, the compiler turned each row's selection
+// into a branch holding that row's table load and its wait: four dependent round trips a row group.)
+//
 // L = 16 lanes a row as described; L = 8 takes rows of 128 CH bytes, eight rows a wave, in the same way (each load or
 // store then covers 128 contiguous bytes of every row).
 template <int CH, int L = 16>
@@ -277,13 +290,18 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
                                                              int kbo) {
   static_assert(L == 16 || L == 8, "16 or 8 lanes a row");
   constexpr int COLS = 16 * L * CH, R = 64 / L;               // bytes a row, rows a wave
+  __shared__ int rows_lut[ROWS_LUT_MAX];
   const int lane = threadIdx.x & 63, rr = lane / L, sub = lane % L;
   // kbo: the output K-blocked, as in rmsnorm_fast; chunk L c + sub of a row is in block (L / 4) c + sub / 4
   const __amdgpu_buffer_rsrc_t wall = uniform_rsrc(out, kbo ? (int)(rows * COLS) : 0);
   const unsigned kcol = (unsigned)((sub >> 2) * kbo + 16 * (sub & 3));
-  v4i wv[CH];                                                   // this lane's weights, packed (each multiply
-#pragma unroll                                                  // selects and sign-extends its byte)
-  for (int c = 0; c < CH; ++c) wv[c] = *reinterpret_cast<const v4i*>(w + 16 * (L * c + sub));
+  // this lane's weights, packed (each multiply selects and sign-extends its byte), through a buffer load: a plain
+  // load of the read-only weights is free to sink past the table's barrier below, and then waits with the rows
+  const __amdgpu_buffer_rsrc_t wr = uniform_rsrc(w, COLS);
+  v4i wv[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+    wv[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (unsigned)(16 * (L * c + sub)), 0, 0));
   unsigned off[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) off[c] = (unsigned)(rr * COLS + 16 * (L * c + sub));
@@ -303,24 +321,12 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
     for (int c = 0; c < CH; ++c)
 #pragma unroll
       for (int q = 0; q < 4; ++q) ss = __builtin_amdgcn_sdot4(xv[c][q], xv[c][q], ss, false);
-    ss = L == 16 ? dpp_sum16(ss) : lane_group_sum<L>(ss);
-    // each row's values on the scalar unit, then the lane's row's selected (no array: an array of the rows' values
-    // indexed by the lane's row is what the compiler would otherwise make of the selects, through scratch)
-    int rm = 0, sh = 0, rnd = 0, lo = 0, hi = 0;
-    static_for<R>([&](auto jc) {
-      constexpr int j = decltype(jc)::value;
-      int t = __builtin_amdgcn_readlane(ss, L * j);
-      const int k = rsqrt_shift(t, lut_len, 32 - __builtin_clz((unsigned)lut_len));
-      t >>= 2 * k;
-      const int shj = shift + k;
-      const int rmj = lut[t] * mult;                            // proven below 2^23 in magnitude
-      const bool mine = rr == j;
-      rm = mine ? rmj : rm;
-      sh = mine ? shj : sh;
-      rnd = mine ? (shj ? 1 << (shj - 1) : 0) : rnd;
-      lo = mine ? (shj >= 24 ? INT32_MIN : -128 * (1 << shj)) : lo;
-      hi = mine ? (shj >= 24 ? INT32_MAX : 128 * (1 << shj) - 1) : hi;
-    });
+    ss = L == 16 ? dpp_sum16(ss) : lane_group_sum<L>(ss);   // the row's sum, in each of its lanes
+    const int k = rsqrt_shift(ss, lut_len, 32 - __builtin_clz((unsigned)lut_len));
+    const int sh = shift + k;
+    const int rm = rows_lut[ss >> (2 * k)] * mult;              // index below lut_len; proven below 2^23 in magnitude
+    const int rnd = sh ? 1 << (sh - 1) : 0;
+    const int lo = sh >= 24 ? INT32_MIN : -128 * (1 << sh), hi = sh >= 24 ? INT32_MAX : 128 * (1 << sh) - 1;
     const __amdgpu_buffer_rsrc_t ws = group(out, r0);
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -342,7 +348,17 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_rows16(const int8_t* __rest
   };
   long long row0 = ((long long)blockIdx.x * R_WAVES + (threadIdx.x >> 6)) * R;
   v4i xa[CH], xb[CH];
+  // the table's reads (words past lut_len read as zeros and are never indexed), then the first row group's, which
+  // stay in flight while the table is stored
+  const __amdgpu_buffer_rsrc_t lr = uniform_rsrc(lut, lut_len * 4);
+  int tv[ROWS_LUT_MAX / R_THREADS];
+#pragma unroll
+  for (int j = 0; j < ROWS_LUT_MAX / R_THREADS; ++j)
+    tv[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(lr, (unsigned)(j * R_THREADS + threadIdx.x) * 4, 0, 0);
   load(row0, xa);
+#pragma unroll
+  for (int j = 0; j < ROWS_LUT_MAX / R_THREADS; ++j) rows_lut[j * R_THREADS + threadIdx.x] = tv[j];
+  __syncthreads();
   while (row0 < rows) {
     load(row0 + step, xb);
     process(xa, row0);
@@ -365,7 +381,7 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_narrow(const int8_t* __rest
                                                              int kbo) {
   constexpr int COLS = 16 * L, R = 64 / L;
   extern __shared__ int narrow_lut[];
-  for (int i0 = threadIdx.x; i0 < lut_len; i0 += R_THREADS) narrow_lut[i0] = lut[i0];
+  stage_lut(narrow_lut, lut, lut_len);
   __syncthreads();
   const int lane = threadIdx.x & 63, rr = lane / L, sub = lane % L;
   const __amdgpu_buffer_rsrc_t wall = uniform_rsrc(out, kbo ? (int)(rows * COLS) : 0);
@@ -425,9 +441,9 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_narrow(const int8_t* __rest
 // and rows past the last get buffer offsets beyond the descriptor (loads 0, stores nothing), as in rmsnorm_fast.
 // The row sum is reduced over the L lanes (DPP within 16 lanes, swizzles across), so every lane of a row holds it
 // and forms that row's table index, multiplier, shift and clamp bounds itself; the table sits in LDS (lut_len words
-// of dynamic LDS, staged once per workgroup), so its per-lane reads do not wait behind the next group's row loads. Each entry's square is one 24-bit
-// multiply of its sign-extended half (SDWA); x w is one 24-bit multiply of that half by the sign-extended weight
-// byte, |x w| <= 2^22. With s24 (every |lut[i] M| < 2^23) x w (lut[i] M) + rnd is one 24-bit multiply-add; without
+// of dynamic LDS, staged once per workgroup), so its per-lane reads do not wait behind the next group's row loads.
+// Each entry's square is one 24-bit multiply of its sign-extended half (SDWA); x w is one 24-bit multiply of that
+// half by the sign-extended weight byte, |x w| <= 2^22. With s24 (every |lut[i] M| < 2^23) x w (lut[i] M) + rnd is one 24-bit multiply-add; without
 // it the product wraps in 32 bits, which is exact because x w lut[i] M + rnd is proven to fit int32.
 template <int H, int B>
 __device__ __forceinline__ int mul_half_byte(unsigned x, unsigned w) {   // sext(half H of x) * sext(byte B of w)
@@ -471,14 +487,7 @@ __global__ __launch_bounds__(R_THREADS) void rmsnorm_wide_fast(const int16_t* __
   static_assert(CH == 1 || L == 64, "several chunks a lane only with a whole wave a row");
   constexpr int RW = 64 / L;                                     // rows a wave holds at once
   extern __shared__ int wide_lut[];
-  for (int i0 = threadIdx.x; i0 < lut_len; i0 += 4 * R_THREADS) {   // four table reads in flight a lane
-    int v[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = i0 + j * R_THREADS < lut_len ? lut[i0 + j * R_THREADS] : 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (i0 + j * R_THREADS < lut_len) wide_lut[i0 + j * R_THREADS] = v[j];
-  }
+  stage_lut(wide_lut, lut, lut_len);
   __syncthreads();
   const int lane = threadIdx.x & 63, rr = lane / L, sub = lane % L;
   const int n = cols >> 3;                                       // 16-byte chunks of x a row
@@ -709,10 +718,10 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
     const long long groups = (rows + RMS_ROWS - 1) / RMS_ROWS;
     const dim3 grid((unsigned)std::min<long long>((groups + R_WAVES - 1) / R_WAVES, 8ll * ctx->num_cu));
     const int ch = cols / 256;
-    if ((flags & ANVIL_RMS_S24) && cols % 256 == 0 && ch <= 4) {      // rows of 256, 512, 768 or 1024 bytes
+    if ((flags & ANVIL_RMS_S24) && cols % 256 == 0 && ch <= 4 && lut_len <= ROWS_LUT_MAX) {   // rows of 256 to 1024
       auto launch = [&](auto kernel) {
-        ANVIL_LAUNCH(kernel, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len, mult,
-                           shift, (long long)rows, out, kbo);
+        ANVIL_LAUNCH(kernel, grid, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len, mult, shift,
+                     (long long)rows, out, kbo);
       };
       if (ch == 1) launch(rmsnorm_rows16<1>);
       else if (ch == 2) launch(rmsnorm_rows16<2>);
@@ -729,7 +738,7 @@ extern "C" int anvil_rmsnorm_int_ex(anvil_ctx* ctx, const void* x, int x_dtype, 
       if (L == 1) launch(rmsnorm_narrow<1>);
       else if (L == 2) launch(rmsnorm_narrow<2>);
       else launch(rmsnorm_narrow<4>);
-    } else if ((flags & ANVIL_RMS_S24) && cols == 128) {             // 8 lanes a row, 8 rows a wave
+    } else if ((flags & ANVIL_RMS_S24) && cols == 128 && lut_len <= ROWS_LUT_MAX) {   // 8 lanes a row, 8 rows a wave
       const long long groups8 = (rows + 7) / 8;
       const dim3 grid8((unsigned)std::min<long long>((groups8 + R_WAVES - 1) / R_WAVES, 8ll * ctx->num_cu));
       ANVIL_LAUNCH((rmsnorm_rows16<1, 8>), grid8, dim3(R_THREADS), 0, ctx->stream, (const int8_t*)x, w, lut, lut_len,
