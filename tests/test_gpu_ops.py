@@ -160,6 +160,23 @@ def test_rmsnorm_shift_reaching_int32_bounds(dev, d):
     assert np.abs(want).max() > 0
 
 
+@pytest.mark.parametrize("n", [5, 1000, 1024, 1025, 3000])
+@pytest.mark.parametrize("d", [128, 256, 768])
+def test_rmsnorm_i8_table_lengths(dev, d, n):
+    """rsqrt tables of n entries: up to 1024 the 16- and 8-lane kernels stage the table in LDS (words past n read as
+    zeros and are never indexed), longer ones take the four-rows-a-wave kernel. Short tables drive k, and with it
+    the requant shift, up to 27."""
+    rng = np.random.default_rng([64, d, n])
+    w = rng.integers(-127, 128, d)
+    lut = rng.integers(1, 1 << 14, n)
+    x = np.concatenate([rng.integers(-128, 128, (90, d)), rng.integers(-2, 3, (40, d)), np.full((2, d), -128),
+                        np.zeros((1, d), int)])
+    want = sem.rmsnorm_int(x, w, lut, 1, 16)
+    got = _rms(dev, x, "i8", w, lut, 1, 16, flags=rt.OP_UNCHECKED | rt.RMS_S24)
+    assert np.array_equal(got, want)
+    assert np.abs(want).max() > 0
+
+
 def _wide_case(d, rows, seed):
     """A proven wide rmsnorm (table, s, c, e from the quantizer for |x| <= 2^15) and rows over the full int16 range:
     random rows, the extreme constant rows, a zero row and quiet rows (small sums: low table indexes, k = 0)."""
