@@ -326,13 +326,17 @@ static void launch_add_typed(anvil_ctx* ctx, const TA* a, const TB* b, int ma, i
 
 // embed_quantize four columns a lane: one wave a row (a workgroup takes four rows, then strides by the grid), its
 // lanes over the row's C / 4 float4 columns of the token's and the position's rows, so no lane divides by C; one
-// 4-byte (i8) or 8-byte (i16) store. Each element as in embed_quantize_kernel.
+// 4-byte (i8) or 8-byte (i16) store. Each element as in embed_quantize_kernel, with the division replaced where
+// that cannot change the result: q = fl(x fl(1 / scale)) is within 3 ulp of x / scale (inv a normal double), so
+// rint(q) is the rint of the correctly rounded quotient unless q lies within 2^-50 |q| of a half-integer (the only
+// points where rint changes value); such an element, and every element when inv is not normal, takes the quotient.
+// q - floor(q) is exact, so the test is too; an infinite or NaN q fails it and takes the quotient.
 template <typename TO>
 __global__ __launch_bounds__(E_THREADS) void embed_quantize_vec4(const int64_t* __restrict__ ids,
                                                                  const float* __restrict__ wte,
                                                                  const float* __restrict__ wpe, long long rows,
-                                                                 int T, int C, int vocab, double scale,
-                                                                 TO* __restrict__ out, int lo, int hi,
+                                                                 int T, int C, int vocab, double scale, double inv,
+                                                                 int use_inv, TO* __restrict__ out, int lo, int hi,
                                                                  unsigned* flags) {
   const int c4 = C >> 2, lane = threadIdx.x & 63;
   const long long step = (long long)gridDim.x * (E_THREADS / 64);
@@ -351,7 +355,9 @@ __global__ __launch_bounds__(E_THREADS) void embed_quantize_vec4(const int64_t* 
                               (double)w.w + (double)p.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          double v = rint(xs[e] / scale);
+          const double q = xs[e] * inv;
+          double v = rint(q);
+          if (!(use_inv && fabs(q - floor(q) - 0.5) > 0x1p-50 * fabs(q))) v = rint(xs[e] / scale);
           v = v < lo ? lo : (v > hi ? hi : v);
           o[e] = (int)v;
         }
@@ -569,12 +575,14 @@ int anvil_embed_quantize(anvil_ctx* ctx, const int64_t* ids, int64_t rows, int T
   const int lo = dtype_lo(out_dtype), hi = dtype_hi(out_dtype);
   if (C % 4 == 0 && al16(wte) && al16(wpe) && ((uintptr_t)out & (out_dtype == ANVIL_I8 ? 3 : 7)) == 0) {
     const dim3 gr((unsigned)std::min<long long>((rows + 3) / 4, 65536)), bl(E_THREADS);   // four rows a workgroup
+    const double inv = 1.0 / scale;
+    const int use_inv = std::isnormal(inv) ? 1 : 0;
     if (out_dtype == ANVIL_I8)
       ANVIL_LAUNCH(embed_quantize_vec4<int8_t>, gr, bl, 0, ctx->stream, ids, wte, wpe, (long long)rows, T, C, vocab,
-                   scale, (int8_t*)out, lo, hi, ctx->flags);
+                   scale, inv, use_inv, (int8_t*)out, lo, hi, ctx->flags);
     else
       ANVIL_LAUNCH(embed_quantize_vec4<int16_t>, gr, bl, 0, ctx->stream, ids, wte, wpe, (long long)rows, T, C, vocab,
-                   scale, (int16_t*)out, lo, hi, ctx->flags);
+                   scale, inv, use_inv, (int16_t*)out, lo, hi, ctx->flags);
     ANVIL_LAUNCHED();
     return ANVIL_OK;
   }

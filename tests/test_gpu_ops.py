@@ -878,6 +878,32 @@ def test_embed_quantize(dev, dtype, C):
     assert (want == lo).any() and (want == hi).any()           # saturation on both sides is exercised
 
 
+@pytest.mark.parametrize("k", [0, 3, 41, 126, -128])
+def test_embed_quantize_at_half_integers(dev, k):
+    """The four-columns-a-lane kernel rounds x / scale through a multiply by 1 / scale away from the half-integers
+    and takes the quotient near them: scales that put x0 / scale at or next to +-(k + 1/2) for some of the table's
+    sums x0 (each such element takes the quotient), and a power-of-two scale (an exact product), all against the
+    host's float64 quotient."""
+    rng = np.random.default_rng([52, k + 200])
+    vocab, T, C = 64, 8, 64
+    wte = rng.normal(0, 0.05, (vocab, C)).astype(np.float32)
+    wpe = np.zeros((T, C), np.float32)
+    wpe[1:] = rng.normal(0, 0.05, (T - 1, C)).astype(np.float32)
+    ids = rng.integers(0, vocab, (4, T))
+    x = wte.astype(np.float64)[ids] + wpe.astype(np.float64)[None, :T]
+    x0 = x[np.abs(x) > 1e-3].ravel()[:6]
+    scales = [float(v) / (k + 0.5) for v in x0]
+    scales += [np.nextafter(s, np.inf) for s in scales[:2]] + [2.0 ** -10]
+    for scale in scales:
+        scale = abs(scale)
+        want = np.clip(np.rint(x / scale), -128, 127).astype(np.int64)
+        out = dev.alloc(ids.size * C)
+        dev.embed_quantize(dev.upload(ids.astype(np.int64)), ids.size, T, C, dev.upload(wte), vocab, dev.upload(wpe),
+                           scale, out, "i8")
+        dev.sync()
+        assert np.array_equal(out.download((4, T, C), np.int8).astype(np.int64), want), scale
+
+
 def test_page_locked_download_round_trip(dev):
     """anvil_host_alloc memory as a download target: every byte of a device buffer arrives, a second download into
     the same host buffer replaces the first, and an oversized request is refused before the copy."""

@@ -9,7 +9,8 @@ is most fragile: exact multiples n = k S and their neighbours, the largest divis
 
 The GEMM epilogues' fused add on byte multiplies (PackedAdd) and their widened LUT index are checked at the end of
 the file, on every int8 operand pair and on int32 values at both ends of the range, and so is the closed form of the
-rsqrt table index that the fused rmsnorm epilogue uses in place of the reference's shift loop.
+rsqrt table index that the fused rmsnorm epilogue uses in place of the reference's shift loop. Last, the embedding
+quantization's rounding of x / scale through a multiply by 1 / scale, guarded near the half-integers.
 """
 import struct
 from fractions import Fraction
@@ -183,3 +184,60 @@ def test_rsqrt_index_closed_form(n):
     idx, k = sem.rsqrt_index(ss, n)
     got = np.array([rsqrt_index_closed(int(v), n) for v in ss])
     assert np.array_equal(got[:, 0], idx) and np.array_equal(got[:, 1], k)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# embed_quantize_vec4 (csrc/eltwise.hip): rint(x / scale) taken as rint(fl(x fl(1 / scale))) unless that product lies
+# within 2^-50 of its magnitude of a half-integer, or 1 / scale is not a normal double; then the quotient itself.
+# Every operation is an IEEE double operation, the same on the host as on the GPU.
+
+def embed_rint(x, s):
+    inv = 1.0 / s
+    use = np.isfinite(inv) and abs(inv) >= np.finfo(np.float64).tiny
+    with np.errstate(invalid="ignore", over="ignore"):
+        q = x * inv
+        v = np.rint(q)
+        exact = ~(use & (np.abs(q - np.floor(q) - 0.5) > 2.0 ** -50 * np.abs(q)))
+        v[exact] = np.rint(x[exact] / s)
+    return v, exact
+
+
+def near_ties(s, rng):
+    """Products of s with every half-integer in [-300.5, 300.5], each with its two neighbours either side, and
+    random multiples of s."""
+    base = (np.arange(-300, 301) + 0.5) * s
+    up, down = np.nextafter(base, np.inf), np.nextafter(base, -np.inf)
+    return np.concatenate([base, up, down, np.nextafter(up, np.inf), np.nextafter(down, -np.inf),
+                           rng.standard_normal(500) * s * 100])
+
+
+def test_embed_rint_equals_the_quotient_rint():
+    """On inputs crowded at the half-integers (where rint changes value) and at random, over scales from 1e-7 to 20,
+    the guarded product rounds as the correctly rounded quotient does; planted: without the guard it does not."""
+    rng = np.random.default_rng(5)
+    unguarded = 0
+    for _ in range(60):
+        s = float(10.0 ** rng.uniform(-7, 1)) * rng.uniform(1, 2)
+        x = near_ties(s, rng)
+        want = np.rint(x / s)
+        got, _ = embed_rint(x, s)
+        assert np.array_equal(got, want), s
+        unguarded += int((np.rint(x * (1.0 / s)) != want).sum())
+    assert unguarded > 0
+
+
+def test_embed_rint_takes_the_quotient_where_the_product_cannot_serve():
+    """A subnormal scale (1 / scale infinite), infinite and NaN inputs, and ties at a power-of-two scale (exact product,
+    ties to even on both paths)."""
+    x = np.array([0.0, 1e-300, -2.5e-300, np.inf, -np.inf, np.nan, 3.0])
+    got, exact = embed_rint(x, 5e-310)
+    assert exact.all()
+    with np.errstate(over="ignore"):
+        want = np.rint(x / 5e-310)
+    assert np.array_equal(got, want, equal_nan=True)
+    got, exact = embed_rint(np.array([np.inf, np.nan, 1.0]), 0.25)
+    assert exact[:2].all() and got[2] == 4.0
+    s = 2.0 ** -12
+    x = (np.arange(-20, 21) + 0.5) * s
+    got, _ = embed_rint(x, s)
+    assert np.array_equal(got, np.rint(x / s)) and np.array_equal(got % 2, np.zeros_like(got))
